@@ -1,0 +1,300 @@
+#!/usr/bin/env python3
+"""Benchmark of the Nova GPU matmul / reduction path on one MI355X.
+
+One step = one launch of the hot path over one batch of synthetic input,
+inputs already resident in HBM.  The headline (``value``) is config 2 of
+linalg.batch_matmul bf16 -> f32, B=8, M=N=K=4096, in TFLOP/s.
+The same line carries configs 3-5 (linear+bias+GELU, the unaligned fp16
+batch GEMMs, LayerNorm and softmax cross-entropy) as ``configs``, each with
+its roofline fraction, the ``roofline`` object of the dominant kernel, and a
+``cpu_baseline`` timed on this host with the CPU oracle.
+
+Timing: torch.cuda.Event pairs on torch's current stream, which is the
+stream libnova_hip launches on (nova_hip.py binds it before every call).
+Reduction inputs rotate over 3 buffer sets so the 256 MB MALL cannot serve
+repeated reads as if they were HBM traffic.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "nova-compiler_amd"))
+
+# MI355X published peaks (dense).
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU
+PEAK_HBM_GBS = 8000.0
+
+C2_FLOP = 2 * 8 * 4096 ** 3                  # 1,099,511,627,776
+C3_FLOP = 2 * 4096 * 4096 * 11008            # 369,367,187,456
+C4_FLOP = 2 * 96 * 197 * 197 * 64            # 476,884,992 (both shapes)
+C4A_BYTES = 19_744_128
+C4B_BYTES = 14_713_536
+LN_BYTES = 16384 * 4096 * 4 * 2 + 4096 * 4 * 2 + 16384 * 4 * 2   # 537,034,752
+SCE_BYTES = 4096 * 32000 * 4 + 4096 * 4 + 4                     # 524,304,388
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU oracle timing (cpu_baseline becomes null)")
+    ap.add_argument("--only", default="", help="comma list of configs to run (c2,c3,c4,ln,sce)")
+    return ap.parse_args()
+
+
+def to_dev(a, dt, torch):
+    import numpy as np
+    import nova_seed as S
+    if dt == S.F32:
+        return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t = torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+    return t.view(torch.bfloat16 if dt == S.BF16 else torch.float16)
+
+
+def time_launches(fn, steps, warmup, torch):
+    """Average ms per call over `steps` calls after `warmup` calls."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_c2(args, torch, nh, S):
+    inp = S.config_inputs("c2")
+    A = to_dev(inp["A"], S.BF16, torch)
+    B = to_dev(inp["B"], S.BF16, torch)
+    del inp
+    C = torch.empty(8, 4096, 4096, device="cuda", dtype=torch.float32)
+    dA, dB, dC = nh.memref_of(A), nh.memref_of(B), nh.memref_of(C)
+    L = nh.lib()
+    fn_ = L._mlir_ciface_nova_hip_batch_matmul_bf16_f32
+    pA, pB, pC = nh.ref(dA), nh.ref(dB), nh.ref(dC)
+
+    def fn(_):
+        rc = fn_(pA, pB, pC)
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, args.steps, args.warmup, torch)
+    finite = bool(torch.isfinite(C[:, ::512, ::512]).all())
+    del A, B, C
+    tf = C2_FLOP / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS, "finite": finite}
+
+
+def bench_c3(args, torch, nh, S):
+    inp = S.config_inputs("c3")
+    x = to_dev(inp["x"], S.BF16, torch)
+    W = to_dev(inp["W"], S.BF16, torch)
+    b = to_dev(inp["bias"], S.BF16, torch)
+    y = torch.empty(4096, 11008, device="cuda", dtype=torch.bfloat16)
+    d = [nh.memref_of(t) for t in (x, W.t(), b, y)]
+    p = [nh.ref(v) for v in d]
+    f_ = nh.lib()._mlir_ciface_nova_hip_linear_bf16_bias_gelu
+
+    def fn(_):
+        rc = f_(*p)
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, max(args.steps // 2, 5), max(args.warmup // 2, 2), torch)
+    tf = C3_FLOP / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS}
+
+
+def bench_c4(args, torch, nh, S, name, nbytes):
+    inp = S.config_inputs(name)
+    sets = []
+    for _ in range(3):
+        A = to_dev(inp["A"], S.F16, torch)
+        B = to_dev(inp["B"], S.F16, torch)
+        C = torch.empty(A.shape[0], A.shape[1], B.shape[2], device="cuda")
+        sets.append(tuple(nh.ref(nh.memref_of(t)) for t in (A, B, C)) + (A, B, C))
+    f_ = nh.lib()._mlir_ciface_nova_hip_batch_matmul_f16_f32
+
+    def fn(i):
+        s = sets[i % 3]
+        rc = f_(s[0], s[1], s[2])
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, args.steps * 4, args.warmup, torch)
+    tf = C4_FLOP / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    # binding roof: min(MFMA peak, AI x HBM)
+    roof = min(PEAK_BF16_TFLOPS, (C4_FLOP / nbytes) * PEAK_HBM_GBS / 1e3)
+    return {"ms": ms, "tflops": tf, "gbs": gbs, "roof_tflops": roof, "frac_roof": tf / roof}
+
+
+def bench_ln(args, torch, nh, S):
+    inp = S.config_inputs("c5_ln")
+    g = to_dev(inp["gamma"], S.F32, torch)
+    b = to_dev(inp["beta"], S.F32, torch)
+    sets = []
+    for _ in range(3):
+        x = to_dev(inp["x"], S.F32, torch)
+        y = torch.empty_like(x)
+        s = torch.empty(16384, device="cuda")
+        r = torch.empty(16384, device="cuda")
+        sets.append(([nh.ref(nh.memref_of(t)) for t in (x, g, b, y, s, r)], (x, y, s, r)))
+    del inp
+    import ctypes
+    f_ = nh.lib()._mlir_ciface_nova_hip_layer_norm_f32
+    eps = ctypes.c_float(1e-5)
+
+    def fn(i):
+        p = sets[i % 3][0]
+        rc = f_(*p, eps)
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, args.steps * 2, args.warmup, torch)
+    gbs = LN_BYTES / (ms * 1e-3) / 1e9
+    return {"ms": ms, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
+
+
+def bench_sce(args, torch, nh, S):
+    inp = S.config_inputs("c5_sce")
+    sets = []
+    for _ in range(3):
+        x = to_dev(inp["logits"], S.F32, torch)
+        t = torch.from_numpy(inp["labels"]).cuda()
+        loss = torch.empty(1, device="cuda")
+        sets.append(([nh.ref(nh.memref_of(v)) for v in (x, t, loss)], (x, t, loss)))
+    del inp
+    f_ = nh.lib()._mlir_ciface_nova_hip_sce_f32
+
+    def fn(i):
+        p = sets[i % 3][0]
+        rc = f_(p[0], p[1], p[2], None)
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, args.steps * 2, args.warmup, torch)
+    gbs = SCE_BYTES / (ms * 1e-3) / 1e9
+    return {"ms": ms, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS,
+            "loss": float(sets[0][1][2].cpu()[0])}
+
+
+def cpu_baseline(S):
+    """The CPU oracle (restatement of Nova's single-threaded CPU pipeline)
+    on a bounded slab of config 2: batch 0, the first R rows, all 4096
+    columns, K = 4096; R grows until ~12 s of CPU work.  TFLOP/s of the
+    slab, which extrapolates linearly to the full config."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import nova_cpu_ref as ref
+    n = 8 * 4096 * 4096
+    A = S.uniform((1, 4096, 4096), 1, dtype=S.BF16)
+    B = S.uniform((1, 4096, 4096), 1, dtype=S.BF16, offset=n)
+    rows, spent = 0, 0.0
+    step = 8
+    while spent < 12.0 and rows < 256:
+        t0 = time.perf_counter()
+        ref.gemm(A[:, rows:rows + step], B, adt=S.BF16, bdt=S.BF16)
+        spent += time.perf_counter() - t0
+        rows += step
+    flop = 2.0 * rows * 4096 * 4096
+    tf = flop / spent / 1e12
+    return {"value": tf, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"config 2 slab: batch 0, rows 0-{rows - 1}, all 4096 columns, K=4096 "
+                      f"({flop:.3g} FLOP in {spent:.1f} s, single thread, "
+                      f"oracle/nova_cpu_ref.c i-j-k loop order); extrapolated linearly",
+            "full_config_seconds_extrapolated": C2_FLOP / (tf * 1e12),
+            "host_cpus": os.cpu_count()}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not "
+              "supported (the multi-GPU sharding plan is design-only).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import nova_hip as nh
+    import nova_seed as S
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    nh.lib()
+    only = set(args.only.split(",")) if args.only else {"c2", "c3", "c4", "ln", "sce"}
+    cfg = {}
+
+    def stage(name, f):
+        t0 = time.time()
+        print(f"[bench] {name} ...", file=sys.stderr, flush=True)
+        r = f()
+        print(f"[bench] {name}: {json.dumps(r)} ({time.time() - t0:.1f} s)", file=sys.stderr,
+              flush=True)
+        torch.cuda.empty_cache()
+        return r
+
+    c2 = stage("c2", lambda: bench_c2(args, torch, nh, S)) if "c2" in only else None
+    if "c3" in only:
+        cfg["c3_linear_bias_gelu_bf16"] = stage("c3", lambda: bench_c3(args, torch, nh, S))
+    if "c4" in only:
+        cfg["c4a_fp16_96x197x197x64"] = stage("c4a", lambda: bench_c4(args, torch, nh, S, "c4a", C4A_BYTES))
+        cfg["c4b_fp16_96x197x64x197"] = stage("c4b", lambda: bench_c4(args, torch, nh, S, "c4b", C4B_BYTES))
+    if "ln" in only:
+        cfg["c5_layer_norm_f32_16384x4096"] = stage("ln", lambda: bench_ln(args, torch, nh, S))
+    if "sce" in only:
+        cfg["c5_sce_f32_4096x32000"] = stage("sce", lambda: bench_sce(args, torch, nh, S))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = stage("cpu_baseline", lambda: cpu_baseline(S))
+
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "gemm_c2_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    head = c2 or {"ms": float("nan"), "tflops": float("nan"), "frac_mfma": float("nan")}
+    line = {
+        "metric": "batch-GEMM TFLOP/s & % MFMA peak; reduction HBM GB/s & % peak (1 MI355X)",
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded counter-based generator (nova-compiler_amd/host/nova_seed.c), "
+                "A,B uniform[-1,1] seed 1",
+        "config": {"workload": "c2: linalg.batch_matmul bf16 x bf16 -> f32 accumulate/output, "
+                               "batch=8, M=N=K=4096",
+                   "kernel": "gemm_mfma_kernel 256x256x64, v_mfma_f32_32x32x16_bf16",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": head["frac_mfma"], "traffic": traffic},
+        "cpu_baseline": cpu,
+        "configs": cfg,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,226 @@
+/*
+ * nova_hip.h -- C ABI of libnova_hip, the MI355X (gfx950) kernels behind
+ * Nova's GPU matmul / reduction path.
+ *
+ * Every compute entry point is named `_mlir_ciface_nova_hip_<op>` and takes
+ * pointers to MLIR strided-memref descriptors, so that a lowering which
+ * emits
+ *     func.func private @nova_hip_<op>(memref<...>, ...) -> i32
+ *         attributes {llvm.emit_c_interface}
+ *     %rc = func.call @nova_hip_<op>(...) : (...) -> i32
+ * links against this library with no glue.  The descriptor layout is the one
+ * MLIR's C interface passes (`_mlir_ciface_<fn>(Desc*...)`), exactly what the
+ * reference's own host harness builds by hand in robust_driver.cpp:9-23 and
+ * driver.cpp:9-17 ({allocated, aligned, offset, sizes[R], strides[R]}).
+ *
+ * Conventions (all entry points):
+ *   - memref data pointers are DEVICE pointers owned by the caller (the
+ *     reference's address-space-1 convention, robust_driver.cpp:25-39);
+ *     the library never allocates or frees caller buffers.  It owns only a
+ *     cached per-stream workspace (SCE partial losses).
+ *   - offsets and strides are in elements and are honoured.  The innermost
+ *     dimension of every operand must have unit stride, except where a GEMM
+ *     operand is a transposed view (its second-to-last stride is 1 instead).
+ *   - return value: NOVA_HIP_SUCCESS (0) or a NOVA_HIP_E* code; the text of
+ *     the last error on the calling thread is in nova_hip_last_error().
+ *     The reference's compiled entry points return void and ignore every
+ *     CUDA status (FixGpuLaunch.cpp:49); these report instead.
+ *   - launches are asynchronous on the calling thread's stream
+ *     (nova_hip_set_stream; default: the null stream).
+ */
+#ifndef NOVA_HIP_H
+#define NOVA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* MLIR StridedMemRefType<T, R> for R = 1, 2, 3 (element type erased). */
+typedef struct NovaMemRef1D {
+  void *allocated;
+  void *aligned;
+  int64_t offset;
+  int64_t sizes[1];
+  int64_t strides[1];
+} NovaMemRef1D;
+
+typedef struct NovaMemRef2D {
+  void *allocated;
+  void *aligned;
+  int64_t offset;
+  int64_t sizes[2];
+  int64_t strides[2];
+} NovaMemRef2D;
+
+typedef struct NovaMemRef3D {
+  void *allocated;
+  void *aligned;
+  int64_t offset;
+  int64_t sizes[3];
+  int64_t strides[3];
+} NovaMemRef3D;
+
+/* Status codes. */
+enum {
+  NOVA_HIP_SUCCESS = 0,
+  NOVA_HIP_EINVAL = 1,    /* null descriptor / data pointer, bad flag bits  */
+  NOVA_HIP_ESHAPE = 2,    /* operand shapes disagree                        */
+  NOVA_HIP_ESTRIDE = 3,   /* stride pattern the kernels do not address      */
+  NOVA_HIP_EDTYPE = 4,    /* dtype / epilogue combination not provided      */
+  NOVA_HIP_ERANGE = 5,    /* size beyond the kernels' index range           */
+  NOVA_HIP_EDEVICE = 6,   /* HIP runtime error (details in last_error)      */
+  NOVA_HIP_ENOMEM = 7     /* workspace allocation failed                    */
+};
+
+/* dtype codes (flags bits 0-3: input, 4-7: output, 12-15: bias). */
+enum {
+  NOVA_HIP_DT_F32 = 0,
+  NOVA_HIP_DT_BF16 = 1,
+  NOVA_HIP_DT_F16 = 2
+};
+
+/* epilogue codes (flags bits 8-11). */
+enum {
+  NOVA_HIP_EPI_NONE = 0,
+  NOVA_HIP_EPI_BIAS = 1,      /* C = A.B + bias[n]                           */
+  NOVA_HIP_EPI_BIAS_GELU = 2, /* C = gelu_tanh(A.B + bias[n])                */
+  NOVA_HIP_EPI_GELU = 3       /* C = gelu_tanh(A.B)                          */
+};
+
+#define NOVA_HIP_GEMM_FLAGS(in_dt, out_dt, epi, bias_dt)                     \
+  ((int32_t)(((in_dt) & 0xf) | (((out_dt) & 0xf) << 4) |                     \
+             (((epi) & 0xf) << 8) | (((bias_dt) & 0xf) << 12)))
+
+/* ------------------------------------------------------------------------
+ * GEMM family.
+ *
+ * General batched contraction C[b,m,n] = epi(sum_k A[b,m,k] * B[b,k,n]),
+ * f32 accumulate.  Replaces, for these ops, the LLVMGPU code generation of
+ * `nova-gpu-optimized-pipeline` (lib/Transforms/LLVMGPU/Passes.cpp:115-372)
+ * applied to the linalg.matmul / linalg.batch_matmul that
+ * NovaMatmulOpLowering produces (NovaToLinalg.cpp:874-1051, rank-3 at :1040,
+ * rank-2 at :1045), the bias accumulator init of FuseMatmulBias
+ * (FuseMatmulBias.cpp:95-199) and the nova.gelu generic
+ * (NovaToLinalgGeneric.cpp:1277-1337) that follows nova.linear.
+ *
+ *   A : [B, M, K]  unit stride on K (row-major) or on M (transposed view);
+ *                  batch stride 0 broadcasts a rank-2 operand
+ *                  (NovaToLinalg.cpp:992-1025).
+ *   B : [B, K, N]  unit stride on N (row-major) or on K (transposed view,
+ *                  e.g. nova.transpose of a [N,K] weight).
+ *   C : [B, M, N]  unit stride on N.
+ *   bias : [N] unit stride, or NULL when the epilogue has no bias.
+ *   flags : NOVA_HIP_GEMM_FLAGS(in, out, epilogue, bias dtype).
+ * Inputs f32 use an exact f32 kernel (sequential k, unfused multiply-add,
+ * the reference's CPU arithmetic); bf16 / f16 inputs use MFMA with f32
+ * accumulate.  Low-precision outputs are rounded to nearest-even.
+ * ---------------------------------------------------------------------- */
+int32_t _mlir_ciface_nova_hip_gemm(const NovaMemRef3D *A, const NovaMemRef3D *B,
+                                   NovaMemRef3D *C, const NovaMemRef1D *bias,
+                                   int32_t flags);
+
+/* nova.matmul rank 2, f32 x f32 -> f32 (NovaOps.cpp:1116-1285 result type;
+ * linalg.matmul at NovaToLinalg.cpp:1045). */
+int32_t _mlir_ciface_nova_hip_matmul_f32(const NovaMemRef2D *A,
+                                         const NovaMemRef2D *B,
+                                         NovaMemRef2D *C);
+
+/* nova.matmul rank 3 (linalg.batch_matmul, NovaToLinalg.cpp:1040), f32. */
+int32_t _mlir_ciface_nova_hip_batch_matmul_f32(const NovaMemRef3D *A,
+                                               const NovaMemRef3D *B,
+                                               NovaMemRef3D *C);
+
+/* linalg.batch_matmul with bf16 ins and f32 outs (test/pipeline-tests/
+ * 03_batch_matmul.mlir:20-26 form; bf16 x bf16 nova.matmul infers f16,
+ * NovaOps.cpp:1198, so the f32-accumulate form is spelled in linalg or with
+ * nova.cast operands). */
+int32_t _mlir_ciface_nova_hip_batch_matmul_bf16_f32(const NovaMemRef3D *A,
+                                                    const NovaMemRef3D *B,
+                                                    NovaMemRef3D *C);
+
+/* Same, f16 ins and f32 outs. */
+int32_t _mlir_ciface_nova_hip_batch_matmul_f16_f32(const NovaMemRef3D *A,
+                                                   const NovaMemRef3D *B,
+                                                   NovaMemRef3D *C);
+
+/* Rank-2 low-precision forms of the two entry points above. */
+int32_t _mlir_ciface_nova_hip_matmul_bf16_f32(const NovaMemRef2D *A,
+                                              const NovaMemRef2D *B,
+                                              NovaMemRef2D *C);
+int32_t _mlir_ciface_nova_hip_matmul_f16_f32(const NovaMemRef2D *A,
+                                             const NovaMemRef2D *B,
+                                             NovaMemRef2D *C);
+
+/* nova.linear (NovaToLinalgGeneric.cpp:1623-1822; result type
+ * NovaOps.cpp:2075-2103) with the bias folded into the accumulator
+ * (FuseMatmulBias.cpp:184-188), optionally followed by nova.gelu
+ * (NovaToLinalgGeneric.cpp:1277-1337) and nova.cast to the output dtype
+ * (NovaToLinalgGeneric.cpp:37-85).
+ *   x : [M, K]; weight : [K, N] (a row-major [K,N] tensor, or the
+ *   nova.transpose view of a row-major [N,K] tensor: strides {1, K});
+ *   bias : [N]; y : [M, N].  flags as for _mlir_ciface_nova_hip_gemm. */
+int32_t _mlir_ciface_nova_hip_linear(const NovaMemRef2D *x,
+                                     const NovaMemRef2D *weight,
+                                     const NovaMemRef1D *bias, NovaMemRef2D *y,
+                                     int32_t flags);
+
+/* The config-3 form: bf16 x, bf16 weight view, bf16 bias, GELU(tanh),
+ * bf16 y, f32 accumulate. */
+int32_t _mlir_ciface_nova_hip_linear_bf16_bias_gelu(const NovaMemRef2D *x,
+                                                    const NovaMemRef2D *weight,
+                                                    const NovaMemRef1D *bias,
+                                                    NovaMemRef2D *y);
+
+/* ------------------------------------------------------------------------
+ * Reductions (HBM bound, no MFMA).
+ * ---------------------------------------------------------------------- */
+
+/* nova.layer_norm over the last dim (NovaLayerNormPattern,
+ * NovaToLinalgGeneric.cpp:1997-2126; results (y, mean_sum, var_sum) of
+ * NovaOps.td:1027-1037 where var_sum carries rstd, :2123).
+ *   x, y : [R, D] f32; gamma, beta : [D] f32;
+ *   mean_sum : [R] f32 row sums S, or NULL;  rstd : [R] f32, or NULL.
+ * eps: the op hard-codes 1e-5 (NovaToLinalgGeneric.cpp:2025). */
+int32_t _mlir_ciface_nova_hip_layer_norm_f32(const NovaMemRef2D *x,
+                                             const NovaMemRef1D *gamma,
+                                             const NovaMemRef1D *beta,
+                                             NovaMemRef2D *y,
+                                             NovaMemRef1D *mean_sum,
+                                             NovaMemRef1D *rstd, float eps);
+
+/* nova.sce (NovaSceForwardLowering, NovaToLinalgGeneric.cpp:801-1010;
+ * results (softmax, loss[1]) of NovaOps.td:880-896) with the mean of
+ * lowerFullReduceMeanToSCF (NovaToLinalg.cpp:1974-2126).
+ *   logits : [R, C] f32; labels : [R] i32 in [0, C);
+ *   loss : [1] f32; softmax : [R, C] f32, or NULL when unused.
+ * A label outside [0, C) makes that row's loss, and so the mean, NaN. */
+int32_t _mlir_ciface_nova_hip_sce_f32(const NovaMemRef2D *logits,
+                                      const NovaMemRef1D *labels,
+                                      NovaMemRef1D *loss,
+                                      NovaMemRef2D *softmax);
+
+/* ------------------------------------------------------------------------
+ * Runtime.  The reference's host runtime is libmlir_cuda_runtime's mgpu*
+ * calls plus cudaMallocAsync / cudaMemcpyAsync declared by FixGpuLaunch.cpp
+ * (:49, :214); this library needs only a stream to launch on.
+ * ---------------------------------------------------------------------- */
+
+/* Stream (a hipStream_t) used by the calling thread's later launches. */
+void nova_hip_set_stream(void *stream);
+void *nova_hip_get_stream(void);
+/* Wait for the calling thread's stream. */
+int32_t nova_hip_synchronize(void);
+/* Text of the calling thread's last error ("" if none). */
+const char *nova_hip_last_error(void);
+/* Library version string. */
+const char *nova_hip_version(void);
+/* Release the cached workspaces (e.g. before a process-level teardown). */
+int32_t nova_hip_release_workspace(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NOVA_HIP_H */

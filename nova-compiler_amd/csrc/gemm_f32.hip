@@ -1,0 +1,167 @@
+// Exact f32 GEMM: C[b,m,n] = init + sum_k A[b,m,k] * B[b,k,n], k ascending,
+// every multiply and add separately rounded.  This is the arithmetic of
+// Nova's CPU pipeline for f32 linalg.matmul / batch_matmul (no fast-math,
+// no FMA contraction, sequential k: Pipeline.cpp:61-187), so the result is
+// bit-identical to it, including the bias-initialised accumulator of
+// FuseMatmulBias (FuseMatmulBias.cpp:184-188).  The reference's GPU path
+// would have used tf32 mma.sync for f32 (SURVEY of
+// NovaGPUNestedLayoutDistributionPatterns.cpp:2460); this kernel does not,
+// because tf32 breaks 1e-4 parity.
+//
+// 64x64 output tile per 256-thread workgroup, 4x4 outputs per thread,
+// K staged through LDS 16 at a time.  f32 GEMM is the plumbing path (bf16
+// and f16 carry the throughput), so it is VALU-bound by design.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "nova_hip_internal.h"
+
+namespace nova_hip {
+namespace {
+
+constexpr int kT = 64;   // output tile edge
+constexpr int kKs = 16;  // k per LDS stage
+
+struct F32Args {
+  const float *A;
+  const float *B;
+  float *C;
+  const void *bias;
+  int64_t sab, sam, sak;
+  int64_t sbb, sbk, sbn;
+  int64_t scb, scm;
+  int M, N, K;
+  int tiles_m, tiles_n;
+  int bias_dt, epi;
+};
+
+__device__ __forceinline__ float bias_value(const void *bias, int dt, int n) {
+  if (dt == NOVA_HIP_DT_F32) return static_cast<const float *>(bias)[n];
+  const uint16_t h = static_cast<const uint16_t *>(bias)[n];
+  if (dt == NOVA_HIP_DT_BF16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ float gelu_ref(float x) {
+#pragma clang fp contract(off)
+  const float x2 = x * x;
+  const float x3 = x2 * x;
+  const float cubic = 4.471500e-02f * x3;
+  const float inner = x + cubic;
+  const float scaled = 0.7978845608028654f * inner;
+  const float t = tanhf(scaled);
+  return (0.5f * x) * (1.0f + t);
+}
+
+__global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
+#pragma clang fp contract(off)
+  __shared__ float sa[kKs][kT + 4];
+  __shared__ float sb[kKs][kT + 4];
+
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / tiles;
+  const int t = blockIdx.x - b * tiles;
+  const int m0 = (t / a.tiles_n) * kT;
+  const int n0 = (t % a.tiles_n) * kT;
+  const int tid = threadIdx.x;
+  const int tx = tid & 15, ty = tid >> 4;
+
+  const float *Ab = a.A + (int64_t)b * a.sab;
+  const float *Bb = a.B + (int64_t)b * a.sbb;
+
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
+
+  float acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + tx * 4 + j;
+    const float init = (has_bias && n < a.N) ? bias_value(a.bias, a.bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i][j] = init;
+  }
+
+  for (int k0 = 0; k0 < a.K; k0 += kKs) {
+    // 64x16 A tile and 16x64 B tile, 4 elements of each per thread.
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int q = tid + e * 256;
+      const int r = q & 63, kk = q >> 6;   // A: row r, k kk
+      const int gm = m0 + r, gk = k0 + kk;
+      sa[kk][r] = (gm < a.M && gk < a.K) ? Ab[(int64_t)gm * a.sam + (int64_t)gk * a.sak] : 0.0f;
+      const int c = q & 63, kb = q >> 6;   // B: k kb, column c
+      const int gn = n0 + c, gkb = k0 + kb;
+      sb[kb][c] = (gn < a.N && gkb < a.K) ? Bb[(int64_t)gkb * a.sbk + (int64_t)gn * a.sbn] : 0.0f;
+    }
+    __syncthreads();
+    const int kend = min(kKs, a.K - k0);
+    for (int kk = 0; kk < kend; ++kk) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = sa[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = sb[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = av[i] * bv[j];
+          acc[i][j] = acc[i][j] + p;
+        }
+    }
+    __syncthreads();
+  }
+
+  float *Cb = a.C + (int64_t)b * a.scb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tx * 4 + j;
+      if (n >= a.N) continue;
+      float v = acc[i][j];
+      if (has_gelu) v = gelu_ref(v);
+      Cb[(int64_t)m * a.scm + n] = v;
+    }
+  }
+}
+
+}  // namespace
+
+int32_t launch_gemm_f32(const GemmProblem &p, hipStream_t s) {
+  if (p.batch == 0 || p.M == 0 || p.N == 0) return NOVA_HIP_SUCCESS;
+  if (p.M > 0x7fffffff || p.N > 0x7fffffff || p.K > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "gemm_f32: dimension exceeds 2^31-1");
+  if (p.out_dt != NOVA_HIP_DT_F32)
+    return fail(NOVA_HIP_EDTYPE, "gemm_f32: f32 inputs produce f32 output only");
+  F32Args a;
+  a.A = static_cast<const float *>(p.A);
+  a.B = static_cast<const float *>(p.B);
+  a.C = static_cast<float *>(p.C);
+  a.bias = p.bias;
+  a.sab = p.sab;
+  a.sbb = p.sbb;
+  // Expand the (contiguous dim, outer stride) description back to strides.
+  a.sam = p.a_kcontig ? p.sa_outer : 1;
+  a.sak = p.a_kcontig ? 1 : p.sa_outer;
+  a.sbk = p.b_kcontig ? 1 : p.sb_outer;
+  a.sbn = p.b_kcontig ? p.sb_outer : 1;
+  a.scb = p.scb;
+  a.scm = p.scm;
+  a.M = (int)p.M;
+  a.N = (int)p.N;
+  a.K = (int)p.K;
+  a.tiles_m = (int)((p.M + kT - 1) / kT);
+  a.tiles_n = (int)((p.N + kT - 1) / kT);
+  a.bias_dt = p.bias_dt;
+  a.epi = p.epi;
+  const int64_t total = p.batch * a.tiles_m * a.tiles_n;
+  if (total > 0x7fffffff) return fail(NOVA_HIP_ERANGE, "gemm_f32: grid too large");
+  hipLaunchKernelGGL(gemm_f32_exact_kernel, dim3((unsigned)total), dim3(256), 0, s, a);
+  return check_hip(hipGetLastError(), "gemm_f32 launch");
+}
+
+}  // namespace nova_hip

@@ -1,0 +1,393 @@
+// C ABI of libnova_hip: descriptor validation, flag decoding, per-thread
+// stream and error text, and the per-stream workspace cache.  Every check
+// here runs on the host before any HIP call, so malformed calls fail with a
+// status code instead of reaching a kernel.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+
+#include "nova_hip_internal.h"
+
+namespace nova_hip {
+
+namespace {
+thread_local char t_err[512] = {0};
+thread_local hipStream_t t_stream = nullptr;
+
+struct Workspace {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::unordered_map<hipStream_t, Workspace> g_ws;
+}  // namespace
+
+int32_t fail(int32_t code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(t_err, sizeof(t_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { t_err[0] = 0; }
+
+hipStream_t current_stream() { return t_stream; }
+
+int32_t check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess) return NOVA_HIP_SUCCESS;
+  return fail(NOVA_HIP_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+void *workspace(hipStream_t s, size_t bytes) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  Workspace &w = g_ws[s];
+  if (w.bytes >= bytes && w.ptr) return w.ptr;
+  if (w.ptr) {
+    // The old buffer may still be read by queued work on this stream.
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      check_hip(e, "workspace: stream synchronize");
+      return nullptr;
+    }
+    (void)hipFree(w.ptr);
+    w.ptr = nullptr;
+    w.bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, want);
+  if (e != hipSuccess) {
+    fail(NOVA_HIP_ENOMEM, "workspace: hipMalloc(%zu): %s", want, hipGetErrorString(e));
+    return nullptr;
+  }
+  // Counters at the front of the workspace must start at zero; kernels
+  // restore them to zero when they finish.
+  e = hipMemsetAsync(p, 0, want, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    check_hip(e, "workspace: clear");
+    return nullptr;
+  }
+  w.ptr = p;
+  w.bytes = want;
+  return p;
+}
+
+namespace {
+
+// ---- descriptor helpers ----------------------------------------------------
+template <typename D>
+const char *data_of(const D *d) {
+  return static_cast<const char *>(d->aligned);
+}
+
+template <typename D>
+bool nonneg_sizes(const D *d, int rank) {
+  for (int i = 0; i < rank; ++i)
+    if (d->sizes[i] < 0) return false;
+  return true;
+}
+
+int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt) {
+  if (flags & ~0xffff) return fail(NOVA_HIP_EINVAL, "gemm: unknown flag bits 0x%x", flags);
+  in_dt = flags & 0xf;
+  out_dt = (flags >> 4) & 0xf;
+  epi = (flags >> 8) & 0xf;
+  bias_dt = (flags >> 12) & 0xf;
+  if (in_dt > NOVA_HIP_DT_F16 || out_dt > NOVA_HIP_DT_F16 || bias_dt > NOVA_HIP_DT_F16 ||
+      epi > NOVA_HIP_EPI_GELU)
+    return fail(NOVA_HIP_EDTYPE, "gemm: bad dtype/epilogue code in flags 0x%x", flags);
+  if (in_dt == NOVA_HIP_DT_F32 && out_dt != NOVA_HIP_DT_F32)
+    return fail(NOVA_HIP_EDTYPE, "gemm: f32 inputs produce f32 output only");
+  return NOVA_HIP_SUCCESS;
+}
+
+// Validate and normalise a batched GEMM given 3-D views.
+int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
+                  const NovaMemRef1D *bias, int32_t flags) {
+  clear_error();
+  if (!A || !B || !C) return fail(NOVA_HIP_EINVAL, "gemm: null descriptor");
+  int in_dt, out_dt, epi, bias_dt;
+  int32_t rc = decode_flags(flags, in_dt, out_dt, epi, bias_dt);
+  if (rc) return rc;
+  if (!nonneg_sizes(A, 3) || !nonneg_sizes(B, 3) || !nonneg_sizes(C, 3))
+    return fail(NOVA_HIP_ESHAPE, "gemm: negative size");
+  const int64_t batch = C->sizes[0], M = C->sizes[1], N = C->sizes[2];
+  const int64_t K = A->sizes[2];
+  if (A->sizes[1] != M || B->sizes[2] != N || B->sizes[1] != K)
+    return fail(NOVA_HIP_ESHAPE,
+                "gemm: shapes A[%lld,%lld,%lld] B[%lld,%lld,%lld] C[%lld,%lld,%lld] disagree",
+                (long long)A->sizes[0], (long long)A->sizes[1], (long long)A->sizes[2],
+                (long long)B->sizes[0], (long long)B->sizes[1], (long long)B->sizes[2],
+                (long long)batch, (long long)M, (long long)N);
+  // Batch: equal, or 1 with any stride (broadcast a rank-2 operand).
+  if ((A->sizes[0] != batch && A->sizes[0] != 1) || (B->sizes[0] != batch && B->sizes[0] != 1))
+    return fail(NOVA_HIP_ESHAPE, "gemm: batch sizes %lld/%lld do not broadcast to %lld",
+                (long long)A->sizes[0], (long long)B->sizes[0], (long long)batch);
+  const bool has_bias = (epi == NOVA_HIP_EPI_BIAS || epi == NOVA_HIP_EPI_BIAS_GELU);
+  if (has_bias) {
+    if (!bias || !bias->aligned) return fail(NOVA_HIP_EINVAL, "gemm: epilogue needs a bias");
+    if (bias->sizes[0] != N) return fail(NOVA_HIP_ESHAPE, "gemm: bias size %lld != N %lld",
+                                         (long long)bias->sizes[0], (long long)N);
+    if (bias->strides[0] != 1 && N > 1) return fail(NOVA_HIP_ESTRIDE, "gemm: bias must be contiguous");
+  }
+  const bool empty = batch == 0 || M == 0 || N == 0;
+  if (!empty && (!A->aligned || !B->aligned || !C->aligned))
+    return fail(NOVA_HIP_EINVAL, "gemm: null data pointer");
+
+  GemmProblem p;
+  p.batch = batch;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.in_dt = in_dt;
+  p.out_dt = out_dt;
+  p.epi = epi;
+  p.bias_dt = bias_dt;
+  const int esz = dtype_size(in_dt);
+  const int osz = dtype_size(out_dt);
+  p.A = data_of(A) + A->offset * esz;
+  p.B = data_of(B) + B->offset * esz;
+  p.C = const_cast<char *>(data_of(C)) + C->offset * osz;
+  p.bias = has_bias ? (const void *)(data_of(bias) + bias->offset * dtype_size(bias_dt)) : nullptr;
+
+  // Each operand is addressed as (unit-stride dim, stride of the other dim).
+  // A [M,K]: unit stride on K (row-major) or on M (transposed view).  A
+  // dim of extent 1 is never stepped, so its stride does not matter.
+  const int64_t a_sm = A->strides[1], a_sk = A->strides[2];
+  if (a_sk == 1 || K <= 1) {
+    p.a_kcontig = true;
+    p.sa_outer = a_sm;
+  } else if (a_sm == 1 || M <= 1) {
+    p.a_kcontig = false;
+    p.sa_outer = a_sk;
+  } else {
+    return fail(NOVA_HIP_ESTRIDE, "gemm: A strides [%lld,%lld] have no unit stride",
+                (long long)a_sm, (long long)a_sk);
+  }
+  // B [K,N]: unit stride on N (row-major) or on K (transposed view, e.g.
+  // nova.transpose of a row-major [N,K] weight).
+  const int64_t b_sk = B->strides[1], b_sn = B->strides[2];
+  if (b_sn == 1 || N <= 1) {
+    p.b_kcontig = false;
+    p.sb_outer = b_sk;
+  } else if (b_sk == 1 || K <= 1) {
+    p.b_kcontig = true;
+    p.sb_outer = b_sn;
+  } else {
+    return fail(NOVA_HIP_ESTRIDE, "gemm: B strides [%lld,%lld] have no unit stride",
+                (long long)b_sk, (long long)b_sn);
+  }
+  if (C->strides[2] != 1 && N > 1) return fail(NOVA_HIP_ESTRIDE, "gemm: C must have unit stride on N");
+  if (M > 1 && C->strides[1] < N) return fail(NOVA_HIP_ESTRIDE, "gemm: C rows overlap");
+  if (p.sa_outer < 0 || p.sb_outer < 0 || C->strides[1] < 0)
+    return fail(NOVA_HIP_ESTRIDE, "gemm: negative strides are not addressed");
+  p.sab = (A->sizes[0] == 1) ? 0 : A->strides[0];
+  p.sbb = (B->sizes[0] == 1) ? 0 : B->strides[0];
+  p.scb = C->strides[0];
+  p.scm = C->strides[1];
+  if (p.sab < 0 || p.sbb < 0 || p.scb < 0)
+    return fail(NOVA_HIP_ESTRIDE, "gemm: negative batch stride");
+  if (empty) return NOVA_HIP_SUCCESS;
+
+  hipStream_t s = current_stream();
+  return (in_dt == NOVA_HIP_DT_F32) ? launch_gemm_f32(p, s) : launch_gemm_mfma(p, s);
+}
+
+NovaMemRef3D lift(const NovaMemRef2D *d) {
+  NovaMemRef3D r;
+  r.allocated = d->allocated;
+  r.aligned = d->aligned;
+  r.offset = d->offset;
+  r.sizes[0] = 1;
+  r.sizes[1] = d->sizes[0];
+  r.sizes[2] = d->sizes[1];
+  r.strides[0] = 0;
+  r.strides[1] = d->strides[0];
+  r.strides[2] = d->strides[1];
+  return r;
+}
+
+int32_t gemm2d(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C,
+               const NovaMemRef1D *bias, int32_t flags) {
+  if (!A || !B || !C) {
+    clear_error();
+    return fail(NOVA_HIP_EINVAL, "gemm: null descriptor");
+  }
+  NovaMemRef3D a = lift(A), b = lift(B), c = lift(C);
+  return gemm_core(&a, &b, &c, bias, flags);
+}
+
+}  // namespace
+}  // namespace nova_hip
+
+using namespace nova_hip;
+
+extern "C" {
+
+int32_t _mlir_ciface_nova_hip_gemm(const NovaMemRef3D *A, const NovaMemRef3D *B,
+                                   NovaMemRef3D *C, const NovaMemRef1D *bias,
+                                   int32_t flags) {
+  return gemm_core(A, B, C, bias, flags);
+}
+
+int32_t _mlir_ciface_nova_hip_matmul_f32(const NovaMemRef2D *A, const NovaMemRef2D *B,
+                                         NovaMemRef2D *C) {
+  return gemm2d(A, B, C, nullptr,
+                NOVA_HIP_GEMM_FLAGS(NOVA_HIP_DT_F32, NOVA_HIP_DT_F32, NOVA_HIP_EPI_NONE, 0));
+}
+
+int32_t _mlir_ciface_nova_hip_batch_matmul_f32(const NovaMemRef3D *A, const NovaMemRef3D *B,
+                                               NovaMemRef3D *C) {
+  return gemm_core(A, B, C, nullptr,
+                   NOVA_HIP_GEMM_FLAGS(NOVA_HIP_DT_F32, NOVA_HIP_DT_F32, NOVA_HIP_EPI_NONE, 0));
+}
+
+int32_t _mlir_ciface_nova_hip_batch_matmul_bf16_f32(const NovaMemRef3D *A,
+                                                    const NovaMemRef3D *B,
+                                                    NovaMemRef3D *C) {
+  return gemm_core(A, B, C, nullptr,
+                   NOVA_HIP_GEMM_FLAGS(NOVA_HIP_DT_BF16, NOVA_HIP_DT_F32, NOVA_HIP_EPI_NONE, 0));
+}
+
+int32_t _mlir_ciface_nova_hip_batch_matmul_f16_f32(const NovaMemRef3D *A,
+                                                   const NovaMemRef3D *B,
+                                                   NovaMemRef3D *C) {
+  return gemm_core(A, B, C, nullptr,
+                   NOVA_HIP_GEMM_FLAGS(NOVA_HIP_DT_F16, NOVA_HIP_DT_F32, NOVA_HIP_EPI_NONE, 0));
+}
+
+int32_t _mlir_ciface_nova_hip_matmul_bf16_f32(const NovaMemRef2D *A, const NovaMemRef2D *B,
+                                              NovaMemRef2D *C) {
+  return gemm2d(A, B, C, nullptr,
+                NOVA_HIP_GEMM_FLAGS(NOVA_HIP_DT_BF16, NOVA_HIP_DT_F32, NOVA_HIP_EPI_NONE, 0));
+}
+
+int32_t _mlir_ciface_nova_hip_matmul_f16_f32(const NovaMemRef2D *A, const NovaMemRef2D *B,
+                                             NovaMemRef2D *C) {
+  return gemm2d(A, B, C, nullptr,
+                NOVA_HIP_GEMM_FLAGS(NOVA_HIP_DT_F16, NOVA_HIP_DT_F32, NOVA_HIP_EPI_NONE, 0));
+}
+
+int32_t _mlir_ciface_nova_hip_linear(const NovaMemRef2D *x, const NovaMemRef2D *weight,
+                                     const NovaMemRef1D *bias, NovaMemRef2D *y,
+                                     int32_t flags) {
+  return gemm2d(x, weight, y, bias, flags);
+}
+
+int32_t _mlir_ciface_nova_hip_linear_bf16_bias_gelu(const NovaMemRef2D *x,
+                                                    const NovaMemRef2D *weight,
+                                                    const NovaMemRef1D *bias,
+                                                    NovaMemRef2D *y) {
+  return gemm2d(x, weight, y, bias,
+                NOVA_HIP_GEMM_FLAGS(NOVA_HIP_DT_BF16, NOVA_HIP_DT_BF16,
+                                    NOVA_HIP_EPI_BIAS_GELU, NOVA_HIP_DT_BF16));
+}
+
+int32_t _mlir_ciface_nova_hip_layer_norm_f32(const NovaMemRef2D *x, const NovaMemRef1D *gamma,
+                                             const NovaMemRef1D *beta, NovaMemRef2D *y,
+                                             NovaMemRef1D *mean_sum, NovaMemRef1D *rstd,
+                                             float eps) {
+  clear_error();
+  if (!x || !gamma || !beta || !y) return fail(NOVA_HIP_EINVAL, "layer_norm: null descriptor");
+  const int64_t R = x->sizes[0], D = x->sizes[1];
+  if (R < 0 || D < 0) return fail(NOVA_HIP_ESHAPE, "layer_norm: negative size");
+  if (y->sizes[0] != R || y->sizes[1] != D)
+    return fail(NOVA_HIP_ESHAPE, "layer_norm: y shape differs from x");
+  if (gamma->sizes[0] != D || beta->sizes[0] != D)
+    return fail(NOVA_HIP_ESHAPE, "layer_norm: gamma/beta size != D");
+  if (mean_sum && mean_sum->sizes[0] != R) return fail(NOVA_HIP_ESHAPE, "layer_norm: mean_sum size != rows");
+  if (rstd && rstd->sizes[0] != R) return fail(NOVA_HIP_ESHAPE, "layer_norm: rstd size != rows");
+  if (R == 0) return NOVA_HIP_SUCCESS;
+  if (D == 0) return fail(NOVA_HIP_ESHAPE, "layer_norm: empty normalised dim");
+  if ((x->strides[1] != 1 && D > 1) || (y->strides[1] != 1 && D > 1) ||
+      (gamma->strides[0] != 1 && D > 1) || (beta->strides[0] != 1 && D > 1))
+    return fail(NOVA_HIP_ESTRIDE, "layer_norm: last dim must be contiguous");
+  if ((mean_sum && mean_sum->strides[0] != 1 && R > 1) || (rstd && rstd->strides[0] != 1 && R > 1))
+    return fail(NOVA_HIP_ESTRIDE, "layer_norm: stats must be contiguous");
+  if (!x->aligned || !y->aligned || !gamma->aligned || !beta->aligned ||
+      (mean_sum && !mean_sum->aligned) || (rstd && !rstd->aligned))
+    return fail(NOVA_HIP_EINVAL, "layer_norm: null data pointer");
+  if ((R > 1 && (x->strides[0] < D || y->strides[0] < D)))
+    return fail(NOVA_HIP_ESTRIDE, "layer_norm: rows overlap");
+  LayerNormProblem p;
+  p.x = reinterpret_cast<const float *>(data_of(x)) + x->offset;
+  p.y = reinterpret_cast<float *>(const_cast<char *>(data_of(y))) + y->offset;
+  p.gamma = reinterpret_cast<const float *>(data_of(gamma)) + gamma->offset;
+  p.beta = reinterpret_cast<const float *>(data_of(beta)) + beta->offset;
+  p.mean_sum = mean_sum ? reinterpret_cast<float *>(const_cast<char *>(data_of(mean_sum))) + mean_sum->offset : nullptr;
+  p.rstd = rstd ? reinterpret_cast<float *>(const_cast<char *>(data_of(rstd))) + rstd->offset : nullptr;
+  p.rows = R;
+  p.D = D;
+  p.sx = x->strides[0];
+  p.sy = y->strides[0];
+  p.eps = eps;
+  return launch_layer_norm(p, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_sce_f32(const NovaMemRef2D *logits, const NovaMemRef1D *labels,
+                                      NovaMemRef1D *loss, NovaMemRef2D *softmax) {
+  clear_error();
+  if (!logits || !labels || !loss) return fail(NOVA_HIP_EINVAL, "sce: null descriptor");
+  const int64_t R = logits->sizes[0], C = logits->sizes[1];
+  if (R < 0 || C < 0) return fail(NOVA_HIP_ESHAPE, "sce: negative size");
+  if (labels->sizes[0] != R) return fail(NOVA_HIP_ESHAPE, "sce: labels size != rows");
+  if (loss->sizes[0] != 1) return fail(NOVA_HIP_ESHAPE, "sce: loss must have shape [1]");
+  if (softmax && (softmax->sizes[0] != R || softmax->sizes[1] != C))
+    return fail(NOVA_HIP_ESHAPE, "sce: softmax shape differs from logits");
+  if (C == 0 && R > 0) return fail(NOVA_HIP_ESHAPE, "sce: zero classes");
+  if ((logits->strides[1] != 1 && C > 1) || (labels->strides[0] != 1 && R > 1) ||
+      (softmax && softmax->strides[1] != 1 && C > 1))
+    return fail(NOVA_HIP_ESTRIDE, "sce: last dim must be contiguous");
+  if (R > 1 && (logits->strides[0] < C || (softmax && softmax->strides[0] < C)))
+    return fail(NOVA_HIP_ESTRIDE, "sce: rows overlap");
+  if (!loss->aligned || (R > 0 && (!logits->aligned || !labels->aligned)) ||
+      (softmax && !softmax->aligned))
+    return fail(NOVA_HIP_EINVAL, "sce: null data pointer");
+  SceProblem p;
+  p.logits = reinterpret_cast<const float *>(data_of(logits)) + logits->offset;
+  p.labels = reinterpret_cast<const int32_t *>(data_of(labels)) + labels->offset;
+  p.loss = reinterpret_cast<float *>(const_cast<char *>(data_of(loss))) + loss->offset;
+  p.softmax = softmax ? reinterpret_cast<float *>(const_cast<char *>(data_of(softmax))) + softmax->offset : nullptr;
+  p.rows = R;
+  p.C = C;
+  p.sx = logits->strides[0];
+  p.ssm = softmax ? softmax->strides[0] : 0;
+  return launch_sce(p, current_stream());
+}
+
+void nova_hip_set_stream(void *stream) { t_stream = static_cast<hipStream_t>(stream); }
+
+void *nova_hip_get_stream(void) { return t_stream; }
+
+int32_t nova_hip_synchronize(void) {
+  clear_error();
+  return check_hip(hipStreamSynchronize(t_stream), "synchronize");
+}
+
+const char *nova_hip_last_error(void) { return t_err; }
+
+const char *nova_hip_version(void) { return "libnova_hip 0.1.0 (gfx950)"; }
+
+int32_t nova_hip_release_workspace(void) {
+  clear_error();
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  int32_t rc = NOVA_HIP_SUCCESS;
+  for (auto &kv : g_ws) {
+    if (kv.second.ptr) {
+      hipError_t e = hipStreamSynchronize(kv.first);
+      if (e == hipSuccess) e = hipFree(kv.second.ptr);
+      if (e != hipSuccess) rc = check_hip(e, "release_workspace");
+    }
+  }
+  g_ws.clear();
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,75 @@
+// Internal declarations shared by the libnova_hip translation units.
+// Host-side helpers (validation, error text, stream) and the launcher
+// signatures each kernel file exports to nova_hip_abi.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nova_hip.h"
+
+namespace nova_hip {
+
+// Error text of the calling thread; returns `code` so call sites can write
+// `return fail(NOVA_HIP_ESHAPE, "...")`.
+int32_t fail(int32_t code, const char *fmt, ...);
+void clear_error();
+hipStream_t current_stream();
+// Convert a HIP status into NOVA_HIP_EDEVICE with text, or success.
+int32_t check_hip(hipError_t e, const char *what);
+
+// Element sizes per dtype code.
+inline int dtype_size(int dt) { return dt == NOVA_HIP_DT_F32 ? 4 : 2; }
+
+// ---- GEMM -----------------------------------------------------------------
+// A normalised, validated view of one batched contraction.  Strides in
+// elements.  `a_kcontig` : A's unit stride is on K (else on M).
+// `b_kcontig` : B's unit stride is on K (else on N).
+struct GemmProblem {
+  const void *A;
+  const void *B;
+  void *C;
+  const void *bias;
+  int64_t batch, M, N, K;
+  int64_t sab, sa_outer;  // batch stride; stride of the non-unit dim of A
+  int64_t sbb, sb_outer;  // batch stride; stride of the non-unit dim of B
+  int64_t scb, scm;       // C batch and row strides (unit on N)
+  bool a_kcontig, b_kcontig;
+  int in_dt, out_dt, bias_dt, epi;
+};
+
+// Launch the MFMA kernels (bf16/f16 in).  Returns a NOVA_HIP_* status.
+int32_t launch_gemm_mfma(const GemmProblem &p, hipStream_t s);
+// Launch the exact f32 kernel (f32 in).
+int32_t launch_gemm_f32(const GemmProblem &p, hipStream_t s);
+
+// ---- reductions ------------------------------------------------------------
+struct LayerNormProblem {
+  const float *x;
+  const float *gamma;
+  const float *beta;
+  float *y;
+  float *mean_sum;  // may be null
+  float *rstd;      // may be null
+  int64_t rows, D;
+  int64_t sx, sy;   // row strides (elements)
+  float eps;
+};
+int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s);
+
+struct SceProblem {
+  const float *logits;
+  const int32_t *labels;
+  float *loss;
+  float *softmax;  // may be null
+  int64_t rows, C;
+  int64_t sx, ssm;  // row strides (elements)
+};
+int32_t launch_sce(const SceProblem &p, hipStream_t s);
+
+// Per-stream device workspace owned by the library.  Returns null and sets
+// the error text on failure.  The pointer stays valid until the next call
+// with a larger size on the same stream, or nova_hip_release_workspace().
+void *workspace(hipStream_t s, size_t bytes);
+
+}  // namespace nova_hip

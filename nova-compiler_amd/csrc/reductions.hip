@@ -1,0 +1,334 @@
+// Row reductions for gfx950: nova.layer_norm and nova.sce (softmax
+// cross-entropy with mean loss).  Both are HBM-bound, so neither uses MFMA:
+// rows are streamed with coalesced 16-byte loads, reduced inside one wave64
+// with cross-lane shuffles, and every input byte is read once.
+//
+// The reference GPU pipeline gives these [parallel, reduction] generics one
+// row per thread with row-strided (uncoalesced) loads and a sequential
+// in-thread reduction (NovaKernelConfig.cpp:1585-1760); the CPU pipeline
+// reads x twice for LayerNorm and the logits three times for SCE.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "nova_hip_internal.h"
+
+namespace nova_hip {
+namespace {
+
+constexpr int kWaves = 4;  // rows per 256-thread workgroup
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm.  Per row (NovaLayerNormPattern, NovaToLinalgGeneric.cpp:
+// 1997-2126):  S = sum x, Q = sum x^2; mean = S*invD; var = Q*invD - mean^2;
+// rstd = 1/sqrt(var + eps); y = ((x - mean) * rstd) * gamma + beta.
+// The elementwise part keeps the reference's operation order (no FMA
+// contraction); S and Q are summed lane-wise then across the wave.
+// ---------------------------------------------------------------------------
+struct LnArgs {
+  const float *x;
+  const float *gamma;
+  const float *beta;
+  float *y;
+  float *mean_sum;
+  float *rstd;
+  int64_t sx, sy;
+  int rows, D;
+  float eps, invD;
+};
+
+// Row held in registers: NV f32x4 per lane covers D <= 256 * NV.
+template <int NV>
+__global__ __launch_bounds__(256) void layer_norm_reg_kernel(LnArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int nv4 = a.D >> 2;
+  const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)row * a.sx);
+  f32x4 v[NV];
+  float s = 0.0f, q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = (c < nv4) ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    s = s + v[i].x; s = s + v[i].y; s = s + v[i].z; s = s + v[i].w;
+    q = q + v[i].x * v[i].x; q = q + v[i].y * v[i].y;
+    q = q + v[i].z * v[i].z; q = q + v[i].w * v[i].w;
+  }
+  s = wave_sum(s);
+  q = wave_sum(q);
+  const float mean = s * a.invD;
+  const float sq_mean = q * a.invD;
+  const float mean_sq = mean * mean;
+  const float var = sq_mean - mean_sq;
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  const f32x4 *g4 = reinterpret_cast<const f32x4 *>(a.gamma);
+  const f32x4 *b4 = reinterpret_cast<const f32x4 *>(a.beta);
+  f32x4 *yr = reinterpret_cast<f32x4 *>(a.y + (int64_t)row * a.sy);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nv4) {
+      const f32x4 g = g4[c], b = b4[c];
+      f32x4 o;
+      o.x = ((v[i].x - mean) * rstd) * g.x + b.x;
+      o.y = ((v[i].y - mean) * rstd) * g.y + b.y;
+      o.z = ((v[i].z - mean) * rstd) * g.z + b.z;
+      o.w = ((v[i].w - mean) * rstd) * g.w + b.w;
+      __builtin_nontemporal_store(o, yr + c);
+    }
+  }
+  if (lane == 0) {
+    if (a.mean_sum) a.mean_sum[row] = s;
+    if (a.rstd) a.rstd[row] = rstd;
+  }
+}
+
+// Any D, any alignment: two passes over the row (the second from cache).
+__global__ __launch_bounds__(256) void layer_norm_any_kernel(LnArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const float *xr = a.x + (int64_t)row * a.sx;
+  float s = 0.0f, q = 0.0f;
+  for (int d = lane; d < a.D; d += 64) {
+    const float v = xr[d];
+    s = s + v;
+    q = q + v * v;
+  }
+  s = wave_sum(s);
+  q = wave_sum(q);
+  const float mean = s * a.invD;
+  const float var = q * a.invD - mean * mean;
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  float *yr = a.y + (int64_t)row * a.sy;
+  for (int d = lane; d < a.D; d += 64)
+    yr[d] = ((xr[d] - mean) * rstd) * a.gamma[d] + a.beta[d];
+  if (lane == 0) {
+    if (a.mean_sum) a.mean_sum[row] = s;
+    if (a.rstd) a.rstd[row] = rstd;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax cross-entropy (NovaSceForwardLowering, NovaToLinalgGeneric.cpp:
+// 801-1010) in one pass over the logits: per lane a running (max, sum of
+// exp(x - max)) updated once per 32-value chunk, merged across the wave.
+//   lse = log(max(sum, 1e-7)); loss_r = lse - (x[label] - max);
+// loss = mean over rows with the 64-chunk order of lowerFullReduceMeanToSCF
+// (NovaToLinalg.cpp:1974-2126), done by the last workgroup to finish.
+// ---------------------------------------------------------------------------
+struct SceArgs {
+  const float *logits;
+  const int32_t *labels;
+  float *loss;
+  float *softmax;
+  float *row_loss;      // workspace [rows]
+  unsigned *counter;    // workspace, zero between calls
+  int64_t sx, ssm;
+  int rows, C;
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// exp(x - m) as 2^(x*log2e - m*log2e): one FMA and one v_exp_f32.
+__device__ __forceinline__ float exp_shifted(float x, float m_l2e) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -m_l2e));
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
+  __shared__ bool s_last;
+  __shared__ float s_part[64];
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+
+  if (row < a.rows) {
+    const float *xr = a.logits + (int64_t)row * a.sx;
+    float m = -INFINITY, s = 0.0f;
+    if constexpr (VEC) {
+      const f32x4 *x4 = reinterpret_cast<const f32x4 *>(xr);
+      const int n4 = a.C >> 2;
+      constexpr int U = 8;  // f32x4 per lane per chunk
+      int base = 0;
+      for (; base + 64 * U <= n4; base += 64 * U) {
+        f32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(x4 + base + lane + 64 * u);
+        float cm = m;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          cm = fmaxf(cm, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
+        const float cml = cm * kLog2e;
+        float cs = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          cs += exp_shifted(v[u].x, cml);
+          cs += exp_shifted(v[u].y, cml);
+          cs += exp_shifted(v[u].z, cml);
+          cs += exp_shifted(v[u].w, cml);
+        }
+        s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) + cs;
+        m = cm;
+      }
+      // Tail: remaining f32x4s, then the scalar remainder.
+      for (int c = base + lane; c < n4; c += 64) {
+        const f32x4 v = x4[c];
+        const float cm = fmaxf(m, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+        const float cml = cm * kLog2e;
+        const float cs = exp_shifted(v.x, cml) + exp_shifted(v.y, cml) +
+                         exp_shifted(v.z, cml) + exp_shifted(v.w, cml);
+        s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) + cs;
+        m = cm;
+      }
+      for (int c = (n4 << 2) + lane; c < a.C; c += 64) {
+        const float v = xr[c];
+        const float cm = fmaxf(m, v);
+        s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) +
+            exp_shifted(v, cm * kLog2e);
+        m = cm;
+      }
+    } else {
+      for (int c = lane; c < a.C; c += 64) {
+        const float v = xr[c];
+        const float cm = fmaxf(m, v);
+        s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) +
+            exp_shifted(v, cm * kLog2e);
+        m = cm;
+      }
+    }
+    // Merge lanes: global max, then rescale each lane's sum to it.
+    const float gm = wave_max(m);
+    const float ls = (m == -INFINITY) ? 0.0f : s * __builtin_amdgcn_exp2f((m - gm) * kLog2e);
+    const float gs = wave_sum(ls);
+    const float safe = fmaxf(gs, 1.0e-7f);
+    const float lse = logf(safe);
+    if (a.softmax) {
+      float *sr = a.softmax + (int64_t)row * a.ssm;
+      const float gml = gm * kLog2e;
+      for (int c = lane; c < a.C; c += 64) sr[c] = exp_shifted(xr[c], gml) / safe;
+    }
+    if (lane == 0) {
+      const int t = a.labels[row];
+      float lr;
+      if (t < 0 || t >= a.C) {
+        lr = __builtin_nanf("");
+      } else {
+        const float shifted = xr[t] - gm;
+        lr = lse - shifted;
+      }
+      a.row_loss[row] = lr;
+    }
+  }
+
+  // Last workgroup to arrive computes the mean.
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned ticket = atomicAdd(a.counter, 1u);
+    s_last = (ticket == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const int per = (a.rows + 63) / 64;
+  if (threadIdx.x < 64) {
+    const int start = threadIdx.x * per;
+    const int end = min(start + per, a.rows);
+    float p = 0.0f;
+    for (int i = start; i < end; ++i) p = p + __builtin_nontemporal_load(a.row_loss + i);
+    s_part[threadIdx.x] = p;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float total = 0.0f;
+    for (int i = 0; i < 64; ++i) total = total + s_part[i];
+    a.loss[0] = total / (float)a.rows;
+    *a.counter = 0u;
+  }
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
+  if (p.rows == 0) return NOVA_HIP_SUCCESS;
+  if (p.rows > 0x7fffffff - kWaves || p.D > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "layer_norm: size exceeds 2^31-1");
+  LnArgs a;
+  a.x = p.x;
+  a.gamma = p.gamma;
+  a.beta = p.beta;
+  a.y = p.y;
+  a.mean_sum = p.mean_sum;
+  a.rstd = p.rstd;
+  a.sx = p.sx;
+  a.sy = p.sy;
+  a.rows = (int)p.rows;
+  a.D = (int)p.D;
+  a.eps = p.eps;
+  a.invD = 1.0f / (float)p.D;
+  const unsigned grid = (unsigned)((p.rows + kWaves - 1) / kWaves);
+  const bool vec = (p.D % 4 == 0) && (p.sx % 4 == 0) && (p.sy % 4 == 0) &&
+                   aligned16(p.x) && aligned16(p.y) && aligned16(p.gamma) &&
+                   aligned16(p.beta);
+  if (vec && p.D <= 256 * 4)
+    hipLaunchKernelGGL(layer_norm_reg_kernel<4>, dim3(grid), dim3(256), 0, s, a);
+  else if (vec && p.D <= 256 * 16)
+    hipLaunchKernelGGL(layer_norm_reg_kernel<16>, dim3(grid), dim3(256), 0, s, a);
+  else if (vec && p.D <= 256 * 32)
+    hipLaunchKernelGGL(layer_norm_reg_kernel<32>, dim3(grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(layer_norm_any_kernel, dim3(grid), dim3(256), 0, s, a);
+  return check_hip(hipGetLastError(), "layer_norm launch");
+}
+
+int32_t launch_sce(const SceProblem &p, hipStream_t s) {
+  if (p.rows > 0x7fffffff - kWaves || p.C > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "sce: size exceeds 2^31-1");
+  // Workspace: [0,256) counter (zero between calls), then row losses.
+  char *ws = static_cast<char *>(workspace(s, 256 + (size_t)p.rows * 4));
+  if (!ws) return NOVA_HIP_ENOMEM;
+  SceArgs a;
+  a.logits = p.logits;
+  a.labels = p.labels;
+  a.loss = p.loss;
+  a.softmax = p.softmax;
+  a.counter = reinterpret_cast<unsigned *>(ws);
+  a.row_loss = reinterpret_cast<float *>(ws + 256);
+  a.sx = p.sx;
+  a.ssm = p.ssm;
+  a.rows = (int)p.rows;
+  a.C = (int)p.C;
+  // An empty batch still launches one workgroup: its mean is 0/0 = NaN, as
+  // the reference's division by the element count gives.
+  const unsigned grid = (unsigned)(p.rows > 0 ? (p.rows + kWaves - 1) / kWaves : 1);
+  const bool vec = (p.sx % 4 == 0) && aligned16(p.logits);
+  if (vec)
+    hipLaunchKernelGGL(sce_kernel<true>, dim3(grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(sce_kernel<false>, dim3(grid), dim3(256), 0, s, a);
+  return check_hip(hipGetLastError(), "sce launch");
+}
+
+}  // namespace nova_hip

@@ -1,0 +1,276 @@
+"""Python binding of libnova_hip (the C ABI in include/nova_hip.h).
+
+Mirrors the Nova op surface the GPU path serves -- ``matmul`` (rank 2 and 3,
+i.e. batch matmul), ``linear`` (+ GELU epilogue), ``layer_norm`` and ``sce``
+-- with the reference's result conventions:
+
+* ``layer_norm`` returns ``(y, mean_sum, rstd)``: NovaOps.td:1027-1037 names
+  the results (output, mean_sum, var_sum) and the lowering puts rstd in the
+  third (NovaToLinalgGeneric.cpp:2123).
+* ``sce`` returns ``(softmax, loss)`` with ``loss`` of shape [1]
+  (NovaOps.td:880-896, NovaToLinalgGeneric.cpp:1008).
+
+Tensors are torch tensors on the GPU; each call passes MLIR strided-memref
+descriptors built from the tensors' data pointers, sizes and strides, and
+launches on torch's current stream.  There is no fallback: if the library is
+missing or a call fails, an exception says so.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Tuple
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnova_hip.so")
+
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU = 0, 1, 2, 3
+
+STATUS = {
+    0: "SUCCESS", 1: "EINVAL", 2: "ESHAPE", 3: "ESTRIDE", 4: "EDTYPE",
+    5: "ERANGE", 6: "EDEVICE", 7: "ENOMEM",
+}
+
+# Every symbol include/nova_hip.h declares.
+EXPORTS = (
+    "_mlir_ciface_nova_hip_gemm",
+    "_mlir_ciface_nova_hip_matmul_f32",
+    "_mlir_ciface_nova_hip_batch_matmul_f32",
+    "_mlir_ciface_nova_hip_batch_matmul_bf16_f32",
+    "_mlir_ciface_nova_hip_batch_matmul_f16_f32",
+    "_mlir_ciface_nova_hip_matmul_bf16_f32",
+    "_mlir_ciface_nova_hip_matmul_f16_f32",
+    "_mlir_ciface_nova_hip_linear",
+    "_mlir_ciface_nova_hip_linear_bf16_bias_gelu",
+    "_mlir_ciface_nova_hip_layer_norm_f32",
+    "_mlir_ciface_nova_hip_sce_f32",
+    "nova_hip_set_stream",
+    "nova_hip_get_stream",
+    "nova_hip_synchronize",
+    "nova_hip_last_error",
+    "nova_hip_version",
+    "nova_hip_release_workspace",
+)
+
+
+def gemm_flags(in_dt: int, out_dt: int, epi: int = EPI_NONE, bias_dt: int = 0) -> int:
+    """NOVA_HIP_GEMM_FLAGS of include/nova_hip.h."""
+    return (in_dt & 0xF) | ((out_dt & 0xF) << 4) | ((epi & 0xF) << 8) | ((bias_dt & 0xF) << 12)
+
+
+def _memref_type(rank: int):
+    class MemRef(ctypes.Structure):
+        _fields_ = [
+            ("allocated", ctypes.c_void_p),
+            ("aligned", ctypes.c_void_p),
+            ("offset", ctypes.c_int64),
+            ("sizes", ctypes.c_int64 * rank),
+            ("strides", ctypes.c_int64 * rank),
+        ]
+    MemRef.__name__ = f"NovaMemRef{rank}D"
+    return MemRef
+
+
+MemRef1D = _memref_type(1)
+MemRef2D = _memref_type(2)
+MemRef3D = _memref_type(3)
+_MEMREF = {1: MemRef1D, 2: MemRef2D, 3: MemRef3D}
+
+
+def make_memref(ptr: int, sizes, strides, offset: int = 0):
+    """Descriptor over raw memory (element offsets and strides)."""
+    rank = len(sizes)
+    d = _MEMREF[rank]()
+    d.allocated = ptr
+    d.aligned = ptr
+    d.offset = offset
+    for i in range(rank):
+        d.sizes[i] = int(sizes[i])
+        d.strides[i] = int(strides[i])
+    return d
+
+
+class NovaHipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"libnova_hip {STATUS.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libnova_hip.so (built in-tree by the package Makefile)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `make -C nova-compiler_amd` "
+            "(or __graft_entry__.build()); there is no fallback path")
+    L = ctypes.CDLL(LIB_PATH)
+    P = ctypes.c_void_p
+    for name in EXPORTS:
+        getattr(L, name)  # raises AttributeError if not exported
+    L._mlir_ciface_nova_hip_gemm.argtypes = [P, P, P, P, ctypes.c_int32]
+    L._mlir_ciface_nova_hip_linear.argtypes = [P, P, P, P, ctypes.c_int32]
+    L._mlir_ciface_nova_hip_linear_bf16_bias_gelu.argtypes = [P, P, P, P]
+    for n in ("matmul_f32", "batch_matmul_f32", "batch_matmul_bf16_f32",
+              "batch_matmul_f16_f32", "matmul_bf16_f32", "matmul_f16_f32"):
+        getattr(L, "_mlir_ciface_nova_hip_" + n).argtypes = [P, P, P]
+    L._mlir_ciface_nova_hip_layer_norm_f32.argtypes = [P, P, P, P, P, P, ctypes.c_float]
+    L._mlir_ciface_nova_hip_sce_f32.argtypes = [P, P, P, P]
+    for name in EXPORTS:
+        if name.startswith("_mlir_ciface_"):
+            getattr(L, name).restype = ctypes.c_int32
+    L.nova_hip_set_stream.argtypes = [P]
+    L.nova_hip_set_stream.restype = None
+    L.nova_hip_get_stream.restype = P
+    L.nova_hip_synchronize.restype = ctypes.c_int32
+    L.nova_hip_last_error.restype = ctypes.c_char_p
+    L.nova_hip_version.restype = ctypes.c_char_p
+    L.nova_hip_release_workspace.restype = ctypes.c_int32
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise NovaHipError(rc, lib().nova_hip_last_error().decode())
+
+
+def ref(d) -> Optional[ctypes.c_void_p]:
+    return None if d is None else ctypes.cast(ctypes.pointer(d), ctypes.c_void_p)
+
+
+# --------------------------------------------------------------------------
+# torch-facing wrappers
+# --------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dt(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return DT_F32
+    if t.dtype == torch.bfloat16:
+        return DT_BF16
+    if t.dtype == torch.float16:
+        return DT_F16
+    raise NovaHipError(4, f"unsupported dtype {t.dtype}")
+
+
+def _torch_dtype(dt: int):
+    torch = _torch()
+    return {DT_F32: torch.float32, DT_BF16: torch.bfloat16, DT_F16: torch.float16}[dt]
+
+
+def memref_of(t):
+    """Descriptor of a torch tensor (element strides, offset folded into ptr)."""
+    return make_memref(t.data_ptr(), tuple(t.shape), tuple(t.stride()), 0)
+
+
+def _bind_stream() -> None:
+    torch = _torch()
+    lib().nova_hip_set_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def _as3(t):
+    return t if t.dim() == 3 else t.unsqueeze(0)
+
+
+def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None):
+    """Batched GEMM through _mlir_ciface_nova_hip_gemm.
+
+    A [Bt,M,K] or [M,K]; B [Bt,K,N] or [K,N] (any unit-stride layout,
+    transposed views included); returns C [Bt,M,N] (or [M,N] for rank-2
+    inputs) in ``out_dtype`` (f32 by default).
+    """
+    torch = _torch()
+    in_dt = _dt(A)
+    if _dt(B) != in_dt:
+        raise NovaHipError(4, "A and B must share a dtype")
+    rank2 = A.dim() == 2 and B.dim() == 2
+    A3, B3 = _as3(A), _as3(B)
+    batch = max(A3.shape[0], B3.shape[0])
+    od = DT_F32 if out_dtype is None else _dt(torch.empty(0, dtype=out_dtype))
+    if out is None:
+        out = torch.empty((batch, A3.shape[1], B3.shape[2]), dtype=_torch_dtype(od),
+                          device=A.device)
+        C3 = out
+    else:
+        od = _dt(out)
+        C3 = _as3(out)
+    bias_dt = _dt(bias) if bias is not None else 0
+    flags = gemm_flags(in_dt, od, epilogue, bias_dt)
+    dA, dB, dC = memref_of(A3), memref_of(B3), memref_of(C3)
+    dbias = memref_of(bias) if bias is not None else None
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_gemm(ref(dA), ref(dB), ref(dC), ref(dbias), flags))
+    return out[0] if (rank2 and out.dim() == 3) else out
+
+
+def matmul(A, B, out=None):
+    """nova.matmul (rank 2 or 3) with f32 accumulate and f32 result."""
+    return gemm(A, B, out)
+
+
+def batch_matmul(A, B, out=None):
+    return gemm(A, B, out)
+
+
+def linear(x, weight, bias, *, gelu: bool = False, out_dtype=None):
+    """nova.linear: x [M,K] . weight [K,N] + bias [N] (weight may be a
+    transposed view of a row-major [N,K] tensor), optional GELU(tanh)."""
+    torch = _torch()
+    od = out_dtype if out_dtype is not None else x.dtype
+    y = torch.empty((x.shape[0], weight.shape[1]), dtype=od, device=x.device)
+    epi = EPI_BIAS_GELU if gelu else EPI_BIAS
+    flags = gemm_flags(_dt(x), _dt(y), epi, _dt(bias))
+    dx, dw, db, dy = memref_of(x), memref_of(weight), memref_of(bias), memref_of(y)
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_linear(ref(dx), ref(dw), ref(db), ref(dy), flags))
+    return y
+
+
+def layer_norm(x, gamma, beta, eps: float = 1e-5, *, y=None, mean_sum=None, rstd=None):
+    """nova.layer_norm over the last dim: returns (y, mean_sum, rstd)."""
+    torch = _torch()
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    if y is None:
+        y = torch.empty_like(x2)
+    if mean_sum is None:
+        mean_sum = torch.empty(x2.shape[0], dtype=torch.float32, device=x.device)
+    if rstd is None:
+        rstd = torch.empty(x2.shape[0], dtype=torch.float32, device=x.device)
+    d = [memref_of(t) for t in (x2, gamma, beta, y, mean_sum, rstd)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_layer_norm_f32(*[ref(v) for v in d], ctypes.c_float(eps)))
+    return y.reshape(shape), mean_sum.reshape(shape[:-1]), rstd.reshape(shape[:-1])
+
+
+def sce(logits, labels, *, softmax: bool = False, loss=None):
+    """nova.sce: returns (softmax or None, loss[1])."""
+    torch = _torch()
+    if loss is None:
+        loss = torch.empty(1, dtype=torch.float32, device=logits.device)
+    sm = torch.empty_like(logits) if softmax else None
+    dl, dt, dloss = memref_of(logits), memref_of(labels), memref_of(loss)
+    dsm = memref_of(sm) if sm is not None else None
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_sce_f32(ref(dl), ref(dt), ref(dloss), ref(dsm)))
+    return sm, loss
+
+
+def synchronize() -> None:
+    _bind_stream()
+    check(lib().nova_hip_synchronize())
+
+
+def version() -> str:
+    return lib().nova_hip_version().decode()

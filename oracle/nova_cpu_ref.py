@@ -1,0 +1,157 @@
+"""ctypes binding of the CPU oracle (oracle/nova_cpu_ref.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+bench's cpu_baseline leg, as the checker or the timed CPU baseline.  Never
+used by the product path.  Function semantics and their reference citations
+are documented in nova_cpu_ref.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnova_cpu_ref.so")
+F32, BF16, F16 = 0, 1, 2
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU = 0, 1, 2, 3
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.nova_ref_gemm.argtypes = [P, I, I64, I64, I64, P, I, I64, I64, I64, P, I, I, P, I,
+                                    I64, I64, I64, I64]
+        L.nova_ref_gemm.restype = I
+        L.nova_ref_gemm_sampled.argtypes = [P, I, I64, I64, I64, P, I, I64, I64, I64, P, I, I,
+                                            I, I64, P, I64, P]
+        L.nova_ref_gemm_sampled.restype = I
+        L.nova_ref_gelu_f32.argtypes = [ctypes.c_float]
+        L.nova_ref_gelu_f32.restype = ctypes.c_float
+        L.nova_ref_gelu_array.argtypes = [P, P, I64]
+        L.nova_ref_layer_norm_f32.argtypes = [P, P, P, P, P, P, I64, I64, ctypes.c_float]
+        L.nova_ref_layer_norm_f32.restype = I
+        L.nova_ref_mean_f32.argtypes = [P, I64]
+        L.nova_ref_mean_f32.restype = ctypes.c_float
+        L.nova_ref_sce_f32.argtypes = [P, P, I64, I64, P, P, P]
+        L.nova_ref_sce_f32.restype = I
+        L.nova_ref_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.nova_ref_f32_to_bf16.restype = ctypes.c_uint16
+        L.nova_ref_f32_to_f16.argtypes = [ctypes.c_float]
+        L.nova_ref_f32_to_f16.restype = ctypes.c_uint16
+        L.nova_ref_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.nova_ref_bf16_to_f32.restype = ctypes.c_float
+        L.nova_ref_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.nova_ref_f16_to_f32.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _dtcode(a: np.ndarray, dt: int | None) -> int:
+    if dt is not None:
+        return dt
+    if a.dtype == np.float32:
+        return F32
+    raise ValueError("uint16 arrays need an explicit dtype code (BF16 or F16)")
+
+
+def _strides(a: np.ndarray):
+    return [s // a.itemsize for s in a.strides]
+
+
+def _gemm_args(A, B, adt, bdt):
+    """(A ptr, dt, sab, sam, sak, B ptr, dt, sbb, sbk, sbn, batch, M, N, K) for
+    A [Bt,M,K] / [M,K] and B [Bt,K,N] / [K,N] numpy views (any strides)."""
+    A3 = A if A.ndim == 3 else A[None]
+    B3 = B if B.ndim == 3 else B[None]
+    sa, sb = _strides(A3), _strides(B3)
+    if A3.shape[0] == 1:
+        sa[0] = 0
+    if B3.shape[0] == 1:
+        sb[0] = 0
+    batch = max(A3.shape[0], B3.shape[0])
+    M, K = A3.shape[1], A3.shape[2]
+    N = B3.shape[2]
+    assert B3.shape[1] == K
+    return (A3.ctypes.data, _dtcode(A, adt), sa[0], sa[1], sa[2],
+            B3.ctypes.data, _dtcode(B, bdt), sb[0], sb[1], sb[2], batch, M, N, K)
+
+
+def gemm(A, B, *, adt=None, bdt=None, bias=None, biasdt=None, epilogue=EPI_NONE,
+         cdt=F32) -> np.ndarray:
+    """Reference GEMM; returns C [Bt,M,N] (f32, or uint16 bits for bf16/f16)."""
+    (pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn, batch, M, N, K) = _gemm_args(A, B, adt, bdt)
+    C = np.empty((batch, M, N), dtype=np.float32 if cdt == F32 else np.uint16)
+    pbias = bias.ctypes.data if bias is not None else None
+    bdtc = _dtcode(bias, biasdt) if bias is not None else 0
+    rc = lib().nova_ref_gemm(pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn, pbias, bdtc,
+                             epilogue, C.ctypes.data, cdt, batch, M, N, K)
+    assert rc == 0, rc
+    return C
+
+
+def gemm_sampled(A, B, idx: np.ndarray, *, adt=None, bdt=None, bias=None, biasdt=None,
+                 epilogue=EPI_NONE, cdt=F32) -> np.ndarray:
+    """Reference values at idx[t] = (b, i, j), as f32 (already rounded to cdt)."""
+    (pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn, batch, M, N, K) = _gemm_args(A, B, adt, bdt)
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    out = np.empty(idx.shape[0], dtype=np.float32)
+    pbias = bias.ctypes.data if bias is not None else None
+    bdtc = _dtcode(bias, biasdt) if bias is not None else 0
+    rc = lib().nova_ref_gemm_sampled(pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn, pbias, bdtc,
+                                     epilogue, cdt, K, idx.ctypes.data, idx.shape[0],
+                                     out.ctypes.data)
+    assert rc == 0, rc
+    return out
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().nova_ref_gelu_array(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def layer_norm(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float = 1e-5):
+    """Returns (y, mean_sum, rstd) like nova.layer_norm."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    R, D = x.shape
+    y = np.empty_like(x)
+    s = np.empty(R, dtype=np.float32)
+    r = np.empty(R, dtype=np.float32)
+    g = np.ascontiguousarray(gamma, dtype=np.float32)
+    b = np.ascontiguousarray(beta, dtype=np.float32)
+    rc = lib().nova_ref_layer_norm_f32(x.ctypes.data, g.ctypes.data, b.ctypes.data,
+                                       y.ctypes.data, s.ctypes.data, r.ctypes.data, R, D,
+                                       ctypes.c_float(eps))
+    assert rc == 0
+    return y, s, r
+
+
+def mean(v: np.ndarray) -> np.float32:
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return np.float32(lib().nova_ref_mean_f32(v.ctypes.data, v.size))
+
+
+def sce(logits: np.ndarray, labels: np.ndarray, softmax: bool = False):
+    """Returns (softmax or None, loss[1], per-row loss)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    t = np.ascontiguousarray(labels, dtype=np.int32)
+    R, C = x.shape
+    sm = np.empty_like(x) if softmax else None
+    lr = np.empty(R, dtype=np.float32)
+    loss = np.empty(1, dtype=np.float32)
+    rc = lib().nova_ref_sce_f32(x.ctypes.data, t.ctypes.data, R, C,
+                                sm.ctypes.data if sm is not None else None,
+                                lr.ctypes.data, loss.ctypes.data)
+    if rc == -2:
+        raise ValueError("label outside [0, C)")
+    assert rc == 0
+    return sm, loss, lr

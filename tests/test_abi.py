@@ -1,0 +1,182 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/nova_hip.h declares, and rejects malformed calls with the right
+status code before any HIP call (validation runs on the host first)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import nova_hip as nh
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "nova_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:_mlir_ciface_)?nova_hip_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    declared = header_functions()
+    assert len(declared) >= 15
+    assert sorted(nh.EXPORTS) == declared
+
+
+def test_library_exports_every_declared_symbol():
+    L = nh.lib()
+    for name in header_functions():
+        assert hasattr(L, name), name
+    assert "gfx950" in nh.version()
+
+
+def test_descriptor_layout_matches_mlir():
+    # {ptr, ptr, i64 offset, i64 sizes[R], i64 strides[R]}
+    assert ctypes.sizeof(nh.MemRef1D) == 8 * 5
+    assert ctypes.sizeof(nh.MemRef2D) == 8 * 7
+    assert ctypes.sizeof(nh.MemRef3D) == 8 * 9
+    assert nh.MemRef3D.sizes.offset == 24
+
+
+FAKE = 1 << 40  # never dereferenced: every call below fails validation
+
+
+def d3(sizes, strides=None, ptr=FAKE):
+    if strides is None:
+        strides = (sizes[1] * sizes[2], sizes[2], 1)
+    return nh.make_memref(ptr, sizes, strides)
+
+
+def d2(sizes, strides=None, ptr=FAKE):
+    if strides is None:
+        strides = (sizes[1], 1)
+    return nh.make_memref(ptr, sizes, strides)
+
+
+def d1(n, stride=1, ptr=FAKE):
+    return nh.make_memref(ptr, (n,), (stride,))
+
+
+def gemm_rc(A, B, C, bias=None, flags=None):
+    if flags is None:
+        flags = nh.gemm_flags(nh.DT_BF16, nh.DT_F32)
+    L = nh.lib()
+    return L._mlir_ciface_nova_hip_gemm(nh.ref(A), nh.ref(B), nh.ref(C), nh.ref(bias), flags)
+
+
+def last_error():
+    return nh.lib().nova_hip_last_error().decode()
+
+
+def test_gemm_null_descriptor():
+    L = nh.lib()
+    assert L._mlir_ciface_nova_hip_gemm(None, None, None, None, 0) == 1
+    assert "null" in last_error()
+
+
+def test_gemm_shape_mismatch():
+    assert gemm_rc(d3((2, 8, 16)), d3((2, 15, 8)), d3((2, 8, 8))) == 2
+    assert "disagree" in last_error()
+    assert gemm_rc(d3((3, 8, 16)), d3((2, 16, 8)), d3((2, 8, 8))) == 2
+    assert "broadcast" in last_error()
+
+
+def test_gemm_bad_flags():
+    A, B, C = d3((1, 8, 16)), d3((1, 16, 8)), d3((1, 8, 8))
+    assert gemm_rc(A, B, C, flags=1 << 20) == 1
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(7, 0)) == 4
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_F32, nh.DT_BF16)) == 4
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_BF16, nh.DT_F32, 9)) == 4
+
+
+def test_gemm_bias_required_and_checked():
+    A, B, C = d3((1, 8, 16)), d3((1, 16, 8)), d3((1, 8, 8))
+    f = nh.gemm_flags(nh.DT_BF16, nh.DT_BF16, nh.EPI_BIAS_GELU, nh.DT_BF16)
+    assert gemm_rc(A, B, C, None, f) == 1
+    assert gemm_rc(A, B, C, d1(7), f) == 2
+    assert gemm_rc(A, B, C, d1(8, stride=2), f) == 3
+
+
+def test_gemm_strides_without_unit_dim():
+    A = d3((1, 8, 16), (128, 32, 2))
+    assert gemm_rc(A, d3((1, 16, 8)), d3((1, 8, 8))) == 3
+    B = d3((1, 16, 8), (128, 16, 2))
+    assert gemm_rc(d3((1, 8, 16)), B, d3((1, 8, 8))) == 3
+    C = d3((1, 8, 8), (64, 8, 2))
+    assert gemm_rc(d3((1, 8, 16)), d3((1, 16, 8)), C) == 3
+    C2 = d3((1, 8, 8), (64, 4, 1))  # rows overlap
+    assert gemm_rc(d3((1, 8, 16)), d3((1, 16, 8)), C2) == 3
+
+
+def test_gemm_null_data_pointer():
+    assert gemm_rc(d3((1, 8, 16), ptr=0), d3((1, 16, 8)), d3((1, 8, 8))) == 1
+
+
+def test_gemm_empty_is_a_no_op():
+    # M == 0: nothing to compute, no HIP call is made.
+    assert gemm_rc(d3((1, 0, 16)), d3((1, 16, 8)), d3((1, 0, 8))) == 0
+    assert gemm_rc(d3((0, 8, 16)), d3((0, 16, 8)), d3((0, 8, 8))) == 0
+
+
+def test_typed_entry_points_validate():
+    L = nh.lib()
+    A, B, C = d2((8, 16)), d2((15, 8)), d2((8, 8))
+    for n in ("matmul_f32", "matmul_bf16_f32", "matmul_f16_f32"):
+        assert getattr(L, "_mlir_ciface_nova_hip_" + n)(nh.ref(A), nh.ref(B), nh.ref(C)) == 2
+    A3, B3, C3 = d3((2, 8, 16)), d3((2, 15, 8)), d3((2, 8, 8))
+    for n in ("batch_matmul_f32", "batch_matmul_bf16_f32", "batch_matmul_f16_f32"):
+        assert getattr(L, "_mlir_ciface_nova_hip_" + n)(nh.ref(A3), nh.ref(B3), nh.ref(C3)) == 2
+    assert L._mlir_ciface_nova_hip_linear_bf16_bias_gelu(
+        nh.ref(d2((8, 16))), nh.ref(d2((16, 8))), nh.ref(d1(9)), nh.ref(d2((8, 8)))) == 2
+    assert L._mlir_ciface_nova_hip_linear(
+        nh.ref(d2((8, 16))), nh.ref(d2((16, 8))), nh.ref(d1(8)), nh.ref(d2((8, 8))),
+        nh.gemm_flags(nh.DT_F32, nh.DT_F16, nh.EPI_BIAS)) == 4
+
+
+def ln_rc(x, g, b, y, s=None, r=None, eps=1e-5):
+    L = nh.lib()
+    return L._mlir_ciface_nova_hip_layer_norm_f32(nh.ref(x), nh.ref(g), nh.ref(b), nh.ref(y),
+                                                  nh.ref(s), nh.ref(r), ctypes.c_float(eps))
+
+
+def test_layer_norm_validation():
+    x, y = d2((4, 64)), d2((4, 64))
+    assert ln_rc(None, d1(64), d1(64), y) == 1
+    assert ln_rc(x, d1(63), d1(64), y) == 2
+    assert ln_rc(x, d1(64), d1(64), d2((4, 32))) == 2
+    assert ln_rc(x, d1(64), d1(64), y, d1(3)) == 2
+    assert ln_rc(d2((4, 64), (64, 2)), d1(64), d1(64), y) == 3
+    assert ln_rc(d2((4, 64), (32, 1)), d1(64), d1(64), y) == 3
+    assert ln_rc(d2((4, 0)), d1(0), d1(0), d2((4, 0))) == 2
+    assert ln_rc(d2((0, 64)), d1(64), d1(64), d2((0, 64))) == 0
+
+
+def sce_rc(x, t, loss, sm=None):
+    L = nh.lib()
+    return L._mlir_ciface_nova_hip_sce_f32(nh.ref(x), nh.ref(t), nh.ref(loss), nh.ref(sm))
+
+
+def test_sce_validation():
+    x = d2((4, 10))
+    assert sce_rc(None, d1(4), d1(1)) == 1
+    assert sce_rc(x, d1(3), d1(1)) == 2
+    assert sce_rc(x, d1(4), d1(2)) == 2
+    assert sce_rc(x, d1(4), d1(1), d2((4, 9))) == 2
+    assert sce_rc(d2((4, 10), (10, 2)), d1(4), d1(1)) == 3
+    assert sce_rc(d2((4, 0)), d1(4), d1(1)) == 2
+
+
+def test_error_text_is_per_call():
+    assert gemm_rc(d3((2, 8, 16)), d3((2, 15, 8)), d3((2, 8, 8))) == 2
+    assert last_error()
+    assert gemm_rc(d3((1, 0, 16)), d3((1, 16, 8)), d3((1, 0, 8))) == 0
+    assert last_error() == ""
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(nh, "LIB_PATH", str(tmp_path / "absent.so"))
+    monkeypatch.setattr(nh, "_lib", None)
+    with pytest.raises(ImportError, match="no fallback"):
+        nh.lib()

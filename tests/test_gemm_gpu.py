@@ -1,0 +1,217 @@
+"""GPU parity for the GEMM family (libnova_hip through its C ABI) against the
+CPU oracle on identical seeded inputs.  Small shapes are compared in full,
+the BASELINE configs at full size on a deterministic sample of outputs.
+Bars: f32 bit-exact (same arithmetic as the reference CPU pipeline);
+bf16/f16 with f32 accumulate: |g-c| <= 2e-2|c| + 1e-2."""
+import numpy as np
+import pytest
+
+import nova_cpu_ref as ref
+import nova_hip as nh
+import nova_seed as S
+from conftest import assert_close_f32, assert_close_lp
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(a, dt, dev):
+    import torch
+    if dt == S.F32:
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    t = torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    return t.view(torch.bfloat16 if dt == S.BF16 else torch.float16)
+
+
+def lp_inputs(shape_a, shape_b, dt, seed):
+    na = int(np.prod(shape_a))
+    return (S.uniform(shape_a, seed, dtype=dt), S.uniform(shape_b, seed, dtype=dt, offset=na))
+
+
+def sample_idx(batch, M, N, count, seed):
+    g = np.random.default_rng(seed)
+    idx = np.stack([g.integers(0, batch, count), g.integers(0, M, count),
+                    g.integers(0, N, count)], 1).astype(np.int64)
+    # always include the corners, where edge-tile bugs live
+    corners = np.array([[b, i, j] for b in (0, batch - 1) for i in (0, M - 1) for j in (0, N - 1)],
+                       np.int64)
+    return np.concatenate([corners, idx])
+
+
+def view_as(a_host, layout, dev, dt):
+    """Device tensor with logical shape of a_host ([..., R, C]); layout 'T'
+    stores it transposed (unit stride on the second-to-last dim)."""
+    if layout == "N":
+        return to_dev(a_host, dt, dev)
+    t = to_dev(np.ascontiguousarray(np.swapaxes(a_host, -1, -2)), dt, dev)
+    return t.transpose(-1, -2)
+
+
+SMALL = [(1, 1, 1, 1), (1, 7, 5, 3), (2, 33, 31, 17), (1, 64, 64, 64), (3, 65, 63, 72),
+         (2, 128, 96, 8), (1, 197, 197, 64), (2, 197, 64, 197), (1, 255, 257, 129),
+         (4, 16, 16, 0)]
+
+
+@pytest.mark.parametrize("dt", [S.BF16, S.F16])
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("shape", SMALL)
+def test_gemm_small_shapes(cuda, dt, layout, shape):
+    batch, M, N, K = shape
+    a, b = lp_inputs((batch, M, K), (batch, K, N), dt, seed=11)
+    want = ref.gemm(a, b, adt=dt, bdt=dt)
+    A = view_as(a, layout[0], cuda, dt)
+    B = view_as(b, layout[1], cuda, dt)
+    got = nh.gemm(A, B).cpu().numpy()
+    assert_close_lp(got, want, f"gemm {shape} {layout} dt={dt}")
+
+
+def test_gemm_mfma_lane_layout_exact(cuda):
+    """Integer-grid inputs make bf16 MFMA exact, so any misplaced lane,
+    row or k-chunk shows up as a wrong integer."""
+    g = np.random.default_rng(12)
+    for (batch, M, N, K) in [(1, 64, 64, 64), (2, 100, 72, 136), (64, 256, 256, 64)]:
+        af = g.integers(-4, 5, (batch, M, K)).astype(np.float32)
+        bf = g.integers(-4, 5, (batch, K, N)).astype(np.float32)
+        a, b = S.round_to(af, S.BF16), S.round_to(bf, S.BF16)
+        want = np.einsum("bmk,bkn->bmn", af.astype(np.int64), bf.astype(np.int64))
+        got = nh.gemm(to_dev(a, S.BF16, cuda), to_dev(b, S.BF16, cuda)).cpu().numpy()
+        assert np.array_equal(got, want.astype(np.float32)), (batch, M, N, K)
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN"])
+def test_gemm_big_tile_path(cuda, layout):
+    """>= 256 macro-tiles of 256x256 selects the big-tile kernel; M and N
+    are not multiples of 256, exercising its masked edges."""
+    batch, M, N, K = 64, 500, 504, 136
+    a, b = lp_inputs((batch, M, K), (batch, K, N), S.BF16, seed=13)
+    A = view_as(a, layout[0], cuda, S.BF16)
+    B = view_as(b, layout[1], cuda, S.BF16)
+    got = nh.gemm(A, B).cpu().numpy()
+    idx = sample_idx(batch, M, N, 20000, 14)
+    want = ref.gemm_sampled(a, b, idx, adt=S.BF16, bdt=S.BF16)
+    assert_close_lp(got[idx[:, 0], idx[:, 1], idx[:, 2]], want, f"big tile {layout}")
+
+
+def test_gemm_broadcast_rank2_operand(cuda):
+    """NovaToLinalg.cpp:992-1025: a rank-2 operand broadcasts over the batch."""
+    a, b = lp_inputs((3, 40, 48), (48, 24), S.F16, seed=15)
+    want = ref.gemm(a, b, adt=S.F16, bdt=S.F16)
+    A = to_dev(a, S.F16, cuda)
+    B = to_dev(b, S.F16, cuda).unsqueeze(0).expand(3, 48, 24)
+    got = nh.gemm(A, B).cpu().numpy()
+    assert_close_lp(got, want, "broadcast")
+
+
+@pytest.mark.parametrize("out_dt", [S.F32, S.BF16, S.F16])
+@pytest.mark.parametrize("epi", [nh.EPI_BIAS, nh.EPI_BIAS_GELU, nh.EPI_GELU])
+def test_gemm_epilogues(cuda, out_dt, epi):
+    import torch
+    M, N, K = 70, 90, 200
+    x = S.normal((M, K), 21, dtype=S.BF16)
+    w = S.normal((N, K), 21, 0.0, 0.05, dtype=S.BF16, offset=M * K)
+    bias = S.normal((N,), 21, 0.0, 0.5, dtype=S.BF16, offset=M * K + N * K)
+    want = ref.gemm(x, w.T, adt=S.BF16, bdt=S.BF16, bias=bias, biasdt=S.BF16, epilogue=epi,
+                    cdt=out_dt)
+    want = S.widen(want, out_dt) if out_dt != S.F32 else want
+    od = {S.F32: torch.float32, S.BF16: torch.bfloat16, S.F16: torch.float16}[out_dt]
+    X = to_dev(x, S.BF16, cuda)
+    W = to_dev(w, S.BF16, cuda)
+    Bb = to_dev(bias, S.BF16, cuda)
+    has_bias = epi in (nh.EPI_BIAS, nh.EPI_BIAS_GELU)
+    got = nh.gemm(X, W.t(), bias=Bb if has_bias else None, epilogue=epi, out_dtype=od)
+    assert_close_lp(got.float().cpu().numpy(), want[0], f"epilogue {epi} out {out_dt}")
+
+
+def test_c1_matmul_f32_bit_exact(cuda):
+    """Config 1: nova.matmul f32 A[256,256] @ B[256,256], U[-1,1] seed 0.
+    Same arithmetic as the CPU pipeline -> identical bits."""
+    inp = S.config_inputs("c1")
+    want = ref.gemm(inp["A"], inp["B"])[0]
+    import ctypes
+    import torch
+    A = to_dev(inp["A"], S.F32, cuda)
+    B = to_dev(inp["B"], S.F32, cuda)
+    C = torch.empty(256, 256, device=cuda)
+    dA, dB, dC = nh.memref_of(A), nh.memref_of(B), nh.memref_of(C)
+    nh._bind_stream()
+    nh.check(nh.lib()._mlir_ciface_nova_hip_matmul_f32(nh.ref(dA), nh.ref(dB), nh.ref(dC)))
+    got = C.cpu().numpy()
+    assert np.array_equal(got, want), float(np.abs(got - want).max())
+
+
+def test_f32_gemm_layouts_bias_gelu_bit_exact(cuda):
+    g = np.random.default_rng(16)
+    a = g.uniform(-1, 1, (2, 37, 70)).astype(np.float32)
+    b = g.uniform(-1, 1, (2, 70, 45)).astype(np.float32)
+    bias = g.uniform(-1, 1, 45).astype(np.float32)
+    want = ref.gemm(a, b, bias=bias, epilogue=ref.EPI_BIAS)
+    for layout in ("NN", "TN", "NT", "TT"):
+        A = view_as(a, layout[0], cuda, S.F32)
+        B = view_as(b, layout[1], cuda, S.F32)
+        got = nh.gemm(A, B, bias=to_dev(bias, S.F32, cuda), epilogue=nh.EPI_BIAS).cpu().numpy()
+        assert np.array_equal(got, want), layout
+    # GELU goes through tanhf on both sides: within the f32 bar, not bitwise.
+    want_g = ref.gemm(a, b, bias=bias, epilogue=ref.EPI_BIAS_GELU)
+    got_g = nh.gemm(to_dev(a, S.F32, cuda), to_dev(b, S.F32, cuda), bias=to_dev(bias, S.F32, cuda),
+                    epilogue=nh.EPI_BIAS_GELU).cpu().numpy()
+    assert_close_f32(got_g, want_g, "f32 bias+gelu")
+
+
+def test_wrapper_kat_on_gpu(cuda):
+    """test/wrapper.c:94-100 through the linear entry point, at full size."""
+    import torch
+    n = 4096
+    x = torch.ones(n, n, device=cuda, dtype=torch.bfloat16)
+    w = torch.ones(n, n, device=cuda, dtype=torch.bfloat16)
+    bias = torch.full((n,), 0.5, device=cuda, dtype=torch.float32)
+    y = nh.linear(x, w, bias, out_dtype=torch.float32)
+    assert float((y - 4096.5).abs().max()) < 0.01
+
+
+def test_c2_batch_matmul_bf16_full_size(cuda):
+    """Config 2: linalg.batch_matmul bf16 -> f32, B=8, M=N=K=4096, seed 1."""
+    inp = S.config_inputs("c2")
+    A = to_dev(inp["A"], S.BF16, cuda)
+    B = to_dev(inp["B"], S.BF16, cuda)
+    import ctypes
+    import torch
+    C = torch.empty(8, 4096, 4096, device=cuda)
+    dA, dB, dC = nh.memref_of(A), nh.memref_of(B), nh.memref_of(C)
+    nh._bind_stream()
+    nh.check(nh.lib()._mlir_ciface_nova_hip_batch_matmul_bf16_f32(nh.ref(dA), nh.ref(dB), nh.ref(dC)))
+    idx = sample_idx(8, 4096, 4096, 65536, 17)
+    it = torch.from_numpy(idx).to(cuda)
+    got = C[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy()
+    want = ref.gemm_sampled(inp["A"], inp["B"], idx, adt=S.BF16, bdt=S.BF16)
+    assert_close_lp(got, want, "c2")
+    assert bool(torch.isfinite(C).all())
+
+
+def test_c3_linear_bias_gelu_full_size(cuda):
+    """Config 3: x[4096,4096] . W^T (W [11008,4096]) + b -> GELU(tanh) -> bf16."""
+    import torch
+    inp = S.config_inputs("c3")
+    x = to_dev(inp["x"], S.BF16, cuda)
+    W = to_dev(inp["W"], S.BF16, cuda)
+    b = to_dev(inp["bias"], S.BF16, cuda)
+    y = torch.empty(4096, 11008, device=cuda, dtype=torch.bfloat16)
+    wt = W.t()  # nova.transpose view: [K,N] with strides (1, K)
+    d = [nh.memref_of(t) for t in (x, wt)] + [nh.memref_of(b), nh.memref_of(y)]
+    nh._bind_stream()
+    nh.check(nh.lib()._mlir_ciface_nova_hip_linear_bf16_bias_gelu(*[nh.ref(v) for v in d]))
+    idx = sample_idx(1, 4096, 11008, 65536, 18)
+    it = torch.from_numpy(idx).to(cuda)
+    got = y[it[:, 1], it[:, 2]].float().cpu().numpy()
+    want = ref.gemm_sampled(inp["x"], inp["W"].T, idx, adt=S.BF16, bdt=S.BF16, bias=inp["bias"],
+                            biasdt=S.BF16, epilogue=ref.EPI_BIAS_GELU, cdt=S.BF16)
+    assert_close_lp(got, want, "c3")
+
+
+@pytest.mark.parametrize("cfg", ["c4a", "c4b"])
+def test_c4_fp16_unaligned_full(cuda, cfg):
+    """Config 4: fp16 batch GEMM with non-tile-aligned shapes (edge tiles)."""
+    inp = S.config_inputs(cfg)
+    want = ref.gemm(inp["A"], inp["B"], adt=S.F16, bdt=S.F16)
+    A = to_dev(inp["A"], S.F16, cuda)
+    B = to_dev(inp["B"], S.F16, cuda)
+    got = nh.batch_matmul(A, B).cpu().numpy()
+    assert_close_lp(got, want, cfg)

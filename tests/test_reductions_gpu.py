@@ -1,0 +1,131 @@
+"""GPU parity for nova.layer_norm and nova.sce (libnova_hip through its C
+ABI) against the CPU oracle on identical seeded inputs, full size for
+config 5, plus the edge cases: ragged / unaligned widths, strided rows,
+single rows, empty batches, out-of-range labels.  Bar: f32, rtol 1e-4 with
+a normwise atol of 1e-4 * max|c|."""
+import math
+
+import numpy as np
+import pytest
+
+import nova_cpu_ref as ref
+import nova_hip as nh
+import nova_seed as S
+from conftest import assert_close_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, cuda):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def check_ln(x, g, b, cuda, what):
+    y_ref, s_ref, r_ref = ref.layer_norm(x, g, b)
+    y, s, r = nh.layer_norm(dev(x, cuda), dev(g, cuda), dev(b, cuda))
+    assert_close_f32(y.cpu().numpy(), y_ref, what + " y")
+    assert_close_f32(s.cpu().numpy(), s_ref, what + " mean_sum")
+    assert_close_f32(r.cpu().numpy(), r_ref, what + " rstd")
+
+
+@pytest.mark.parametrize("rows,D", [(1, 1), (3, 3), (5, 64), (7, 1000), (33, 1024),
+                                    (9, 4096), (4, 5000), (2, 9000), (130, 257)])
+def test_layer_norm_shapes(cuda, rows, D):
+    x = S.normal((rows, D), 31)
+    g = (1 + S.normal((D,), 31, 0, 0.1, offset=rows * D)).astype(np.float32)
+    b = S.normal((D,), 31, 0, 0.1, offset=rows * D + D)
+    check_ln(x, g, b, cuda, f"ln {rows}x{D}")
+
+
+def test_layer_norm_strided_rows(cuda):
+    import torch
+    wide = S.normal((16, 1200), 32)
+    x = dev(wide, cuda)[:, 100:1124]  # row stride 1200, offset 100
+    g = dev(np.ones(1024, np.float32), cuda)
+    b = dev(np.zeros(1024, np.float32), cuda)
+    y, s, r = nh.layer_norm(x, g, b)
+    y_ref, s_ref, r_ref = ref.layer_norm(wide[:, 100:1124], np.ones(1024, np.float32),
+                                         np.zeros(1024, np.float32))
+    assert_close_f32(y.cpu().numpy(), y_ref, "strided y")
+    assert_close_f32(r.cpu().numpy(), r_ref, "strided rstd")
+
+
+def test_layer_norm_constant_rows_give_beta(cuda):
+    x = np.full((8, 4096), 3.0, np.float32)
+    g = S.normal((4096,), 33)
+    b = S.normal((4096,), 33, offset=4096)
+    y, s, r = nh.layer_norm(dev(x, cuda), dev(g, cuda), dev(b, cuda))
+    assert np.array_equal(y.cpu().numpy(), np.broadcast_to(b, (8, 4096)))
+    assert np.allclose(r.cpu().numpy(), 1 / math.sqrt(1e-5), rtol=1e-6)
+
+
+def test_c5_layer_norm_full_size(cuda):
+    inp = S.config_inputs("c5_ln")
+    check_ln(inp["x"], inp["gamma"], inp["beta"], cuda, "c5 ln")
+
+
+def check_sce(x, t, cuda, what, softmax=False):
+    sm_ref, loss_ref, _ = ref.sce(x, t, softmax=softmax)
+    sm, loss = nh.sce(dev(x, cuda), dev(t, cuda), softmax=softmax)
+    assert_close_f32(loss.cpu().numpy(), loss_ref, what + " loss")
+    if softmax:
+        assert_close_f32(sm.cpu().numpy(), sm_ref, what + " softmax")
+
+
+@pytest.mark.parametrize("rows,C", [(1, 1), (1, 3), (5, 10), (64, 1000), (65, 2049),
+                                    (130, 4096), (7, 32000), (200, 333)])
+def test_sce_shapes(cuda, rows, C):
+    x = S.normal((rows, C), 41, 0, 2)
+    t = S.labels(rows, C, 41, offset=2 * rows * C)
+    check_sce(x, t, cuda, f"sce {rows}x{C}", softmax=(rows * C <= 1 << 20))
+
+
+def test_sce_closed_forms_on_gpu(cuda):
+    x = np.zeros((100, 5000), np.float32)
+    t = (np.arange(100) * 37 % 5000).astype(np.int32)
+    _, loss = nh.sce(dev(x, cuda), dev(t, cuda))
+    assert abs(float(loss.cpu()[0]) - math.log(5000)) < 1e-4 * math.log(5000)
+    x[np.arange(100), t] = 80.0
+    _, loss = nh.sce(dev(x, cuda), dev(t, cuda))
+    assert 0 <= float(loss.cpu()[0]) < 1e-5
+
+
+def test_sce_repeat_calls_identical(cuda):
+    """The last-workgroup mean restores its arrival counter: back-to-back
+    calls (and a smaller second call) give identical, correct results."""
+    x = S.normal((300, 777), 42, 0, 2)
+    t = S.labels(300, 777, 42, offset=2 * 300 * 777)
+    X, T = dev(x, cuda), dev(t, cuda)
+    _, l1 = nh.sce(X, T)
+    _, l2 = nh.sce(X, T)
+    _, l3 = nh.sce(X[:17], T[:17])
+    _, ref17, _ = ref.sce(x[:17], t[:17])
+    assert float(l1.cpu()[0]) == float(l2.cpu()[0])
+    assert_close_f32(l3.cpu().numpy(), ref17, "second, smaller call")
+
+
+def test_sce_strided_rows(cuda):
+    wide = S.normal((40, 600), 43, 0, 2)
+    t = S.labels(40, 500, 43, offset=2 * 40 * 600)
+    X = dev(wide, cuda)[:, 3:503]
+    _, loss = nh.sce(X, dev(t, cuda))
+    _, loss_ref, _ = ref.sce(wide[:, 3:503], t)
+    assert_close_f32(loss.cpu().numpy(), loss_ref, "strided sce")
+
+
+def test_sce_empty_batch_and_bad_label_give_nan(cuda):
+    import torch
+    x = torch.zeros(0, 10, device=cuda)
+    t = torch.zeros(0, dtype=torch.int32, device=cuda)
+    _, loss = nh.sce(x, t)
+    assert math.isnan(float(loss.cpu()[0]))
+    x = dev(S.normal((4, 10), 44), cuda)
+    t = dev(np.array([1, 2, 10, 3], np.int32), cuda)
+    _, loss = nh.sce(x, t)
+    assert math.isnan(float(loss.cpu()[0]))
+
+
+def test_c5_sce_full_size(cuda):
+    inp = S.config_inputs("c5_sce")
+    check_sce(inp["logits"], inp["labels"], cuda, "c5 sce")
