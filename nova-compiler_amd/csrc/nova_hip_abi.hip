@@ -138,7 +138,9 @@ int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
     if (bias->strides[0] != 1 && N > 1) return fail(NOVA_HIP_ESTRIDE, "gemm: bias must be contiguous");
   }
   const bool empty = batch == 0 || M == 0 || N == 0;
-  if (!empty && (!A->aligned || !B->aligned || !C->aligned))
+  // With K == 0 the operands hold no elements (their data pointer may be
+  // null) and C is just the epilogue of a zero accumulator.
+  if (!empty && (!C->aligned || (K > 0 && (!A->aligned || !B->aligned))))
     return fail(NOVA_HIP_EINVAL, "gemm: null data pointer");
 
   GemmProblem p;

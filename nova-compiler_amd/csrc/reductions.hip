@@ -150,9 +150,10 @@ struct SceArgs {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// exp(x - m) as 2^(x*log2e - m*log2e): one FMA and one v_exp_f32.
-__device__ __forceinline__ float exp_shifted(float x, float m_l2e) {
-  return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -m_l2e));
+// exp(x - m) as 2^((x - m) * log2e) on v_exp_f32.  The subtraction comes
+// first, as in the reference (subf then math.exp), so x == m gives exactly 1.
+__device__ __forceinline__ float exp_shifted(float x, float m) {
+  return __builtin_amdgcn_exp2f((x - m) * kLog2e);
 }
 
 template <bool VEC>
@@ -178,14 +179,13 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
           cm = fmaxf(cm, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
-        const float cml = cm * kLog2e;
         float cs = 0.0f;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          cs += exp_shifted(v[u].x, cml);
-          cs += exp_shifted(v[u].y, cml);
-          cs += exp_shifted(v[u].z, cml);
-          cs += exp_shifted(v[u].w, cml);
+          cs += exp_shifted(v[u].x, cm);
+          cs += exp_shifted(v[u].y, cm);
+          cs += exp_shifted(v[u].z, cm);
+          cs += exp_shifted(v[u].w, cm);
         }
         s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) + cs;
         m = cm;
@@ -194,9 +194,8 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
       for (int c = base + lane; c < n4; c += 64) {
         const f32x4 v = x4[c];
         const float cm = fmaxf(m, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
-        const float cml = cm * kLog2e;
-        const float cs = exp_shifted(v.x, cml) + exp_shifted(v.y, cml) +
-                         exp_shifted(v.z, cml) + exp_shifted(v.w, cml);
+        const float cs = exp_shifted(v.x, cm) + exp_shifted(v.y, cm) +
+                         exp_shifted(v.z, cm) + exp_shifted(v.w, cm);
         s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) + cs;
         m = cm;
       }
@@ -204,7 +203,7 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
         const float v = xr[c];
         const float cm = fmaxf(m, v);
         s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) +
-            exp_shifted(v, cm * kLog2e);
+            exp_shifted(v, cm);
         m = cm;
       }
     } else {
@@ -212,7 +211,7 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
         const float v = xr[c];
         const float cm = fmaxf(m, v);
         s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - cm) * kLog2e)) +
-            exp_shifted(v, cm * kLog2e);
+            exp_shifted(v, cm);
         m = cm;
       }
     }
@@ -224,8 +223,7 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
     const float lse = logf(safe);
     if (a.softmax) {
       float *sr = a.softmax + (int64_t)row * a.ssm;
-      const float gml = gm * kLog2e;
-      for (int c = lane; c < a.C; c += 64) sr[c] = exp_shifted(xr[c], gml) / safe;
+      for (int c = lane; c < a.C; c += 64) sr[c] = exp_shifted(xr[c], gm) / safe;
     }
     if (lane == 0) {
       const int t = a.labels[row];
