@@ -1,0 +1,250 @@
+// Device-side pieces shared by the two MFMA GEMM kernels (register-staged,
+// gemm_mfma.hip; LDS-DMA, gemm_dma.hip): argument block, MFMA wrapper,
+// buffer resources, XCD-aware tile order and the bias / GELU / store
+// epilogue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "nova_hip_internal.h"
+
+namespace nova_hip {
+namespace gemm {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;          // four wave64s in a 2x2 grid
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset beyond every range
+
+struct GemmArgs {
+  const uint16_t *A;
+  const uint16_t *B;
+  void *C;
+  const void *bias;
+  int64_t sab, sa_outer;
+  int64_t sbb, sb_outer;
+  int64_t scb, scm;
+  uint32_t a_bytes, b_bytes;  // byte extent of one batch slice of A / B
+  int M, N, K;
+  int tiles_m, tiles_n, batch;
+  int out_dt, bias_dt, epi;
+};
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == NOVA_HIP_DT_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Raw buffer over `bytes` bytes at p: loads at offsets >= bytes return zero
+// without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ float bias_at(const void *bias, int dt, int n) {
+  if (dt == NOVA_HIP_DT_F32) return static_cast<const float *>(bias)[n];
+  const uint16_t h = static_cast<const uint16_t *>(bias)[n];
+  if (dt == NOVA_HIP_DT_BF16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), in the operation
+// order of NovaGeluForwardPattern (NovaToLinalgGeneric.cpp:1310-1331).
+__device__ __forceinline__ float gelu_tanh(float x) {
+#pragma clang fp contract(off)
+  const float x2 = x * x;
+  const float x3 = x2 * x;
+  const float cubic = 4.471500e-02f * x3;
+  const float inner = x + cubic;
+  const float scaled = 0.7978845608028654f * inner;
+  const float t = tanhf(scaled);
+  return (0.5f * x) * (1.0f + t);
+}
+
+// GELU with tanh from the hardware exponential and reciprocal,
+// tanh(s) = 1 - 2 / (1 + e^(2s)) (exact limits +-1 at overflow / underflow
+// of e^(2s)); the polynomial part keeps the reference's f32 operation order
+// (NovaToLinalgGeneric.cpp:1310-1331).  Absolute error of tanh ~1e-7, far
+// inside the bf16 output rounding.
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+#pragma clang fp contract(off)
+  const float x2 = x * x;
+  const float x3 = x2 * x;
+  const float cubic = 4.471500e-02f * x3;
+  const float inner = x + cubic;
+  const float scaled = 0.7978845608028654f * inner;
+  const float e = __builtin_amdgcn_exp2f(scaled * 2.8853900817779268f);  // e^(2s)
+  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return (0.5f * x) * (1.0f + t);
+}
+
+__device__ __forceinline__ uint16_t to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Map the linear workgroup id to (batch, tile_m, tile_n), wave-uniform.
+__device__ __forceinline__ void tile_of(int id, const GemmArgs &a, int &b, int &tm, int &tn) {
+  const int total = a.batch * a.tiles_m * a.tiles_n;
+  // Hardware hands consecutive workgroup ids to the 8 XCDs round robin;
+  // renumber so each XCD sees one contiguous range of tiles.
+  if ((total & 7) == 0) {
+    const int per_xcd = total >> 3;
+    id = (id & 7) * per_xcd + (id >> 3);
+  }
+  const int per_batch = a.tiles_m * a.tiles_n;
+  b = id / per_batch;
+  int t = id - b * per_batch;
+  // Group 4 tile-rows: consecutive ids sweep a 4-row band column by column.
+  constexpr int G = 4;
+  const int band = t / (G * a.tiles_n);
+  const int first = band * G;
+  const int gsz = min(a.tiles_m - first, G);
+  const int in_band = t - band * G * a.tiles_n;
+  tm = first + in_band % gsz;
+  tn = in_band / gsz;
+  b = __builtin_amdgcn_readfirstlane(b);
+  tm = __builtin_amdgcn_readfirstlane(tm);
+  tn = __builtin_amdgcn_readfirstlane(tn);
+}
+
+// Epilogue for a wave's TM x TN grid of 32x32 accumulator tiles whose
+// top-left output is (mw, nw) in batch bidx.  Accumulator element v of lane
+// l sits at row 8*(v/4) + 4*(l/32) + v%4, column l%32 of its tile.
+template <int TM, int TN>
+__device__ __forceinline__ void store_outputs(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                              int bidx, int mw, int nw, int lane) {
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  char *Cb = static_cast<char *>(a.C) +
+             (int64_t)bidx * a.scb * (a.out_dt == NOVA_HIP_DT_F32 ? 4 : 2);
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = nw + j * 32 + lrow;
+    if (n >= a.N) continue;
+    const float bv = has_bias ? bias_at(a.bias, a.bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = mw + i * 32 + 8 * (v >> 2) + 4 * lhalf + (v & 3);
+        if (m >= a.M) continue;
+        float x = acc[i][j][v];
+        if (has_bias) x = x + bv;
+        if (has_gelu) x = gelu_tanh(x);
+        const int64_t off = (int64_t)m * a.scm + n;
+        if (a.out_dt == NOVA_HIP_DT_F32)
+          reinterpret_cast<float *>(Cb)[off] = x;
+        else if (a.out_dt == NOVA_HIP_DT_BF16)
+          reinterpret_cast<uint16_t *>(Cb)[off] = to_bf16(x);
+        else
+          reinterpret_cast<uint16_t *>(Cb)[off] = to_f16(x);
+      }
+    }
+  }
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Epilogue for full tiles when the MFMAs were issued with B as the first
+// operand, so acc[i][j] holds the 32x32 output tile transposed: lane l owns
+// output row (l % 32) and, for g = 0..3, the four consecutive columns
+// 8g + 4(l/32) + 0..3 in elements v = 4g .. 4g+3.  Every output is one 16-byte
+// (f32) or 8-byte (bf16/f16) store; no bounds checks (full tiles only).
+template <int TM, int TN, int ODT, int EPI>
+__device__ __forceinline__ void store_full_t(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                             int bidx, int mw, int nw, int lane) {
+  constexpr bool kBias = (EPI == NOVA_HIP_EPI_BIAS || EPI == NOVA_HIP_EPI_BIAS_GELU);
+  constexpr bool kGelu = (EPI == NOVA_HIP_EPI_BIAS_GELU || EPI == NOVA_HIP_EPI_GELU);
+  constexpr int kEsz = ODT == NOVA_HIP_DT_F32 ? 4 : 2;
+  const int lr = lane & 31, lh = lane >> 5;
+  f32x4 bias[TN][4];
+  if constexpr (kBias) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = nw + 32 * j + 8 * g + 4 * lh;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bias[j][g][e] = bias_at(a.bias, a.bias_dt, n + e);
+      }
+  }
+  char *Cb = static_cast<char *>(a.C) + (int64_t)bidx * a.scb * kEsz;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    char *row = Cb + ((int64_t)(mw + 32 * i + lr) * a.scm + nw + 4 * lh) * kEsz;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                   acc[i][j][4 * g + 3]};
+        if constexpr (kBias) x = x + bias[j][g];
+        if constexpr (kGelu) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = gelu_tanh_fast(x[e]);
+        }
+        char *dst = row + (32 * j + 8 * g) * kEsz;
+        if constexpr (ODT == NOVA_HIP_DT_F32) {
+          *reinterpret_cast<f32x4 *>(dst) = x;
+        } else if constexpr (ODT == NOVA_HIP_DT_BF16) {
+          *reinterpret_cast<u32x2 *>(dst) =
+              u32x2{to_bf16(x[0]) | ((uint32_t)to_bf16(x[1]) << 16),
+                    to_bf16(x[2]) | ((uint32_t)to_bf16(x[3]) << 16)};
+        } else {
+          *reinterpret_cast<u32x2 *>(dst) =
+              u32x2{to_f16(x[0]) | ((uint32_t)to_f16(x[1]) << 16),
+                    to_f16(x[2]) | ((uint32_t)to_f16(x[3]) << 16)};
+        }
+      }
+  }
+}
+
+// Runtime (output dtype, epilogue) -> one compact specialisation.
+template <int TM, int TN>
+__device__ __forceinline__ void store_full(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                           int bidx, int mw, int nw, int lane) {
+  switch (a.out_dt * 4 + a.epi) {
+#define NOVA_EPI_CASE(O, E) \
+  case O * 4 + E:           \
+    store_full_t<TM, TN, O, E>(acc, a, bidx, mw, nw, lane); \
+    break;
+    NOVA_EPI_CASE(0, 0) NOVA_EPI_CASE(0, 1) NOVA_EPI_CASE(0, 2) NOVA_EPI_CASE(0, 3)
+    NOVA_EPI_CASE(1, 0) NOVA_EPI_CASE(1, 1) NOVA_EPI_CASE(1, 2) NOVA_EPI_CASE(1, 3)
+    NOVA_EPI_CASE(2, 0) NOVA_EPI_CASE(2, 1) NOVA_EPI_CASE(2, 2) NOVA_EPI_CASE(2, 3)
+#undef NOVA_EPI_CASE
+    default:
+      break;
+  }
+}
+
+}  // namespace gemm
+
+// Launchers (host).  launch_gemm_dma returns NOVA_HIP_EDTYPE when the
+// problem is not one the DMA kernel addresses (the caller then uses the
+// register-staged kernel).
+bool gemm_dma_applicable(const gemm::GemmArgs &a, bool akc, bool bkc, bool vec);
+int32_t launch_gemm_dma(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc, hipStream_t s);
+
+}  // namespace nova_hip

@@ -4,114 +4,87 @@
 // Replaces the NVPTX code generation of nova-gpu-optimized-pipeline for
 // linalg.matmul / linalg.batch_matmul (lib/Transforms/LLVMGPU/Passes.cpp:
 // 115-372: tile+distribute, pad, promote to shared memory, mma.sync,
-// 3-stage cp.async).  Designed for CDNA4 instead:
-//   * macro-tile BM x BN x 64, four wave64s in a 2x2 grid, each wave owning
-//     (BM/2) x (BN/2) of the output as 32x32 v_mfma_f32_32x32x16_{bf16,f16}
-//     tiles held in accumulation registers;
-//   * operands staged through LDS, two stages (double buffer): global loads
-//     of stage k+1 are in flight while stage k feeds the MFMAs;
-//   * LDS holds both operands K-contiguous ([rows][64] per stage) with the
-//     16-byte chunk index XOR-swizzled by (row & 7), so the ds_read_b128 of
-//     eight consecutive rows and the ds_write_b128 of one row's eight chunks
-//     hit distinct banks;
-//   * an operand whose unit stride is on M or N (B of a row-major [K,N]
-//     matrix, A of a transposed view) is fetched as 8x8 blocks and
-//     transposed in registers before the LDS write;
-//   * edge tiles (M, N, K not multiples of the tile) are zero-padded at
-//     load time and masked at store time -- the role of NovaGPUPadOperands;
-//   * workgroups are renumbered so the 1/8 of the grid that the hardware
-//     dispatches to one XCD is one contiguous, tile-row-grouped range (its
-//     own L2 then serves the operand re-reads).
-#include <hip/hip_runtime.h>
-#include <math.h>
-#include <stdint.h>
-
-#include "nova_hip_internal.h"
+// 3-stage cp.async).  Two kernels, chosen per problem by launch_gemm_mfma:
+//
+//  * gemm_dma.hip -- aligned problems made of whole 256x256x32 tiles (the
+//    large configs): operands go global -> LDS by DMA, four stages deep.
+//  * this file -- every other shape: register-staged loads, two LDS stages.
+//    Macro-tile BM x BN x 64, four wave64s in a 2x2 grid, each owning
+//    (BM/2) x (BN/2) of the output as 32x32 v_mfma_f32_32x32x16 tiles.
+//    LDS holds both operands K-contiguous ([rows][64] per stage) with the
+//    16-byte chunk index XOR-swizzled by row, so the ds_read_b128 of
+//    consecutive rows and the ds_write_b128 of one row's eight chunks hit
+//    distinct banks.  An operand whose unit stride is on M or N is
+//    fetched as 8x8 blocks and transposed in registers before the LDS
+//    write.  Edge tiles are zero-padded at load time (buffer loads outside
+//    the operand's range return zero) and masked at store time -- the role
+//    of NovaGPUPadOperands.
+#include "gemm_common.h"
 
 namespace nova_hip {
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+using namespace gemm;
 
-constexpr int kBK = 64;        // K per LDS stage
-constexpr int kThreads = 256;  // four wave64s
+constexpr int kBK = 64;  // K per LDS stage
 
-struct GemmArgs {
-  const uint16_t *A;
-  const uint16_t *B;
-  void *C;
-  const void *bias;
-  int64_t sab, sa_outer;
-  int64_t sbb, sb_outer;
-  int64_t scb, scm;
-  int M, N, K;
-  int tiles_m, tiles_n, batch;
-  int out_dt, bias_dt, epi;
-};
-
-template <int DT>
-__device__ __forceinline__ f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (DT == NOVA_HIP_DT_BF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
-        0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
-        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-        0);
-  }
-}
-
-// LDS chunk slot of (row, 16-byte chunk c) inside one operand stage.
+// LDS chunk slot of (row, 16-byte chunk c) inside one operand stage.  The
+// XOR by (row ^ row/8) keeps both 8 and 16 consecutive rows of a
+// ds_read_b128 on distinct banks (LDS serving 8 or 16 lanes per cycle).
 __device__ __forceinline__ int lds_slot(int row, int c) {
-  return row * 8 + (c ^ (row & 7));
+  return row * 8 + (c ^ ((row ^ (row >> 3)) & 7));
 }
 
 // ---------------------------------------------------------------------------
-// Tile loaders.  An operand tile is R rows (M for A, N for B) x 64 k.
+// Tile loaders.  An operand tile is R rows (M for A, N for B) x 64 k, read
+// through a buffer resource whose range covers the operand's batch slice:
+// any load outside it (edge rows, k past K, whole tiles past the end of the
+// K loop) returns zeros without touching memory, so edges need no branches.
 //   KC  : the operand's unit stride is on K.
-//   VEC : 16-byte global loads are legal (aligned base, outer stride % 8 == 0,
-//         K % 8 == 0 for KC; rows % 8 == 0 for !KC).  Otherwise elements are
-//         fetched one by one.
-// Registers: NREG chunks per thread.
+//   VEC : 16-byte loads are legal (16-byte aligned rows and chunks).
+//         Otherwise elements are fetched one by one (2-byte buffer loads).
 // ---------------------------------------------------------------------------
 template <int R, bool KC>
 struct TileShape {
-  // KC: R*8 chunks over 256 threads.  !KC: R/8*8 blocks of 8x8, one block
+  // KC: R*8 chunks over 256 threads.  !KC: R blocks of 8x8, one block
   // (8 chunks) per participating thread.
-  static constexpr int kBlocks = KC ? 0 : (R / 8) * 8;
+  static constexpr int kBlocks = KC ? 0 : R;
   static constexpr int kBlockIters = KC ? 0 : (kBlocks + kThreads - 1) / kThreads;
   static constexpr int NREG = KC ? (R * 8) / kThreads : 8 * kBlockIters;
 };
 
+struct Operand {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int64_t s_outer;  // elements
+  int row0, rows, K;
+};
+
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
 template <int R, bool KC, bool VEC>
-__device__ __forceinline__ void load_tile(u32x4 *reg, const uint16_t *base,
-                                          int64_t s_outer, int row0, int rows,
-                                          int k0, int K, int tid) {
+__device__ __forceinline__ void load_tile(u32x4 *reg, const Operand &o, int k0, int tid) {
   if constexpr (KC) {
 #pragma unroll
     for (int i = 0; i < TileShape<R, KC>::NREG; ++i) {
       const int q = tid + i * kThreads;
       const int r = q >> 3, c = q & 7;
-      const int gr = row0 + r, gk = k0 + c * 8;
+      const int gr = o.row0 + r, gk = k0 + c * 8;
+      const uint32_t base = (uint32_t)(((int64_t)gr * o.s_outer + gk) * 2);
       if constexpr (VEC) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (gr < rows && gk < K)
-          v = *reinterpret_cast<const u32x4 *>(base + (int64_t)gr * s_outer + gk);
-        reg[i] = v;
+        reg[i] = load16(o.rsrc, (gr < o.rows && gk < o.K) ? base : kOOB);
       } else {
         uint32_t w[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          uint32_t lo = 0, hi = 0;
-          if (gr < rows) {
-            const uint16_t *p = base + (int64_t)gr * s_outer;
-            if (gk + 2 * e < K) lo = p[gk + 2 * e];
-            if (gk + 2 * e + 1 < K) hi = p[gk + 2 * e + 1];
-          }
+          const bool rok = gr < o.rows;
+          const uint32_t lo = load2(o.rsrc, (rok && gk + 2 * e < o.K) ? base + 4 * e : kOOB);
+          const uint32_t hi = load2(o.rsrc, (rok && gk + 2 * e + 1 < o.K) ? base + 4 * e + 2 : kOOB);
           w[e] = lo | (hi << 16);
         }
         reg[i] = u32x4{w[0], w[1], w[2], w[3]};
@@ -124,25 +97,21 @@ __device__ __forceinline__ void load_tile(u32x4 *reg, const uint16_t *base,
     for (int it = 0; it < TileShape<R, KC>::kBlockIters; ++it) {
       const int q = tid + it * kThreads;
       const int kb = q & 7, rb = q >> 3;
-      const int gr = row0 + rb * 8;
+      const int gr = o.row0 + rb * 8;
+      const bool qok = q < TileShape<R, KC>::kBlocks;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int gk = k0 + kb * 8 + j;
+        const uint32_t base = (uint32_t)(((int64_t)gk * o.s_outer + gr) * 2);
         if constexpr (VEC) {
-          u32x4 v = {0u, 0u, 0u, 0u};
-          if (q < TileShape<R, KC>::kBlocks && gk < K && gr < rows)
-            v = *reinterpret_cast<const u32x4 *>(base + (int64_t)gk * s_outer + gr);
-          reg[it * 8 + j] = v;
+          reg[it * 8 + j] = load16(o.rsrc, (qok && gk < o.K && gr < o.rows) ? base : kOOB);
         } else {
           uint32_t w[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            uint32_t lo = 0, hi = 0;
-            if (q < TileShape<R, KC>::kBlocks && gk < K) {
-              const uint16_t *p = base + (int64_t)gk * s_outer;
-              if (gr + 2 * e < rows) lo = p[gr + 2 * e];
-              if (gr + 2 * e + 1 < rows) hi = p[gr + 2 * e + 1];
-            }
+            const bool kok = qok && gk < o.K;
+            const uint32_t lo = load2(o.rsrc, (kok && gr + 2 * e < o.rows) ? base + 4 * e : kOOB);
+            const uint32_t hi = load2(o.rsrc, (kok && gr + 2 * e + 1 < o.rows) ? base + 4 * e + 2 : kOOB);
             w[e] = lo | (hi << 16);
           }
           reg[it * 8 + j] = u32x4{w[0], w[1], w[2], w[3]};
@@ -153,8 +122,7 @@ __device__ __forceinline__ void load_tile(u32x4 *reg, const uint16_t *base,
 }
 
 template <int R, bool KC>
-__device__ __forceinline__ void store_tile(u32x4 *lds, const u32x4 *reg,
-                                           int tid) {
+__device__ __forceinline__ void store_tile(u32x4 *lds, const u32x4 *reg, int tid) {
   if constexpr (KC) {
 #pragma unroll
     for (int i = 0; i < TileShape<R, KC>::NREG; ++i) {
@@ -176,67 +144,12 @@ __device__ __forceinline__ void store_tile(u32x4 *lds, const u32x4 *reg,
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t x = in[2 * e][d], y = in[2 * e + 1][d];
-          w[e] = (r & 1) ? ((x >> 16) | (y & 0xffff0000u))
-                         : ((x & 0xffffu) | (y << 16));
+          w[e] = (r & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
         }
         lds[lds_slot(rb * 8 + r, kb)] = u32x4{w[0], w[1], w[2], w[3]};
       }
     }
   }
-}
-
-__device__ __forceinline__ float bias_at(const void *bias, int dt, int n) {
-  if (dt == NOVA_HIP_DT_F32) return static_cast<const float *>(bias)[n];
-  const uint16_t h = static_cast<const uint16_t *>(bias)[n];
-  if (dt == NOVA_HIP_DT_BF16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
-  return static_cast<float>(__builtin_bit_cast(_Float16, h));
-}
-
-// gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), in the operation
-// order of NovaGeluForwardPattern (NovaToLinalgGeneric.cpp:1310-1331).
-__device__ __forceinline__ float gelu_tanh(float x) {
-#pragma clang fp contract(off)
-  const float x2 = x * x;
-  const float x3 = x2 * x;
-  const float cubic = 4.471500e-02f * x3;
-  const float inner = x + cubic;
-  const float scaled = 0.7978845608028654f * inner;
-  const float t = tanhf(scaled);
-  return (0.5f * x) * (1.0f + t);
-}
-
-__device__ __forceinline__ uint16_t to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
-
-__device__ __forceinline__ uint16_t to_f16(float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
-}
-
-// Map the linear workgroup id to (batch, tile_m, tile_n).
-__device__ __forceinline__ void tile_of(int id, const GemmArgs &a, int &b,
-                                        int &tm, int &tn) {
-  const int total = a.batch * a.tiles_m * a.tiles_n;
-  // Hardware hands consecutive workgroup ids to the 8 XCDs round robin;
-  // renumber so each XCD sees one contiguous range of tiles.
-  if ((total & 7) == 0) {
-    const int per_xcd = total >> 3;
-    id = (id & 7) * per_xcd + (id >> 3);
-  }
-  const int per_batch = a.tiles_m * a.tiles_n;
-  b = id / per_batch;
-  int t = id - b * per_batch;
-  // Group 4 tile-rows: consecutive ids sweep a 4-row band column by column.
-  constexpr int G = 4;
-  const int band = t / (G * a.tiles_n);
-  const int first = band * G;
-  const int gsz = min(a.tiles_m - first, G);
-  const int in_band = t - band * G * a.tiles_n;
-  tm = first + in_band % gsz;
-  tn = in_band / gsz;
 }
 
 template <int DT, int BM, int BN, bool AKC, bool BKC, bool VEC>
@@ -258,8 +171,17 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs a) {
   tile_of(blockIdx.x, a, bidx, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const uint16_t *Ab = a.A + (int64_t)bidx * a.sab;
-  const uint16_t *Bb = a.B + (int64_t)bidx * a.sbb;
+  Operand oa, ob;
+  oa.rsrc = make_rsrc(a.A + (int64_t)bidx * a.sab, a.a_bytes);
+  oa.s_outer = a.sa_outer;
+  oa.row0 = m0;
+  oa.rows = a.M;
+  oa.K = a.K;
+  ob.rsrc = make_rsrc(a.B + (int64_t)bidx * a.sbb, a.b_bytes);
+  ob.s_outer = a.sb_outer;
+  ob.row0 = n0;
+  ob.rows = a.N;
+  ob.K = a.K;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -269,85 +191,70 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  u32x4 ra[SA::NREG];
-  u32x4 rb[SB::NREG];
+  const int lrow = lane & 31;   // row (A) / column (B) inside a 32-tile
+  const int lhalf = lane >> 5;  // which 8-wide k half of a 16-k step
 
+  // One LDS stage through the MFMAs; fragments of step kk+1 are read while
+  // the MFMAs of step kk run.  The scheduling barriers keep that order: left
+  // alone, the scheduler sinks reads next to their first use to save
+  // registers and exposes the LDS latency at every step.
+  auto compute = [&](const u32x4 *sa, const u32x4 *sb) __attribute__((always_inline)) {
+    u32x4 fa[2][TM], fb[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[0][i] = sa[lds_slot(wm * WTM + i * 32 + lrow, lhalf)];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[0][j] = sb[lds_slot(wn * WTN + j * 32 + lrow, lhalf)];
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int cb = kk & 1, nb = cb ^ 1;
+      if (kk + 1 < kBK / 16) {
+        const int chunk = (kk + 1) * 2 + lhalf;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[nb][i] = sa[lds_slot(wm * WTM + i * 32 + lrow, chunk)];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[nb][j] = sb[lds_slot(wn * WTN + j * 32 + lrow, chunk)];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<DT>(fa[cb][i], fb[cb][j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // The global loads of tile t+1 are issued before the MFMAs of tile t and
+  // written to the other LDS stage after them.  Loads past the last tile
+  // fall outside the buffer range and return zeros, so the loop body is
+  // unconditional.
+  u32x4 ra[SA::NREG], rb[SB::NREG];
   const int nk = (a.K + kBK - 1) / kBK;
-  load_tile<BM, AKC, VEC>(ra, Ab, a.sa_outer, m0, a.M, 0, a.K, tid);
-  load_tile<BN, BKC, VEC>(rb, Bb, a.sb_outer, n0, a.N, 0, a.K, tid);
+  load_tile<BM, AKC, VEC>(ra, oa, 0, tid);
+  load_tile<BN, BKC, VEC>(rb, ob, 0, tid);
   store_tile<BM, AKC>(lds_a[0], ra, tid);
   store_tile<BN, BKC>(lds_b[0], rb, tid);
   __syncthreads();
 
-  const int lrow = lane & 31;   // row (A) / column (B) inside a 32-tile
-  const int lhalf = lane >> 5;  // which 8-wide k half of a 16-k step
-
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      load_tile<BM, AKC, VEC>(ra, Ab, a.sa_outer, m0, a.M, (kt + 1) * kBK, a.K, tid);
-      load_tile<BN, BKC, VEC>(rb, Bb, a.sb_outer, n0, a.N, (kt + 1) * kBK, a.K, tid);
-    }
-    const u32x4 *sa = lds_a[cur];
-    const u32x4 *sb = lds_b[cur];
-#pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int chunk = kk * 2 + lhalf;
-      u32x4 fa[TM], fb[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = sa[lds_slot(wm * WTM + i * 32 + lrow, chunk)];
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = sb[lds_slot(wn * WTN + j * 32 + lrow, chunk)];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<DT>(fa[i], fb[j], acc[i][j]);
-    }
-    if (kt + 1 < nk) {
-      store_tile<BM, AKC>(lds_a[cur ^ 1], ra, tid);
-      store_tile<BN, BKC>(lds_b[cur ^ 1], rb, tid);
-    }
+    load_tile<BM, AKC, VEC>(ra, oa, (kt + 1) * kBK, tid);
+    load_tile<BN, BKC, VEC>(rb, ob, (kt + 1) * kBK, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(lds_a[cur], lds_b[cur]);
+    store_tile<BM, AKC>(lds_a[cur ^ 1], ra, tid);
+    store_tile<BN, BKC>(lds_b[cur ^ 1], rb, tid);
     __syncthreads();
   }
 
-  // Epilogue.  Accumulator element v of lane l in a 32x32 tile sits at
-  // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
-  char *Cb = static_cast<char *>(a.C) +
-             (int64_t)bidx * a.scb * (a.out_dt == NOVA_HIP_DT_F32 ? 4 : 2);
-  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
-  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = n0 + wn * WTN + j * 32 + lrow;
-    if (n >= a.N) continue;
-    const float bv = has_bias ? bias_at(a.bias, a.bias_dt, n) : 0.0f;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int m = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lhalf + (v & 3);
-        if (m >= a.M) continue;
-        float x = acc[i][j][v];
-        if (has_bias) x = x + bv;
-        if (has_gelu) x = gelu_tanh(x);
-        const int64_t off = (int64_t)m * a.scm + n;
-        if (a.out_dt == NOVA_HIP_DT_F32)
-          reinterpret_cast<float *>(Cb)[off] = x;
-        else if (a.out_dt == NOVA_HIP_DT_BF16)
-          reinterpret_cast<uint16_t *>(Cb)[off] = to_bf16(x);
-        else
-          reinterpret_cast<uint16_t *>(Cb)[off] = to_f16(x);
-      }
-    }
-  }
+  store_outputs<TM, TN>(acc, a, bidx, m0 + wm * WTM, n0 + wn * WTN, lane);
 }
 
 template <int DT, int BM, int BN, bool AKC, bool BKC, bool VEC>
 int32_t launch_cfg(const GemmArgs &a, hipStream_t s) {
   const int64_t total = (int64_t)a.batch * a.tiles_m * a.tiles_n;
   if (total > 0x7fffffff) return fail(NOVA_HIP_ERANGE, "gemm: grid too large");
-  hipLaunchKernelGGL((gemm_mfma_kernel<DT, BM, BN, AKC, BKC, VEC>),
-                     dim3((unsigned)total), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((gemm_mfma_kernel<DT, BM, BN, AKC, BKC, VEC>), dim3((unsigned)total),
+                     dim3(kThreads), 0, s, a);
   return check_hip(hipGetLastError(), "gemm_mfma launch");
 }
 
@@ -360,8 +267,7 @@ int32_t dispatch_layout(const GemmArgs &a, bool akc, bool bkc, hipStream_t s) {
 }
 
 template <int DT>
-int32_t dispatch_dtype(const GemmArgs &a, bool akc, bool bkc, bool big, bool vec,
-                       hipStream_t s) {
+int32_t dispatch_dtype(const GemmArgs &a, bool akc, bool bkc, bool big, bool vec, hipStream_t s) {
   if (big) return dispatch_layout<DT, 256, 256, true>(a, akc, bkc, s);
   if (vec) return dispatch_layout<DT, 64, 64, true>(a, akc, bkc, s);
   return dispatch_layout<DT, 64, 64, false>(a, akc, bkc, s);
@@ -395,12 +301,24 @@ int32_t launch_gemm_mfma(const GemmProblem &p, hipStream_t s) {
   a.bias_dt = p.bias_dt;
   a.epi = p.epi;
 
+  // Byte extent of one batch slice of each operand: the buffer range the
+  // kernel's loads are checked against.  Buffer offsets are 32-bit.
+  const int64_t a_ext = p.a_kcontig ? (p.M - 1) * p.sa_outer + p.K : (p.K - 1) * p.sa_outer + p.M;
+  const int64_t b_ext = p.b_kcontig ? (p.N - 1) * p.sb_outer + p.K : (p.K - 1) * p.sb_outer + p.N;
+  if (a_ext * 2 > 0x7fffffff || b_ext * 2 > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "gemm: an operand's batch slice exceeds 2 GiB");
+  a.a_bytes = p.K > 0 ? (uint32_t)(a_ext * 2) : 0u;
+  a.b_bytes = p.K > 0 ? (uint32_t)(b_ext * 2) : 0u;
+
   // 16-byte global loads need aligned bases, outer strides that keep every
   // row aligned, and whole 8-element chunks along the contiguous dim.
   bool vec = aligned16(p.A) && aligned16(p.B) && (p.sa_outer % 8 == 0) &&
              (p.sb_outer % 8 == 0) && (p.sab % 8 == 0) && (p.sbb % 8 == 0);
   vec = vec && (p.a_kcontig ? (p.K % 8 == 0) : (p.M % 8 == 0));
   vec = vec && (p.b_kcontig ? (p.K % 8 == 0) : (p.N % 8 == 0));
+
+  if (gemm_dma_applicable(a, p.a_kcontig, p.b_kcontig, vec))
+    return launch_gemm_dma(a, p.in_dt, p.a_kcontig, p.b_kcontig, s);
 
   // Tile choice: 256x256 when the grid still fills the chip, else 64x64.
   const int64_t big_tiles = p.batch * ((p.M + 255) / 256) * ((p.N + 255) / 256);

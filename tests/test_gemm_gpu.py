@@ -77,6 +77,24 @@ def test_gemm_mfma_lane_layout_exact(cuda):
         assert np.array_equal(got, want.astype(np.float32)), (batch, M, N, K)
 
 
+@pytest.mark.parametrize("dt", [S.BF16, S.F16])
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+def test_gemm_dma_path_exact(cuda, dt, layout):
+    """Whole 256x256 tiles, K % 128 == 0 and >= 128 tiles select the LDS-DMA
+    kernel (transposing LDS reads for M/N-contiguous operands).  Integer
+    grids make the result exact, so any lane / swizzle slip is caught."""
+    g = np.random.default_rng(19)
+    batch, M, N, K = 32, 512, 256, 384
+    af = g.integers(-4, 5, (batch, M, K)).astype(np.float32)
+    bf = g.integers(-4, 5, (batch, K, N)).astype(np.float32)
+    a, b = S.round_to(af, dt), S.round_to(bf, dt)
+    want = np.matmul(af.astype(np.float64), bf.astype(np.float64)).astype(np.float32)
+    A = view_as(a, layout[0], cuda, dt)
+    B = view_as(b, layout[1], cuda, dt)
+    got = nh.gemm(A, B).cpu().numpy()
+    assert np.array_equal(got, want), (layout, float(np.abs(got - want).max()))
+
+
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN"])
 def test_gemm_big_tile_path(cuda, layout):
     """>= 256 macro-tiles of 256x256 selects the big-tile kernel; M and N
