@@ -45,7 +45,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (cpu_baseline becomes null)")
-    ap.add_argument("--only", default="", help="comma list of configs to run (c2,c3,c4,ln,sce)")
+    ap.add_argument("--only", default="",
+                    help="comma list of configs to run (c2,c3,c4,ln,sce; copy = HBM copy calibration)")
     return ap.parse_args()
 
 
@@ -195,6 +196,22 @@ def bench_sce(args, torch, nh, S):
             "loss": float(sets[0][1][2].cpu()[0])}
 
 
+def bench_copy(args, torch):
+    """A plain device copy of 256 MiB (torch's copy kernel): the practical
+    read+write HBM ceiling the reductions are compared with, and the known
+    byte count that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    n = 64 * 1024 * 1024
+    xs = [torch.empty(n, device="cuda").fill_(1.0) for _ in range(3)]
+    ys = [torch.empty(n, device="cuda") for _ in range(3)]
+
+    def fn(i):
+        ys[i % 3].copy_(xs[i % 3])
+
+    ms = time_launches(fn, args.steps * 2, args.warmup, torch)
+    gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+    return {"ms": ms, "bytes": 2 * n * 4, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
+
+
 def cpu_baseline(S):
     """The CPU oracle (restatement of Nova's single-threaded CPU pipeline)
     on a bounded slab of config 2: batch 0, the first R rows, all 4096
@@ -258,6 +275,8 @@ def main():
         cfg["c5_layer_norm_f32_16384x4096"] = stage("ln", lambda: bench_ln(args, torch, nh, S))
     if "sce" in only:
         cfg["c5_sce_f32_4096x32000"] = stage("sce", lambda: bench_sce(args, torch, nh, S))
+    if "copy" in only:  # calibration only; not part of the default run
+        cfg["hbm_copy_256MiB"] = stage("copy", lambda: bench_copy(args, torch))
 
     cpu = None
     if not args.no_cpu_baseline:

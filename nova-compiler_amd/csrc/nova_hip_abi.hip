@@ -65,15 +65,6 @@ void *workspace(hipStream_t s, size_t bytes) {
     fail(NOVA_HIP_ENOMEM, "workspace: hipMalloc(%zu): %s", want, hipGetErrorString(e));
     return nullptr;
   }
-  // Counters at the front of the workspace must start at zero; kernels
-  // restore them to zero when they finish.
-  e = hipMemsetAsync(p, 0, want, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) {
-    (void)hipFree(p);
-    check_hip(e, "workspace: clear");
-    return nullptr;
-  }
   w.ptr = p;
   w.bytes = want;
   return p;

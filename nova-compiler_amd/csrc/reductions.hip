@@ -51,54 +51,64 @@ struct LnArgs {
   float eps, invD;
 };
 
-// Row held in registers: NV f32x4 per lane covers D <= 256 * NV.
+// Row held in registers: NV f32x4 per lane covers D <= 256 * NV.  The grid
+// is persistent (a few workgroups per CU): gamma and beta are staged in LDS
+// once per workgroup instead of re-read from L2 for every row, and each wave
+// walks rows with a grid stride.
 template <int NV>
 __global__ __launch_bounds__(256) void layer_norm_reg_kernel(LnArgs a) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
+  __shared__ f32x4 sg[64 * NV], sb[64 * NV];
   const int nv4 = a.D >> 2;
-  const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)row * a.sx);
-  f32x4 v[NV];
-  float s = 0.0f, q = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + 64 * i;
-    v[i] = (c < nv4) ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    s = s + v[i].x; s = s + v[i].y; s = s + v[i].z; s = s + v[i].w;
-    q = q + v[i].x * v[i].x; q = q + v[i].y * v[i].y;
-    q = q + v[i].z * v[i].z; q = q + v[i].w * v[i].w;
-  }
-  s = wave_sum(s);
-  q = wave_sum(q);
-  const float mean = s * a.invD;
-  const float sq_mean = q * a.invD;
-  const float mean_sq = mean * mean;
-  const float var = sq_mean - mean_sq;
-  const float rstd = 1.0f / sqrtf(var + a.eps);
   const f32x4 *g4 = reinterpret_cast<const f32x4 *>(a.gamma);
   const f32x4 *b4 = reinterpret_cast<const f32x4 *>(a.beta);
-  f32x4 *yr = reinterpret_cast<f32x4 *>(a.y + (int64_t)row * a.sy);
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nv4) {
-      const f32x4 g = g4[c], b = b4[c];
-      f32x4 o;
-      o.x = ((v[i].x - mean) * rstd) * g.x + b.x;
-      o.y = ((v[i].y - mean) * rstd) * g.y + b.y;
-      o.z = ((v[i].z - mean) * rstd) * g.z + b.z;
-      o.w = ((v[i].w - mean) * rstd) * g.w + b.w;
-      __builtin_nontemporal_store(o, yr + c);
-    }
+  for (int c = threadIdx.x; c < nv4; c += 256) {
+    sg[c] = g4[c];
+    sb[c] = b4[c];
   }
-  if (lane == 0) {
-    if (a.mean_sum) a.mean_sum[row] = s;
-    if (a.rstd) a.rstd[row] = rstd;
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  for (int row = blockIdx.x * kWaves + (threadIdx.x >> 6); row < a.rows;
+       row += gridDim.x * kWaves) {
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)row * a.sx);
+    f32x4 v[NV];
+    float s = 0.0f, q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      v[i] = (c < nv4) ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      s = s + v[i].x; s = s + v[i].y; s = s + v[i].z; s = s + v[i].w;
+      q = q + v[i].x * v[i].x; q = q + v[i].y * v[i].y;
+      q = q + v[i].z * v[i].z; q = q + v[i].w * v[i].w;
+    }
+    s = wave_sum(s);
+    q = wave_sum(q);
+    const float mean = s * a.invD;
+    const float sq_mean = q * a.invD;
+    const float mean_sq = mean * mean;
+    const float var = sq_mean - mean_sq;
+    const float rstd = 1.0f / sqrtf(var + a.eps);
+    f32x4 *yr = reinterpret_cast<f32x4 *>(a.y + (int64_t)row * a.sy);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nv4) {
+        const f32x4 g = sg[c], b = sb[c];
+        f32x4 o;
+        o.x = ((v[i].x - mean) * rstd) * g.x + b.x;
+        o.y = ((v[i].y - mean) * rstd) * g.y + b.y;
+        o.z = ((v[i].z - mean) * rstd) * g.z + b.z;
+        o.w = ((v[i].w - mean) * rstd) * g.w + b.w;
+        __builtin_nontemporal_store(o, yr + c);
+      }
+    }
+    if (lane == 0) {
+      if (a.mean_sum) a.mean_sum[row] = s;
+      if (a.rstd) a.rstd[row] = rstd;
+    }
   }
 }
 
@@ -134,8 +144,7 @@ __global__ __launch_bounds__(256) void layer_norm_any_kernel(LnArgs a) {
 // 801-1010) in one pass over the logits: per lane a running (max, sum of
 // exp(x - max)) updated once per 32-value chunk, merged across the wave.
 //   lse = log(max(sum, 1e-7)); loss_r = lse - (x[label] - max);
-// loss = mean over rows with the 64-chunk order of lowerFullReduceMeanToSCF
-// (NovaToLinalg.cpp:1974-2126), done by the last workgroup to finish.
+// Row losses go to a workspace; sce_mean_kernel forms the mean.
 // ---------------------------------------------------------------------------
 struct SceArgs {
   const float *logits;
@@ -143,7 +152,6 @@ struct SceArgs {
   float *loss;
   float *softmax;
   float *row_loss;      // workspace [rows]
-  unsigned *counter;    // workspace, zero between calls
   int64_t sx, ssm;
   int rows, C;
 };
@@ -158,8 +166,6 @@ __device__ __forceinline__ float exp_shifted(float x, float m) {
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
-  __shared__ bool s_last;
-  __shared__ float s_part[64];
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
 
@@ -238,30 +244,113 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
     }
   }
 
-  // Last workgroup to arrive computes the mean.
-  __threadfence();
+}
+
+// Row held in registers across one 512-thread workgroup (rows of up to
+// 2048*NV classes): every logit is read from HBM once, with NV 16-byte loads
+// per thread in flight, and max / sum of exp are exact two-pass
+// reductions over the registers (no running rescale).  The row's loss goes
+// to the workspace for sce_mean_kernel.
+constexpr int kRowThreads = 512;
+
+__device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
+  // wave64 reduction, then across the 8 waves through LDS.
+  v = is_max ? wave_max(v) : wave_sum(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();  // red[] may still be read by the previous reduction
+  if (lane == 0) red[wave] = v;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned ticket = atomicAdd(a.counter, 1u);
-    s_last = (ticket == gridDim.x - 1);
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kRowThreads / 64; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  return r;
+}
+
+template <int NV>
+__global__ __launch_bounds__(kRowThreads) void sce_row_kernel(SceArgs a) {
+  __shared__ float red[kRowThreads / 64];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int n4 = a.C >> 2;
+  const float *xr = a.logits + (int64_t)row * a.sx;
+  const f32x4 *x4 = reinterpret_cast<const f32x4 *>(xr);
+  f32x4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = tid + kRowThreads * i;
+    v[i] = c < n4 ? __builtin_nontemporal_load(x4 + c)
+                  : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const int per = (a.rows + 63) / 64;
-  if (threadIdx.x < 64) {
-    const int start = threadIdx.x * per;
-    const int end = min(start + per, a.rows);
-    float p = 0.0f;
-    for (int i = start; i < end; ++i) p = p + __builtin_nontemporal_load(a.row_loss + i);
-    s_part[threadIdx.x] = p;
+  // the C % 4 tail (at most 3 values) goes to thread 0's spare lane slots
+  float tail[3] = {-INFINITY, -INFINITY, -INFINITY};
+  if (tid == 0) {
+    const int c0 = n4 * 4;
+#pragma unroll
+    for (int e = 0; e < 3; ++e)
+      if (c0 + e < a.C) tail[e] = xr[c0 + e];
   }
+  float m = fmaxf(fmaxf(tail[0], tail[1]), tail[2]);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+  const float gm = block_reduce(m, red, true);
+  float s = exp_shifted(tail[0], gm) + exp_shifted(tail[1], gm) + exp_shifted(tail[2], gm);
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    s += (exp_shifted(v[i].x, gm) + exp_shifted(v[i].y, gm)) +
+         (exp_shifted(v[i].z, gm) + exp_shifted(v[i].w, gm));
+  const float gs = block_reduce(s, red, false);
+  const float safe = fmaxf(gs, 1.0e-7f);
+  if (a.softmax) {
+    float *sr = a.softmax + (int64_t)row * a.ssm;
+    f32x4 *s4 = reinterpret_cast<f32x4 *>(sr);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = tid + kRowThreads * i;
+      if (c < n4) {
+        f32x4 o;
+        o.x = exp_shifted(v[i].x, gm) / safe;
+        o.y = exp_shifted(v[i].y, gm) / safe;
+        o.z = exp_shifted(v[i].z, gm) / safe;
+        o.w = exp_shifted(v[i].w, gm) / safe;
+        __builtin_nontemporal_store(o, s4 + c);
+      }
+    }
+    if (tid == 0)
+      for (int c = n4 * 4; c < a.C; ++c) sr[c] = exp_shifted(xr[c], gm) / safe;
+  }
+  if (tid == 0) {
+    const int t = a.labels[row];
+    float lr;
+    if (t < 0 || t >= a.C) {
+      lr = __builtin_nanf("");
+    } else {
+      lr = logf(safe) - (xr[t] - gm);
+    }
+    a.row_loss[row] = lr;
+  }
+
+}
+
+// Mean of the row losses with the order of lowerFullReduceMeanToSCF
+// (NovaToLinalg.cpp:1974-2126): 64 contiguous chunks of ceil(R/64), each
+// summed sequentially, then the 64 partials sequentially, then / R.  A
+// separate launch: stream order makes every row kernel's stores visible
+// without the device-scope fences (an L2 write-back and invalidate per
+// wave) that a last-workgroup-done scheme would need.
+__global__ __launch_bounds__(64) void sce_mean_kernel(const float *row_loss, int rows,
+                                                      float *loss) {
+  __shared__ float part[64];
+  const int per = (rows + 63) / 64;
+  const int start = threadIdx.x * per;
+  const int end = min(start + per, rows);
+  float p = 0.0f;
+  for (int i = start; i < end; ++i) p = p + row_loss[i];
+  part[threadIdx.x] = p;
   __syncthreads();
   if (threadIdx.x == 0) {
     float total = 0.0f;
-    for (int i = 0; i < 64; ++i) total = total + s_part[i];
-    a.loss[0] = total / (float)a.rows;
-    *a.counter = 0u;
+    for (int i = 0; i < 64; ++i) total = total + part[i];
+    loss[0] = total / (float)rows;
   }
 }
 
@@ -290,12 +379,17 @@ int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
   const bool vec = (p.D % 4 == 0) && (p.sx % 4 == 0) && (p.sy % 4 == 0) &&
                    aligned16(p.x) && aligned16(p.y) && aligned16(p.gamma) &&
                    aligned16(p.beta);
+  // Persistent grid for the register kernels: 4 workgroups per CU (2 for
+  // the widest rows, whose registers allow only that many), never more
+  // than one row per wave.
+  const unsigned pgrid4 = grid < 1024u ? grid : 1024u;
+  const unsigned pgrid2 = grid < 512u ? grid : 512u;
   if (vec && p.D <= 256 * 4)
-    hipLaunchKernelGGL(layer_norm_reg_kernel<4>, dim3(grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(layer_norm_reg_kernel<4>, dim3(pgrid4), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 16)
-    hipLaunchKernelGGL(layer_norm_reg_kernel<16>, dim3(grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(layer_norm_reg_kernel<16>, dim3(pgrid4), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 32)
-    hipLaunchKernelGGL(layer_norm_reg_kernel<32>, dim3(grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(layer_norm_reg_kernel<32>, dim3(pgrid2), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(layer_norm_any_kernel, dim3(grid), dim3(256), 0, s, a);
   return check_hip(hipGetLastError(), "layer_norm launch");
@@ -304,29 +398,43 @@ int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
 int32_t launch_sce(const SceProblem &p, hipStream_t s) {
   if (p.rows > 0x7fffffff - kWaves || p.C > 0x7fffffff)
     return fail(NOVA_HIP_ERANGE, "sce: size exceeds 2^31-1");
-  // Workspace: [0,256) counter (zero between calls), then row losses.
-  char *ws = static_cast<char *>(workspace(s, 256 + (size_t)p.rows * 4));
+  // Workspace: the per-row losses.
+  float *ws = static_cast<float *>(workspace(s, (size_t)p.rows * 4 + 4));
   if (!ws) return NOVA_HIP_ENOMEM;
   SceArgs a;
   a.logits = p.logits;
   a.labels = p.labels;
   a.loss = p.loss;
   a.softmax = p.softmax;
-  a.counter = reinterpret_cast<unsigned *>(ws);
-  a.row_loss = reinterpret_cast<float *>(ws + 256);
+  a.row_loss = ws;
   a.sx = p.sx;
   a.ssm = p.ssm;
   a.rows = (int)p.rows;
   a.C = (int)p.C;
-  // An empty batch still launches one workgroup: its mean is 0/0 = NaN, as
-  // the reference's division by the element count gives.
-  const unsigned grid = (unsigned)(p.rows > 0 ? (p.rows + kWaves - 1) / kWaves : 1);
-  const bool vec = (p.sx % 4 == 0) && aligned16(p.logits);
-  if (vec)
+  const unsigned grid = (unsigned)((p.rows + kWaves - 1) / kWaves);
+  const bool vec = (p.sx % 4 == 0) && aligned16(p.logits) &&
+                   (!p.softmax || (p.ssm % 4 == 0 && aligned16(p.softmax)));
+  // Rows of 2K..32K classes: one workgroup per row, row in registers.
+  const int64_t n4 = p.C / 4;
+  if (vec && p.rows > 0 && p.C > 2048 && n4 <= (int64_t)kRowThreads * 16) {
+    const unsigned g = (unsigned)p.rows;
+    if (n4 <= kRowThreads * 4)
+      hipLaunchKernelGGL(sce_row_kernel<4>, dim3(g), dim3(kRowThreads), 0, s, a);
+    else if (n4 <= kRowThreads * 8)
+      hipLaunchKernelGGL(sce_row_kernel<8>, dim3(g), dim3(kRowThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL(sce_row_kernel<16>, dim3(g), dim3(kRowThreads), 0, s, a);
+  } else if (vec && p.rows > 0) {
     hipLaunchKernelGGL(sce_kernel<true>, dim3(grid), dim3(256), 0, s, a);
-  else
+  } else if (p.rows > 0) {
     hipLaunchKernelGGL(sce_kernel<false>, dim3(grid), dim3(256), 0, s, a);
-  return check_hip(hipGetLastError(), "sce launch");
+  }
+  int32_t rc = check_hip(hipGetLastError(), "sce launch");
+  if (rc) return rc;
+  // An empty batch still gets the mean: 0 / 0 = NaN, as the reference's
+  // division by the element count gives.
+  hipLaunchKernelGGL(sce_mean_kernel, dim3(1), dim3(64), 0, s, a.row_loss, a.rows, a.loss);
+  return check_hip(hipGetLastError(), "sce mean launch");
 }
 
 }  // namespace nova_hip
