@@ -1,29 +1,31 @@
-// MFMA GEMM for aligned problems made of whole 256x256x32 tiles (the large
+// MFMA GEMM for aligned problems made of whole 256x256 tiles (the large
 // configs: batch GEMM 8x4096^3, linear 4096x4096x11008).
 //
 // Operands travel global -> LDS with buffer_load ... lds (LDS DMA): no
-// staging registers, so the K loop can keep three tiles in flight in a
-// four-stage LDS ring (4 x 32 KB).  Each stage holds
-//   * a K-contiguous operand as [256 rows][4 chunks of 8 k], 16-byte chunk
+// staging registers.  K is consumed in steps of BK = 64 so that every
+// K-contiguous row segment a DMA instruction fetches is one whole 128-byte
+// line (with BK = 32 the L2 served twice the requests for the same bytes
+// and ran 93% busy at half the needed rate).  Two LDS stages of 64 KB: the
+// DMA of tile t+1 runs under the MFMAs of tile t.  Each stage holds
+//   * a K-contiguous operand as [256 rows][8 chunks of 8 k], 16-byte chunk
 //     index XOR-swizzled by row so the ds_read_b128 of 16 consecutive rows
 //     covers all banks;
 //   * an M/N-contiguous operand (row-major [K,N] B, or a transposed A) as
-//     [32 k][32 chunks of 8 rows], chunk index XOR ((k & 3) << 1), read
-//     with ds_read_b64_tr_b16, which transposes 16-bit data across each
-//     16-lane group (lane i gets element i of four rows); an XOR by k keeps
-//     the rows read together on distinct banks.
+//     [64 k][32 chunks of 8 rows], read with ds_read_b64_tr_b16, which
+//     transposes 16-bit data across each 16-lane group (lane i gets element
+//     i of four rows); an XOR by k keeps the rows read together on distinct
+//     banks.
 // A DMA instruction writes 64 lanes x 16 bytes contiguously, so the
 // swizzle is applied by choosing, per lane, which global chunk to fetch.
 //
 // Four wave64s in a 2x2 grid each own 128x128 of the output as 4x4 tiles of
 // v_mfma_f32_32x32x16 (256 accumulation registers), issued with B as the
 // first operand so each lane accumulates four consecutive output columns
-// and the epilogue writes them with one vector store.  Per K step (tile t):
-//   read fragments of k16-step 1 | MFMAs of step 0 | wait for this wave's
-//   DMA of tile t+1, barrier | DMA of tile t+4 into the freed stage |
-//   read tile t+1's first fragments | MFMAs of step 1.
-// so LDS latency is never exposed at a stage boundary and global latency
-// has three tiles (~3000 MFMA cycles) to land.
+// and the epilogue writes them with one vector store.  Per K step (tile t,
+// four k16 steps): the fragments of k16-step s+1 are read while the MFMAs
+// of step s run; after step 2 the wave waits for its DMA of tile t+1, one
+// barrier, then the DMA of tile t+2 goes into the freed stage while tile
+// t+1's first fragments are read under the MFMAs of step 3.
 #include "gemm_common.h"
 
 namespace nova_hip {
@@ -31,73 +33,59 @@ namespace {
 
 using namespace gemm;
 
-constexpr int BM = 256, BN = 256, BK = 32;
-constexpr int kSlots = 1024;  // 16-byte slots per operand per stage (16 KB)
+constexpr int BM = 256, BN = 256;
+#ifndef NOVA_DMA_BK
+#define NOVA_DMA_BK 64
+#endif
+constexpr int BK = NOVA_DMA_BK;
+constexpr int kChunks = BK / 8;              // 16-byte chunks per K-contiguous row
+constexpr int kSlots = BM * BK / 8;          // 16-byte slots per operand per stage
+constexpr int kLoads = kSlots / kThreads;    // DMA instructions per thread per operand
+constexpr int kStages = 2;
 constexpr int TM = 4, TN = 4;  // 32x32 tiles per wave (128 x 128)
+static_assert(kStages * 2 * kSlots * 16 <= 160 * 1024, "LDS budget");
+static_assert(2 * kLoads <= TM * TN && TM + TN <= TM * TN, "one DMA load and read per MFMA");
 
 typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-// Swizzles, conflict-free whether the LDS serves 8 (32 banks) or 16 (64
-// banks) lanes of a ds_read_b128 per cycle, and 16 or 32 lanes of a
-// ds_read_b64_tr_b16:
-//   K-contiguous: chunk c of row r at c ^ ((r/2 ^ r/4) & 3)
-//   M/N-contiguous: 16-byte chunk c of k-row k at c ^ (2(k&3) ^ 4(k&3))
-__device__ __forceinline__ int kc_slot(int row, int c) {
-  return row * 4 + (c ^ (((row >> 1) ^ (row >> 2)) & 3));
-}
-__device__ __forceinline__ int mn_slot(int k, int c16) {
-  return k * 32 + (c16 ^ (((k & 3) << 1) ^ ((k & 3) << 2)));
-}
-
-// sched_group_barrier instruction classes.
-constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
-
-// vmcnt(n) with expcnt and lgkmcnt left free (gfx9 encoding).
+// vmcnt(n) with expcnt and lgkmcnt left free; lgkmcnt(0) with the others
+// free (gfx9 encodings).
 #define NOVA_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
+#define NOVA_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
-// Scheduling pattern: spread NMEM memory instructions (the first NREADS are
-// LDS reads, the rest DMA loads) evenly over the first NSLOT of NMFMA MFMAs,
-// one scheduling group each, then leave the remaining MFMAs in one group.
-template <int M, int HI, int NREADS, int SYNC>
-__device__ __forceinline__ void sched_mem() {
-  if constexpr (M < HI) {
-    __builtin_amdgcn_sched_group_barrier(M < NREADS ? kSchedDsRead : kSchedVmemRead, 1, SYNC);
-    sched_mem<M + 1, HI, NREADS, SYNC>();
-  }
+// Swizzles, conflict-free whether the LDS serves 8 or 16 lanes of a
+// ds_read_b128 per cycle (16 or 32 lanes of a ds_read_b64_tr_b16):
+//   K-contiguous: chunk c of row r at c ^ f(r)
+//   M/N-contiguous: 16-byte chunk c of k-row k at c ^ (2(k&3) ^ 4(k&3))
+__device__ __forceinline__ int kc_swz(int row) {
+  if constexpr (kChunks == 8) return (row ^ (row >> 3)) & 7;
+  else return ((row >> 1) ^ (row >> 2)) & 3;
 }
-template <int I, int NSLOT, int NMFMA, int NMEM, int NREADS, int SYNC>
-__device__ __forceinline__ void sched_interleave() {
-  if constexpr (I < NSLOT) {
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, SYNC);
-    sched_mem<I * NMEM / NSLOT, (I + 1) * NMEM / NSLOT, NREADS, SYNC>();
-    sched_interleave<I + 1, NSLOT, NMFMA, NMEM, NREADS, SYNC>();
-  } else if constexpr (NMFMA > NSLOT) {
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, NMFMA - NSLOT, SYNC);
-  }
-}
+__device__ __forceinline__ int kc_slot(int row, int c) { return row * kChunks + (c ^ kc_swz(row)); }
+__device__ __forceinline__ int mn_swz(int k) { return ((k & 3) << 1) ^ ((k & 3) << 2); }
+__device__ __forceinline__ int mn_slot(int k, int c16) { return k * 32 + (c16 ^ mn_swz(k)); }
 
 struct DmaOperand {
   __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t off[4];   // this lane's byte offset for each of its 4 DMA loads, k0 = 0
-  uint32_t k_step;   // bytes to advance one K tile
+  uint32_t off[kLoads];  // this lane's byte offset for each of its DMA loads, k0 = 0
+  uint32_t k_step;       // bytes to advance one K tile
 };
 
 // Per-lane source offsets: wave w's load i fills slots [(i*4 + w) * 64, +64).
+// Slot s holds the chunk kc_slot / mn_slot place there (the XOR swizzle is
+// its own inverse).
 template <bool KC>
 __device__ __forceinline__ void dma_setup(DmaOperand &o, int64_t s_outer, int row0, int wave,
                                           int lane) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kLoads; ++i) {
     const int s = (i * 4 + wave) * 64 + lane;
     int64_t e;
-    // Slot s holds the chunk that kc_slot / mn_slot place there (the XOR
-    // swizzle is its own inverse).
     if constexpr (KC) {
-      const int row = s >> 2, c = (s & 3) ^ (((row >> 1) ^ (row >> 2)) & 3);
+      const int row = s / kChunks, c = (s % kChunks) ^ kc_swz(s / kChunks);
       e = (int64_t)(row0 + row) * s_outer + c * 8;
     } else {
-      const int k = s >> 5, c16 = (s & 31) ^ (((k & 3) << 1) ^ ((k & 3) << 2));
+      const int k = s >> 5, c16 = (s & 31) ^ mn_swz(s >> 5);
       e = (int64_t)k * s_outer + row0 + c16 * 8;
     }
     o.off[i] = (uint32_t)(e * 2);
@@ -105,26 +93,46 @@ __device__ __forceinline__ void dma_setup(DmaOperand &o, int64_t s_outer, int ro
   o.k_step = KC ? (uint32_t)(BK * 2) : (uint32_t)(BK * s_outer * 2);
 }
 
-// Issue the 4 DMA loads of K tile kt into `stage` (kt past the end: the
+// Issue the DMA loads of K tile kt into `stage` (kt past the end: the
 // offsets fall outside the buffer range and nothing is read).
 __device__ __forceinline__ void dma_issue(const DmaOperand &o, u32x4 *stage, int kt, int nk,
                                           int wave) {
   const bool live = kt < nk;
   const uint32_t add = (uint32_t)kt * o.k_step;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kLoads; ++i) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         o.rsrc, (lds_void *)(stage + (i * 4 + wave) * 64), 16, live ? o.off[i] + add : kOOB, 0, 0,
         0);
   }
 }
 
-// Fragment of a 32-row block for k16-step kk.
+// LDS reads as inline assembly.  Written as intrinsics or plain loads, the
+// compiler assumes they may read what any in-flight LDS DMA writes and
+// drains the DMA queue (vmcnt) before them; it cannot tell the two ring
+// stages apart.  As assembly they are invisible to that analysis, and the
+// kernel places the lgkmcnt waits for them itself.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const lds_void *)p;
+}
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ u32x2v lds_read_tr(uint32_t addr) {
+  u32x2v v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Fragment of a 32-row block for k16-step kk (issued, not yet landed).
 template <bool KC>
 __device__ __forceinline__ u32x4 read_frag(const u32x4 *stage, int row_base, int kk, int lane) {
   if constexpr (KC) {
     const int row = row_base + (lane & 31);
-    return stage[kc_slot(row, kk * 2 + (lane >> 5))];
+    return lds_read_b128(lds_addr(stage + kc_slot(row, kk * 2 + (lane >> 5))));
   } else {
     const int g = lane >> 4, p = lane & 15;
     const int n = row_base + 16 * (g & 1) + 4 * (p & 3);
@@ -132,20 +140,16 @@ __device__ __forceinline__ u32x4 read_frag(const u32x4 *stage, int row_base, int
     const uint16_t *base = reinterpret_cast<const uint16_t *>(stage);
     const int e0 = mn_slot(kb, n >> 3) * 8 + (n & 7);
     const int e1 = mn_slot(kb + 4, n >> 3) * 8 + (n & 7);
-    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + e0));
-    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + e1));
-    const uint32_t w0 = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
-    const uint32_t w1 = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
-    const uint32_t w2 = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
-    const uint32_t w3 = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
-    return u32x4{w0, w1, w2, w3};
+    const u32x2v lo = lds_read_tr(lds_addr(base + e0));
+    const u32x2v hi = lds_read_tr(lds_addr(base + e1));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
   }
 }
 
 template <int DT, bool AKC, bool BKC>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
-  __shared__ u32x4 sa0[kSlots], sa1[kSlots], sa2[kSlots], sa3[kSlots];
-  __shared__ u32x4 sb0[kSlots], sb1[kSlots], sb2[kSlots], sb3[kSlots];
+  __shared__ u32x4 ring_a[kStages][kSlots];
+  __shared__ u32x4 ring_b[kStages][kSlots];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -172,71 +176,83 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
 
   const int nk = a.K / BK;
   const int am = wm * 128, bn = wn * 128;
-  // LDS read instructions per read_all: one per K-contiguous fragment, two
-  // (transposing reads) per M/N-contiguous one.
-  constexpr int kReads = (AKC ? TM : 2 * TM) + (BKC ? TN : 2 * TN);
+  constexpr int kSteps = BK / 16;
+  constexpr int kFrags = TM + TN;
 
-  u32x4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  u32x4 fa[2][TM], fb[2][TN];
 
-  auto read_all = [&](u32x4 (&fa)[TM], u32x4 (&fb)[TN], const u32x4 *A, const u32x4 *B,
-                      int kk) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[i] = read_frag<AKC>(A, am + i * 32, kk, lane);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[j] = read_frag<BKC>(B, bn + j * 32, kk, lane);
-  };
-  auto mfma_all = [&](const u32x4 (&fa)[TM], const u32x4 (&fb)[TN]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = mfma_32x32x16<DT>(fb[j], fa[i], acc[i][j]);
-  };
-
-  // Prologue: tiles 0..3 in flight, tile 0 landed, its first fragments read.
-  dma_issue(oa, sa0, 0, nk, wave);
-  dma_issue(ob, sb0, 0, nk, wave);
-  dma_issue(oa, sa1, 1, nk, wave);
-  dma_issue(ob, sb1, 1, nk, wave);
-  dma_issue(oa, sa2, 2, nk, wave);
-  dma_issue(ob, sb2, 2, nk, wave);
-  dma_issue(oa, sa3, 3, nk, wave);
-  dma_issue(ob, sb3, 3, nk, wave);
-  NOVA_WAIT_VMCNT(24);
-  __syncthreads();
-  read_all(fa0, fb0, sa0, sb0, 0);
-
-  // One K step on stage (A, B); (NA, NB) is the next stage.
   // (Every lambda here must inline: a call would force acc into memory.)
-  auto step = [&](const u32x4 *A, const u32x4 *B, u32x4 *FA, u32x4 *FB, const u32x4 *NA,
-                  const u32x4 *NB, int t) __attribute__((always_inline)) {
-    // Fragment reads of k16-step 1 slotted between the first MFMAs of step 0
-    // (early, so they have landed by the barrier).
-    read_all(fa1, fb1, A, B, 1);
-    mfma_all(fa0, fb0);
-    sched_interleave<0, 8, TM * TN, kReads, kReads, 0>();
-    __builtin_amdgcn_sched_barrier(0);
-    NOVA_WAIT_VMCNT(16);  // this wave's DMA of tile t+1 has landed
-    __syncthreads();      // ... everyone's has, and nobody reads tile t any more
-    // Next stage's first fragments, then the DMA of tile t+4, each slotted
-    // between MFMAs of step 1 so the matrix pipe never waits on issue.
-    read_all(fa0, fb0, NA, NB, 0);
-    dma_issue(oa, FA, t + 4, nk, wave);
-    dma_issue(ob, FB, t + 4, nk, wave);
-    mfma_all(fa1, fb1);
-    sched_interleave<0, 12, TM * TN, kReads + 8, kReads, 1>();
-    __builtin_amdgcn_sched_barrier(0);
+  auto read_one = [&](int f, int buf, const u32x4 *A, const u32x4 *B, int kk)
+                      __attribute__((always_inline)) {
+    if (f < TM) fa[buf][f] = read_frag<AKC>(A, am + f * 32, kk, lane);
+    else fb[buf][f - TM] = read_frag<BKC>(B, bn + (f - TM) * 32, kk, lane);
+  };
+  auto mfma_one = [&](int m, int buf) __attribute__((always_inline)) {
+    const int i = m / TN, j = m % TN;
+    acc[i][j] = mfma_32x32x16<DT>(fb[buf][j], fa[buf][i], acc[i][j]);
   };
 
-  // nk is a multiple of 4 (K % 128 == 0): one exit, so the accumulators
-  // keep a single register assignment through the loop.
-  for (int t = 0; t < nk; t += 4) {
-    step(sa0, sb0, sa0, sb0, sa1, sb1, t);
-    step(sa1, sb1, sa1, sb1, sa2, sb2, t + 1);
-    step(sa2, sb2, sa2, sb2, sa3, sb3, t + 2);
-    step(sa3, sb3, sa3, sb3, sa0, sb0, t + 3);
+  // Prologue: tiles 0 and 1 in flight, tile 0 landed, its first fragments read.
+  dma_issue(oa, ring_a[0], 0, nk, wave);
+  dma_issue(ob, ring_b[0], 0, nk, wave);
+  dma_issue(oa, ring_a[1], 1, nk, wave);
+  dma_issue(ob, ring_b[1], 1, nk, wave);
+  NOVA_WAIT_VMCNT(2 * kLoads);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int f = 0; f < kFrags; ++f) read_one(f, 0, ring_a[0], ring_b[0], 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Every instruction group below is fenced with sched_barrier(0), so the
+  // order written is the order issued: MFMA m of a k16 step, then the
+  // fragment read m of the next step (and, in the last step, DMA load m).
+  int cur = 0;
+  for (int t = 0; t < nk; ++t) {
+    u32x4 *A = ring_a[cur], *B = ring_b[cur];
+    const int nxt = cur ^ 1;
+#pragma unroll
+    for (int s = 0; s < kSteps - 1; ++s) {
+      NOVA_WAIT_LGKMCNT0();  // fragments of step s
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < TM * TN; ++m) {
+        mfma_one(m, s & 1);
+        if (m < kFrags) read_one(m, (s + 1) & 1, A, B, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // This wave's fragments of the last step and its DMA of tile t+1 have
+    // landed; after the barrier everyone's have, and tile t's stage is free.
+    NOVA_WAIT_LGKMCNT0();
+    NOVA_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // Last step: tile t+1's first fragments and the DMA of tile t+2 into
+    // tile t's stage, one of each after every MFMA.
+    const bool live = t + 2 < nk;
+    const uint32_t add_a = (uint32_t)(t + 2) * oa.k_step, add_b = (uint32_t)(t + 2) * ob.k_step;
+#pragma unroll
+    for (int m = 0; m < TM * TN; ++m) {
+      mfma_one(m, (kSteps - 1) & 1);
+      if (m < kFrags) read_one(m, 0, ring_a[nxt], ring_b[nxt], 0);
+      if (m < kLoads)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(oa.rsrc, (lds_void *)(A + (m * 4 + wave) * 64), 16,
+                                                 live ? oa.off[m] + add_a : kOOB, 0, 0, 0);
+      else if (m < 2 * kLoads)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ob.rsrc,
+                                                 (lds_void *)(B + ((m - kLoads) * 4 + wave) * 64),
+                                                 16, live ? ob.off[m - kLoads] + add_b : kOOB, 0,
+                                                 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    cur = nxt;
   }
-  // No DMA may still target this workgroup's LDS when it retires.
+  // No DMA may still target this workgroup's LDS when it retires, and the
+  // (unused) fragment reads past the last tile must have landed.
   NOVA_WAIT_VMCNT(0);
+  NOVA_WAIT_LGKMCNT0();
+  __builtin_amdgcn_sched_barrier(0);
 
   store_full<TM, TN>(acc, a, bidx, m0 + am, n0 + bn, lane);
 }
@@ -265,7 +281,7 @@ bool gemm_dma_applicable(const gemm::GemmArgs &a, bool akc, bool bkc, bool vec) 
   // Full tiles only, and vector stores need 16-byte aligned output rows.
   const bool c_ok = (reinterpret_cast<uintptr_t>(a.C) & 15u) == 0 && a.scm % 8 == 0 &&
                     a.scb % 8 == 0;
-  return vec && c_ok && a.M % BM == 0 && a.N % BN == 0 && a.K % (4 * BK) == 0 && a.K > 0 &&
+  return vec && c_ok && a.M % BM == 0 && a.N % BN == 0 && a.K % BK == 0 && a.K > 0 &&
          tiles >= 128 && tiles <= 0x7fffffff;
 }
 
