@@ -42,9 +42,17 @@ constexpr int kChunks = BK / 8;              // 16-byte chunks per K-contiguous 
 constexpr int kSlots = BM * BK / 8;          // 16-byte slots per operand per stage
 constexpr int kLoads = kSlots / kThreads;    // DMA instructions per thread per operand
 constexpr int kStages = 2;
+// The DMA of a tile is spread over this many k16 steps (see the main loop).
+#ifndef NOVA_DMA_SPREAD
+#define NOVA_DMA_SPREAD 2
+#endif
+constexpr int kSpread = NOVA_DMA_SPREAD;
+constexpr int kPerStep = (2 * kLoads + kSpread - 1) / kSpread;  // DMA loads per k16 step
 constexpr int TM = 4, TN = 4;  // 32x32 tiles per wave (128 x 128)
 static_assert(kStages * 2 * kSlots * 16 <= 160 * 1024, "LDS budget");
-static_assert(2 * kLoads <= TM * TN && TM + TN <= TM * TN, "one DMA load and read per MFMA");
+static_assert(kPerStep <= TM * TN && TM + TN <= TM * TN &&
+                  kSpread <= BK / 16,
+              "one DMA load and one fragment read per MFMA at most");
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -93,18 +101,20 @@ __device__ __forceinline__ void dma_setup(DmaOperand &o, int64_t s_outer, int ro
   o.k_step = KC ? (uint32_t)(BK * 2) : (uint32_t)(BK * s_outer * 2);
 }
 
-// Issue the DMA loads of K tile kt into `stage` (kt past the end: the
-// offsets fall outside the buffer range and nothing is read).
-__device__ __forceinline__ void dma_issue(const DmaOperand &o, u32x4 *stage, int kt, int nk,
-                                          int wave) {
+// DMA load q of K tile kt: q < kLoads are A's loads into sa, the rest B's
+// into sb (kt past the end: the offset falls outside the buffer range and
+// nothing is read).
+__device__ __forceinline__ void dma_load(const DmaOperand &oa, const DmaOperand &ob, u32x4 *sa,
+                                         u32x4 *sb, int q, int kt, int nk, int wave) {
   const bool live = kt < nk;
-  const uint32_t add = (uint32_t)kt * o.k_step;
-#pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
+  if (q < kLoads)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(oa.rsrc, (lds_void *)(sa + (q * 4 + wave) * 64), 16,
+                                             live ? oa.off[q] + (uint32_t)kt * oa.k_step : kOOB, 0,
+                                             0, 0);
+  else
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        o.rsrc, (lds_void *)(stage + (i * 4 + wave) * 64), 16, live ? o.off[i] + add : kOOB, 0, 0,
-        0);
-  }
+        ob.rsrc, (lds_void *)(sb + ((q - kLoads) * 4 + wave) * 64), 16,
+        live ? ob.off[q - kLoads] + (uint32_t)kt * ob.k_step : kOOB, 0, 0, 0);
 }
 
 // LDS reads as inline assembly.  Written as intrinsics or plain loads, the
@@ -192,12 +202,24 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
     acc[i][j] = mfma_32x32x16<DT>(fb[buf][j], fa[buf][i], acc[i][j]);
   };
 
-  // Prologue: tiles 0 and 1 in flight, tile 0 landed, its first fragments read.
-  dma_issue(oa, ring_a[0], 0, nk, wave);
-  dma_issue(ob, ring_b[0], 0, nk, wave);
-  dma_issue(oa, ring_a[1], 1, nk, wave);
-  dma_issue(ob, ring_b[1], 1, nk, wave);
-  NOVA_WAIT_VMCNT(2 * kLoads);
+  // The DMA of tile t+2 goes into tile t's stage, which is free from tile
+  // t's barrier on.  Its 2*kLoads loads are spread over kSpread k16 steps:
+  // portion 0 in the last step of tile t (after the barrier), portion p in
+  // step p-1 of tile t+1.  All must land before tile t+1's barrier, which
+  // waits for them (vmcnt(0)) ahead of the first read of tile t+2.
+  auto dma_portion = [&](int p, u32x4 *sa, u32x4 *sb, int kt, int m)
+                         __attribute__((always_inline)) {
+    if (m < kPerStep && p * kPerStep + m < 2 * kLoads)
+      dma_load(oa, ob, sa, sb, p * kPerStep + m, kt, nk, wave);
+  };
+
+  // Prologue: tile 0 and portion 0 of tile 1 in flight, tile 0 landed, its
+  // first fragments read.
+#pragma unroll
+  for (int q = 0; q < 2 * kLoads; ++q) dma_load(oa, ob, ring_a[0], ring_b[0], q, 0, nk, wave);
+#pragma unroll
+  for (int m = 0; m < kPerStep; ++m) dma_portion(0, ring_a[1], ring_b[1], 1, m);
+  NOVA_WAIT_VMCNT(kPerStep);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -206,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
 
   // Every instruction group below is fenced with sched_barrier(0), so the
   // order written is the order issued: MFMA m of a k16 step, then the
-  // fragment read m of the next step (and, in the last step, DMA load m).
+  // fragment read m of the next step, then DMA load m of the step's portion.
   int cur = 0;
   for (int t = 0; t < nk; ++t) {
     u32x4 *A = ring_a[cur], *B = ring_b[cur];
@@ -219,6 +241,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
       for (int m = 0; m < TM * TN; ++m) {
         mfma_one(m, s & 1);
         if (m < kFrags) read_one(m, (s + 1) & 1, A, B, s + 1);
+        if (s + 1 < kSpread) dma_portion(s + 1, ring_a[nxt], ring_b[nxt], t + 1, m);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -228,22 +251,12 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
     NOVA_WAIT_VMCNT(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    // Last step: tile t+1's first fragments and the DMA of tile t+2 into
-    // tile t's stage, one of each after every MFMA.
-    const bool live = t + 2 < nk;
-    const uint32_t add_a = (uint32_t)(t + 2) * oa.k_step, add_b = (uint32_t)(t + 2) * ob.k_step;
+    // Last step: tile t+1's first fragments and portion 0 of tile t+2's DMA.
 #pragma unroll
     for (int m = 0; m < TM * TN; ++m) {
       mfma_one(m, (kSteps - 1) & 1);
       if (m < kFrags) read_one(m, 0, ring_a[nxt], ring_b[nxt], 0);
-      if (m < kLoads)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(oa.rsrc, (lds_void *)(A + (m * 4 + wave) * 64), 16,
-                                                 live ? oa.off[m] + add_a : kOOB, 0, 0, 0);
-      else if (m < 2 * kLoads)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ob.rsrc,
-                                                 (lds_void *)(B + ((m - kLoads) * 4 + wave) * 64),
-                                                 16, live ? ob.off[m - kLoads] + add_b : kOOB, 0,
-                                                 0, 0);
+      dma_portion(0, A, B, t + 2, m);
       __builtin_amdgcn_sched_barrier(0);
     }
     cur = nxt;
