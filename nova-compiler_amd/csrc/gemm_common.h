@@ -8,6 +8,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "nova_hip_internal.h"
 
 namespace nova_hip {
@@ -129,10 +131,47 @@ __device__ __forceinline__ void tile_of(int id, const GemmArgs &a, int &b, int &
 
 // Epilogue for a wave's TM x TN grid of 32x32 accumulator tiles whose
 // top-left output is (mw, nw) in batch bidx.  Accumulator element v of lane
-// l sits at row 8*(v/4) + 4*(l/32) + v%4, column l%32 of its tile.
+// l sits at row 8*(v/4) + 4*(l/32) + v%4, column l%32 of its tile; a store
+// instruction writes 32 consecutive columns of two rows.  Bounds-checked
+// (edge tiles), specialised on output dtype and epilogue.
+template <int TM, int TN, int ODT, int EPI>
+__device__ __forceinline__ void store_outputs_t(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                                int bidx, int mw, int nw, int lane) {
+  constexpr bool kBias = (EPI == NOVA_HIP_EPI_BIAS || EPI == NOVA_HIP_EPI_BIAS_GELU);
+  constexpr bool kGelu = (EPI == NOVA_HIP_EPI_BIAS_GELU || EPI == NOVA_HIP_EPI_GELU);
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  typedef typename std::conditional<ODT == NOVA_HIP_DT_F32, float, uint16_t>::type T;
+  T *Cb = static_cast<T *>(a.C) + (int64_t)bidx * a.scb;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = nw + j * 32 + lrow;
+    const bool n_ok = n < a.N;
+    const float bv = (kBias && n_ok) ? bias_at(a.bias, a.bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = mw + i * 32 + 8 * (v >> 2) + 4 * lhalf + (v & 3);
+        float x = acc[i][j][v];
+        if constexpr (kBias) x = x + bv;
+        if constexpr (kGelu) x = gelu_tanh(x);
+        if (n_ok && m < a.M) {
+          T *dst = Cb + (int64_t)m * a.scm + n;
+          if constexpr (ODT == NOVA_HIP_DT_F32) *dst = x;
+          else if constexpr (ODT == NOVA_HIP_DT_BF16) *dst = to_bf16(x);
+          else *dst = to_f16(x);
+        }
+      }
+    }
+  }
+}
+
+// The same with the output dtype and epilogue decided per element: smaller
+// code, used for large per-wave grids (4 x 4 tiles), where the specialised
+// form runs out of registers.
 template <int TM, int TN>
-__device__ __forceinline__ void store_outputs(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
-                                              int bidx, int mw, int nw, int lane) {
+__device__ __forceinline__ void store_outputs_any(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                                  int bidx, int mw, int nw, int lane) {
   const int lrow = lane & 31, lhalf = lane >> 5;
   char *Cb = static_cast<char *>(a.C) +
              (int64_t)bidx * a.scb * (a.out_dt == NOVA_HIP_DT_F32 ? 4 : 2);
@@ -161,6 +200,29 @@ __device__ __forceinline__ void store_outputs(const f32x16 (&acc)[TM][TN], const
           reinterpret_cast<uint16_t *>(Cb)[off] = to_f16(x);
       }
     }
+  }
+}
+
+// Runtime (output dtype, epilogue) -> one specialisation of store_outputs_t
+// (grids of up to 4 tiles per wave).
+template <int TM, int TN>
+__device__ __forceinline__ void store_outputs(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                              int bidx, int mw, int nw, int lane) {
+  if constexpr (TM * TN > 4) {
+    store_outputs_any<TM, TN>(acc, a, bidx, mw, nw, lane);
+    return;
+  }
+  switch (a.out_dt * 4 + a.epi) {
+#define NOVA_EPI_CASE(O, E) \
+  case O * 4 + E:           \
+    store_outputs_t<TM, TN, O, E>(acc, a, bidx, mw, nw, lane); \
+    break;
+    NOVA_EPI_CASE(0, 0) NOVA_EPI_CASE(0, 1) NOVA_EPI_CASE(0, 2) NOVA_EPI_CASE(0, 3)
+    NOVA_EPI_CASE(1, 0) NOVA_EPI_CASE(1, 1) NOVA_EPI_CASE(1, 2) NOVA_EPI_CASE(1, 3)
+    NOVA_EPI_CASE(2, 0) NOVA_EPI_CASE(2, 1) NOVA_EPI_CASE(2, 2) NOVA_EPI_CASE(2, 3)
+#undef NOVA_EPI_CASE
+    default:
+      break;
   }
 }
 
@@ -246,5 +308,8 @@ __device__ __forceinline__ void store_full(const f32x16 (&acc)[TM][TN], const Ge
 // register-staged kernel).
 bool gemm_dma_applicable(const gemm::GemmArgs &a, bool akc, bool bkc, bool vec);
 int32_t launch_gemm_dma(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc, hipStream_t s);
+// Small-K kernel (gemm_small.hip): whole K staged in LDS per output tile.
+bool gemm_small_applicable(const gemm::GemmArgs &a, bool akc, bool bkc);
+int32_t launch_gemm_small(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc, hipStream_t s);
 
 }  // namespace nova_hip

@@ -319,6 +319,10 @@ int32_t launch_gemm_mfma(const GemmProblem &p, hipStream_t s) {
 
   if (gemm_dma_applicable(a, p.a_kcontig, p.b_kcontig, vec))
     return launch_gemm_dma(a, p.in_dt, p.a_kcontig, p.b_kcontig, s);
+  // Rows without 16-byte alignment would cost the tiled kernel 2-byte loads;
+  // with a small K the staged kernel copies them whole instead.
+  if (!vec && gemm_small_applicable(a, p.a_kcontig, p.b_kcontig))
+    return launch_gemm_small(a, p.in_dt, p.a_kcontig, p.b_kcontig, s);
 
   // Tile choice: 256x256 when the grid still fills the chip, else 64x64.
   const int64_t big_tiles = p.batch * ((p.M + 255) / 256) * ((p.N + 255) / 256);

@@ -1,0 +1,300 @@
+// MFMA GEMM for small K (config 4: fp16 96x197x197x64 and 96x197x64x197,
+// attention-score shaped).  Such problems move far more output than they
+// compute, and their rows are rarely 16-byte aligned (197 fp16 = 394 B), so
+// the tiled kernels would fall back to 2-byte loads and several passes.
+//
+// One workgroup owns a 64 x NT output tile of one batch (NT = 64..256) and
+// the whole K range.  Both operands are staged into LDS once, normalised:
+//   * an operand is a set of "lines", each contiguous in memory -- rows of
+//     a K-contiguous operand (A rows / B columns), or k-lines of an M/N-
+//     contiguous one;
+//   * each thread writes one aligned 16-byte LDS chunk of a line: it loads
+//     the two aligned global chunks covering it and funnel-shifts them by the
+//     line's misalignment (v_alignbyte), zeroing elements past the line's
+//     end; lines past the operand are written as zeros;
+//   * the buffer resource starts at the slice base rounded down to 16 bytes
+//     and ends at its end rounded up (the rounding never leaves the 16-byte
+//     blocks, hence the pages, holding the slice's first and last bytes).
+// The LDS layouts are then the ones the MFMA wants: [row][k] read with
+// ds_read_b128, or [k][row] read with the transposing ds_read_b64_tr_b16.
+// Eight waves stage; four of them, in a 2x2 grid, then each own 32 rows x
+// NT/2 columns as NT/64 tiles of v_mfma_f32_32x32x16, and the epilogue
+// writes bounds-checked coalesced stores.
+#include "gemm_common.h"
+
+namespace nova_hip {
+namespace {
+
+using namespace gemm;
+
+constexpr int kBM = 64;
+constexpr int kMaxNT = 256;
+constexpr int kLdsBytes = 64 * 1024;  // staging budget per workgroup
+// Staging runs on eight waves, the MFMAs and the epilogue on the first four
+// (2x2 grid): staging is the long, latency-bound part.
+constexpr int kStageThreads = 512;
+// Chunks staged per thread per round, for A and for B (two loads each).
+constexpr int kBatchA = 4, kBatchB = 4;
+
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+struct SmallArgs {
+  GemmArgs g;
+  int a_kc, b_kc;  // unit stride on K
+  int pa, pb;      // LDS bytes per staged line of A / B (multiple of 16)
+  int kp;          // K rounded up to 16
+  int nt;          // output columns per workgroup
+};
+
+// Staging geometry of one operand for one workgroup.
+struct Lines {
+  __amdgpu_buffer_rsrc_t rsrc;  // slice base rounded down to 16 B .. end rounded up
+  uint32_t c0;                  // byte offset of line 0 from the resource base
+  uint32_t step;                // bytes between consecutive lines
+  int nvalid;                   // lines holding data
+  int nalloc;                   // lines written to LDS (those past nvalid as zeros)
+  int len;                      // valid elements per line
+  int ncpl;                     // 16-byte LDS chunks written per line
+  int pitch;                    // LDS bytes per line
+};
+
+__device__ __forceinline__ Lines make_lines(const uint16_t *slice, uint32_t slice_bytes,
+                                            int64_t line0, int64_t stride, int nvalid,
+                                            int nalloc, int len, int ncpl, int pitch) {
+  Lines l;
+  // Every input is wave-uniform; readfirstlane keeps the resource in scalar
+  // registers (a resource in vector registers turns each load into a loop).
+  const uint64_t addr = reinterpret_cast<uintptr_t>(slice);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)addr);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32));
+  const uint32_t delta = lo & 15u;
+  const char *base = reinterpret_cast<const char *>(((uint64_t)hi << 32) | (lo & ~15u));
+  const int range = __builtin_amdgcn_readfirstlane((int)((slice_bytes + delta + 15u) & ~15u));
+  l.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, range, 0x00020000);
+  l.c0 = delta + (uint32_t)(line0 * 2);
+  l.step = (uint32_t)(stride * 2);
+  l.nvalid = nvalid;
+  l.nalloc = nalloc;
+  l.len = len;
+  l.ncpl = ncpl;
+  l.pitch = pitch;
+  return l;
+}
+
+// Normalised chunk q (line i = q / ncpl, chunk c = q % ncpl): the two aligned
+// global chunks holding elements 8c .. 8c+7 of line i.  Chunks with no valid
+// element load from beyond the resource's range: zeros, no memory access,
+// and no branch to split the batch of loads.
+struct Raw {
+  u32x4 lo, hi;
+};
+__device__ __forceinline__ Raw chunk_load(const Lines &l, int q, int nq) {
+  const int i = q / l.ncpl, c = q - i * l.ncpl;
+  const bool live = q < nq && i < l.nvalid && 8 * c < l.len;
+  const uint32_t off = ((l.c0 + (uint32_t)i * l.step) & ~15u) + 16u * c;
+  Raw r;
+  r.lo = __builtin_amdgcn_raw_buffer_load_b128(l.rsrc, live ? off : kOOB, 0, 0);
+  r.hi = __builtin_amdgcn_raw_buffer_load_b128(l.rsrc, live ? off + 16u : kOOB, 0, 0);
+  return r;
+}
+
+// Bytes [s, s+16) of lo:hi (s even, 0..14), elements of the line at or past
+// `len` zeroed, written to the chunk's LDS slot.
+__device__ __forceinline__ void chunk_store(const Lines &l, char *lds, int q, int nq, Raw r) {
+  if (q >= nq) return;
+  const int i = q / l.ncpl, c = q - i * l.ncpl;
+  const uint32_t sh = (l.c0 + (uint32_t)i * l.step) & 15u;
+  const uint32_t w[8] = {r.lo[0], r.lo[1], r.lo[2], r.lo[3], r.hi[0], r.hi[1], r.hi[2], r.hi[3]};
+  // Skip sh/4 whole dwords in two steps (by 1, then by 2), as bit masks:
+  // written as conditional selects, the compiler turns them into an indexed
+  // array and routes it through scratch memory.
+  const uint32_t m1 = 0u - ((sh >> 2) & 1u), m2 = 0u - ((sh >> 3) & 1u);
+  uint32_t t[7], sel[5];
+#pragma unroll
+  for (int e = 0; e < 7; ++e) t[e] = w[e] ^ ((w[e] ^ w[e + 1]) & m1);
+#pragma unroll
+  for (int e = 0; e < 5; ++e) sel[e] = t[e] ^ ((t[e] ^ t[e + 2]) & m2);
+  u32x4 out;
+  const int e0 = 8 * c;
+  const bool line_ok = i < l.nvalid;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t v = __builtin_amdgcn_alignbyte(sel[d + 1], sel[d], sh & 3u);
+    const int e = e0 + 2 * d;
+    if (!line_ok || e >= l.len) v = 0u;
+    else if (e + 1 >= l.len) v &= 0xffffu;
+    out[d] = v;
+  }
+  *reinterpret_cast<u32x4 *>(lds + i * l.pitch + 16 * c) = out;
+}
+
+// Stage both operands.  Each round issues up to kBatchA chunks of A and
+// kBatchB of B per thread (two loads each) before their LDS writes, so the
+// latencies overlap.  (A and B get loops of their own: a resource chosen per
+// lane would leave the wave-uniform registers.)
+__device__ __forceinline__ void stage(const Lines &la, const Lines &lb, char *lds_a, char *lds_b,
+                                      int tid) {
+  constexpr int T = kStageThreads;
+  const int na = la.nalloc * la.ncpl, nb = lb.nalloc * lb.ncpl;
+  for (int r = 0; r * T * kBatchA < na || r * T * kBatchB < nb; ++r) {
+    Raw va[kBatchA], vb[kBatchB];
+    const int qa = tid + r * T * kBatchA, qb = tid + r * T * kBatchB;
+#pragma unroll
+    for (int u = 0; u < kBatchA; ++u) va[u] = chunk_load(la, qa + u * T, na);
+#pragma unroll
+    for (int u = 0; u < kBatchB; ++u) vb[u] = chunk_load(lb, qb + u * T, nb);
+#pragma unroll
+    for (int u = 0; u < kBatchA; ++u) chunk_store(la, lds_a, qa + u * T, na, va[u]);
+#pragma unroll
+    for (int u = 0; u < kBatchB; ++u) chunk_store(lb, lds_b, qb + u * T, nb, vb[u]);
+  }
+}
+
+// MFMA fragment of 32 rows (M rows of A or N columns of B) starting at
+// `row0` of the workgroup's window, k16 step kk: lane l gets row row0 + l%32,
+// k = 16 kk + 8 (l/32) + 0..7.  kc: LDS holds [row][k] (one 16-byte read);
+// otherwise [k][row], read with ds_read_b64_tr_b16 (within each 16-lane group
+// lane i receives element i of the four k-lines its group addresses).
+__device__ __forceinline__ u32x4 read_frag(const char *lds, int pitch, bool kc, int row0, int kk,
+                                           int lane) {
+  if (kc) {
+    const int row = row0 + (lane & 31), k0 = kk * 16 + 8 * (lane >> 5);
+    return *reinterpret_cast<const u32x4 *>(lds + row * pitch + 2 * k0);
+  }
+  const int g = lane >> 4, p = lane & 15;
+  const int n = row0 + 16 * (g & 1) + 4 * (p & 3);
+  const int kb = kk * 16 + 8 * (g >> 1) + (p >> 2);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4 *)(lds + kb * pitch + 2 * n));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4 *)(lds + (kb + 4) * pitch + 2 * n));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+  return u32x4{l2[0], l2[1], h2[0], h2[1]};
+}
+
+template <int DT, int TNW>
+__global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const GemmArgs &a = s.g;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Tile indices come out of VALU divisions; readfirstlane tells the compiler
+  // they are wave-uniform, so the buffer resources stay in scalar registers
+  // (otherwise every load becomes a waterfall loop).
+  const int per_batch = a.tiles_m * a.tiles_n;
+  const int bidx = __builtin_amdgcn_readfirstlane(blockIdx.x / per_batch);
+  const int t = blockIdx.x - bidx * per_batch;
+  const int tm = __builtin_amdgcn_readfirstlane(t / a.tiles_n);
+  const int tn = __builtin_amdgcn_readfirstlane(t - tm * a.tiles_n);
+  const int m0 = tm * kBM, n0 = tn * s.nt;
+  const int m_valid = min(kBM, a.M - m0), n_valid = min(s.nt, a.N - n0);
+
+  const uint16_t *A = a.A + (int64_t)bidx * a.sab;
+  const uint16_t *B = a.B + (int64_t)bidx * a.sbb;
+  // A K-contiguous: lines are the valid rows m0.. (sa_outer apart), kp
+  // elements each (k >= K zeroed); otherwise lines are k = 0..kp-1 (sa_outer
+  // apart, k >= K zeroed) over the valid part of the row window m0...
+  // Likewise B with N and NT.  LDS rows or columns past the valid ones are
+  // left unwritten: they only feed outputs the epilogue discards.
+  const int ka = (m_valid + 7) / 8, kb = (n_valid + 7) / 8;
+  const Lines la = s.a_kc ? make_lines(A, a.a_bytes, (int64_t)m0 * a.sa_outer, a.sa_outer,
+                                       m_valid, m_valid, a.K, s.kp / 8, s.pa)
+                          : make_lines(A, a.a_bytes, m0, a.sa_outer, a.K, s.kp, m_valid, ka,
+                                       s.pa);
+  const Lines lb = s.b_kc ? make_lines(B, a.b_bytes, (int64_t)n0 * a.sb_outer, a.sb_outer,
+                                       n_valid, n_valid, a.K, s.kp / 8, s.pb)
+                          : make_lines(B, a.b_bytes, n0, a.sb_outer, a.K, s.kp, n_valid, kb,
+                                       s.pb);
+  char *lds_a = smem;
+  char *lds_b = smem + (s.a_kc ? kBM : s.kp) * s.pa;
+  stage(la, lb, lds_a, lds_b, tid);
+  __syncthreads();
+  if (wave >= 4) return;
+
+  f32x16 acc[1][TNW];
+#pragma unroll
+  for (int j = 0; j < TNW; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[0][j][v] = 0.0f;
+
+  const int ksteps = s.kp / 16;
+  const int nw = wn * (TNW * 32);
+#pragma unroll 2
+  for (int kk = 0; kk < ksteps; ++kk) {
+    const u32x4 fa = read_frag(lds_a, s.pa, s.a_kc, wm * 32, kk, lane);
+    u32x4 fb[TNW];
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, s.pb, s.b_kc, nw + 32 * j, kk, lane);
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
+  }
+  store_outputs<1, TNW>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
+}
+
+template <int DT>
+int32_t launch_dt(const SmallArgs &s, size_t lds, hipStream_t st) {
+  const dim3 grid((unsigned)(s.g.batch * s.g.tiles_m * s.g.tiles_n)), block(kStageThreads);
+  switch (s.nt / 64) {
+    case 1: hipLaunchKernelGGL((gemm_small_kernel<DT, 1>), grid, block, lds, st, s); break;
+    case 2: hipLaunchKernelGGL((gemm_small_kernel<DT, 2>), grid, block, lds, st, s); break;
+    case 3: hipLaunchKernelGGL((gemm_small_kernel<DT, 3>), grid, block, lds, st, s); break;
+    default: hipLaunchKernelGGL((gemm_small_kernel<DT, 4>), grid, block, lds, st, s); break;
+  }
+  return check_hip(hipGetLastError(), "gemm_small launch");
+}
+
+// Staging geometry chosen on the host: output columns per workgroup, K
+// rounded up to whole k16 steps, and each operand's LDS line pitch (its
+// padded width plus 16 bytes, which spreads the rows of a fragment read
+// over the banks).
+struct SmallPlan {
+  int nt, kp, pa, pb, a_lines, b_lines;
+  size_t lds;
+};
+
+SmallPlan plan_small(int64_t N, int64_t K, bool akc, bool bkc) {
+  SmallPlan p;
+  p.nt = N >= kMaxNT ? kMaxNT : (int)(((N + 63) / 64) * 64);
+  p.kp = (int)(((K + 15) / 16) * 16);
+  p.pa = (akc ? p.kp : kBM) * 2 + 16;
+  p.a_lines = akc ? kBM : p.kp;
+  p.pb = (bkc ? p.kp : p.nt) * 2 + 16;
+  p.b_lines = bkc ? p.nt : p.kp;
+  p.lds = (size_t)p.a_lines * p.pa + (size_t)p.b_lines * p.pb;
+  return p;
+}
+
+}  // namespace
+
+bool gemm_small_applicable(const gemm::GemmArgs &a, bool akc, bool bkc) {
+  if (a.K <= 0 || a.K > 512) return false;
+  // Resources reach up to 30 bytes past a slice (both ends rounded to 16).
+  if (a.a_bytes > 0x7fffff00u || a.b_bytes > 0x7fffff00u) return false;
+  // The whole K range of a 64-row A window and an NT-column B window must
+  // fit the staging budget.
+  const SmallPlan p = plan_small(a.N, a.K, akc, bkc);
+  return p.lds <= (size_t)kLdsBytes;
+}
+
+int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool bkc,
+                          hipStream_t st) {
+  SmallArgs s;
+  s.g = a_in;
+  const SmallPlan p = plan_small(a_in.N, a_in.K, akc, bkc);
+  s.a_kc = akc;
+  s.b_kc = bkc;
+  s.pa = p.pa;
+  s.pb = p.pb;
+  s.nt = p.nt;
+  s.kp = p.kp;
+  s.g.tiles_m = (a_in.M + kBM - 1) / kBM;
+  s.g.tiles_n = (a_in.N + p.nt - 1) / p.nt;
+  if ((int64_t)s.g.batch * s.g.tiles_m * s.g.tiles_n > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "gemm: too many output tiles");
+  if (in_dt == NOVA_HIP_DT_BF16) return launch_dt<NOVA_HIP_DT_BF16>(s, p.lds, st);
+  return launch_dt<NOVA_HIP_DT_F16>(s, p.lds, st);
+}
+
+}  // namespace nova_hip

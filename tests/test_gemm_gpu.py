@@ -233,3 +233,41 @@ def test_c4_fp16_unaligned_full(cuda, cfg):
     B = to_dev(inp["B"], S.F16, cuda)
     got = nh.batch_matmul(A, B).cpu().numpy()
     assert_close_lp(got, want, cfg)
+
+
+def _strided_view(host, layout, dev, dt, offset, batch_pad):
+    """Device view of host [batch, R, C] at element `offset` of a flat buffer,
+    batch stride R*C + batch_pad; layout 'T' stores each slice transposed."""
+    import torch
+    batch, R, C = host.shape
+    sl = host if layout == "N" else np.swapaxes(host, -1, -2)
+    inner = sl.shape[1] * sl.shape[2]
+    sb = inner + batch_pad
+    flat = np.zeros(offset + batch * sb + 8, host.dtype)
+    for b in range(batch):
+        flat[offset + b * sb: offset + b * sb + inner] = np.ascontiguousarray(sl[b]).ravel()
+    t = to_dev(flat, dt, dev)
+    if layout == "N":
+        return torch.as_strided(t, (batch, R, C), (sb, C, 1), offset)
+    return torch.as_strided(t, (batch, R, C), (sb, 1, R), offset)
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("shape", [(3, 37, 45, 23), (2, 197, 197, 64), (2, 197, 64, 197),
+                                   (2, 70, 300, 40)])
+@pytest.mark.parametrize("offsets", [(1, 5), (3, 0), (0, 7)])
+def test_gemm_staged_misaligned_exact(cuda, layout, shape, offsets):
+    """Small-K kernel: slice bases at every 16-byte misalignment (odd storage
+    offsets and odd batch strides).  Integer inputs make the f32 sums exact,
+    so any misplaced element shows as an exact mismatch."""
+    batch, M, N, K = shape
+    g = np.random.default_rng(batch * 1000 + M + N + K)
+    a = g.integers(-4, 5, size=(batch, M, K)).astype(np.float32)
+    b = g.integers(-4, 5, size=(batch, K, N)).astype(np.float32)
+    a16 = a.astype(np.float16).view(np.uint16)
+    b16 = b.astype(np.float16).view(np.uint16)
+    A = _strided_view(a16, layout[0], cuda, S.F16, offsets[0], 3)
+    B = _strided_view(b16, layout[1], cuda, S.F16, offsets[1], 5)
+    got = nh.gemm(A, B).cpu().numpy()
+    want = np.einsum("bmk,bkn->bmn", a.astype(np.float64), b.astype(np.float64))
+    np.testing.assert_array_equal(got, want.astype(np.float32))
