@@ -55,7 +55,7 @@ struct LnArgs {
 // is persistent (a few workgroups per CU): gamma and beta are staged in LDS
 // once per workgroup instead of re-read from L2 for every row, and each wave
 // walks rows with a grid stride.
-template <int NV>
+template <int NV, bool FULL>
 __global__ __launch_bounds__(256) void layer_norm_reg_kernel(LnArgs a) {
 #pragma clang fp contract(off)
   __shared__ f32x4 sg[64 * NV], sb[64 * NV];
@@ -68,15 +68,21 @@ __global__ __launch_bounds__(256) void layer_norm_reg_kernel(LnArgs a) {
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  for (int row = blockIdx.x * kWaves + (threadIdx.x >> 6); row < a.rows;
-       row += gridDim.x * kWaves) {
+  // FULL: D == 256 * NV, so every lane's NV chunks are inside the row and
+  // the loads and stores need no guards (guarded, they cost ~5% here).
+  auto in_row = [&](int c) __attribute__((always_inline)) { return FULL || c < nv4; };
+  // Each workgroup takes a contiguous block of rows, its waves interleaved
+  // inside it, so one workgroup's reads and its S / rstd writes stay close.
+  const int per_wg = (a.rows + gridDim.x - 1) / gridDim.x;
+  const int row_end = min(a.rows, (int)(blockIdx.x + 1) * per_wg);
+  for (int row = blockIdx.x * per_wg + (threadIdx.x >> 6); row < row_end; row += kWaves) {
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)row * a.sx);
     f32x4 v[NV];
     float s = 0.0f, q = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = lane + 64 * i;
-      v[i] = (c < nv4) ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      v[i] = in_row(c) ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -95,7 +101,7 @@ __global__ __launch_bounds__(256) void layer_norm_reg_kernel(LnArgs a) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = lane + 64 * i;
-      if (c < nv4) {
+      if (in_row(c)) {
         const f32x4 g = sg[c], b = sb[c];
         f32x4 o;
         o.x = ((v[i].x - mean) * rstd) * g.x + b.x;
@@ -384,12 +390,16 @@ int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
   // than one row per wave.
   const unsigned pgrid4 = grid < 1024u ? grid : 1024u;
   const unsigned pgrid2 = grid < 512u ? grid : 512u;
-  if (vec && p.D <= 256 * 4)
-    hipLaunchKernelGGL(layer_norm_reg_kernel<4>, dim3(pgrid4), dim3(256), 0, s, a);
+  if (vec && p.D == 256 * 4)
+    hipLaunchKernelGGL((layer_norm_reg_kernel<4, true>), dim3(pgrid4), dim3(256), 0, s, a);
+  else if (vec && p.D <= 256 * 4)
+    hipLaunchKernelGGL((layer_norm_reg_kernel<4, false>), dim3(pgrid4), dim3(256), 0, s, a);
+  else if (vec && p.D == 256 * 16)
+    hipLaunchKernelGGL((layer_norm_reg_kernel<16, true>), dim3(pgrid4), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 16)
-    hipLaunchKernelGGL(layer_norm_reg_kernel<16>, dim3(pgrid4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<16, false>), dim3(pgrid4), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 32)
-    hipLaunchKernelGGL(layer_norm_reg_kernel<32>, dim3(pgrid2), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<32, false>), dim3(pgrid2), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(layer_norm_any_kernel, dim3(grid), dim3(256), 0, s, a);
   return check_hip(hipGetLastError(), "layer_norm launch");
