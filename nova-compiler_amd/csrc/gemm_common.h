@@ -36,6 +36,7 @@ struct GemmArgs {
   int M, N, K;
   int tiles_m, tiles_n, batch;
   int out_dt, bias_dt, epi;
+  int round;  // workgroups resident at once (one per CU), or 0: see round_tile_of
 };
 
 template <int DT>
@@ -104,19 +105,12 @@ __device__ __forceinline__ uint16_t to_f16(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
-// Map the linear workgroup id to (batch, tile_m, tile_n), wave-uniform.
-__device__ __forceinline__ void tile_of(int id, const GemmArgs &a, int &b, int &tm, int &tn) {
-  const int total = a.batch * a.tiles_m * a.tiles_n;
-  // Hardware hands consecutive workgroup ids to the 8 XCDs round robin;
-  // renumber so each XCD sees one contiguous range of tiles.
-  if ((total & 7) == 0) {
-    const int per_xcd = total >> 3;
-    id = (id & 7) * per_xcd + (id >> 3);
-  }
+// Map a linear tile index to (batch, tile_m, tile_n), wave-uniform: within
+// a batch, consecutive indices sweep a band of 4 tile-rows column by column.
+__device__ __forceinline__ void band_tile(int t, const GemmArgs &a, int &b, int &tm, int &tn) {
   const int per_batch = a.tiles_m * a.tiles_n;
-  b = id / per_batch;
-  int t = id - b * per_batch;
-  // Group 4 tile-rows: consecutive ids sweep a 4-row band column by column.
+  b = t / per_batch;
+  t -= b * per_batch;
   constexpr int G = 4;
   const int band = t / (G * a.tiles_n);
   const int first = band * G;
@@ -127,6 +121,37 @@ __device__ __forceinline__ void tile_of(int id, const GemmArgs &a, int &b, int &
   b = __builtin_amdgcn_readfirstlane(b);
   tm = __builtin_amdgcn_readfirstlane(tm);
   tn = __builtin_amdgcn_readfirstlane(tn);
+}
+
+// Workgroup id -> tile for kernels with several workgroups per CU: the
+// hardware hands consecutive workgroup ids to the 8 XCDs round robin, so
+// renumber to give each XCD one contiguous range of tiles (its own L2 sees
+// neighbouring tiles).
+__device__ __forceinline__ void tile_of(int id, const GemmArgs &a, int &b, int &tm, int &tn) {
+  const int total = a.batch * a.tiles_m * a.tiles_n;
+  if ((total & 7) == 0) {
+    const int per_xcd = total >> 3;
+    id = (id & 7) * per_xcd + (id >> 3);
+  }
+  band_tile(id, a, b, tm, tn);
+}
+
+// Workgroup id -> tile for kernels with one workgroup per CU, which run in
+// rounds of a.round workgroups (a.round = CU count, a multiple of 8).  In
+// each full round, XCD x (ids q = x mod 8 of the round) takes the round's
+// tiles [x*round/8, (x+1)*round/8): all eight XCDs work on neighbouring
+// tiles of the same band sweep, so an operand panel one XCD fetches from HBM
+// is found in the MALL by the XCDs that share it, and each XCD's 32 tiles
+// form a 4 x 8 block whose panels its L2 shares.  The last, partial round
+// keeps the identity order.
+__device__ __forceinline__ void round_tile_of(int id, const GemmArgs &a, int &b, int &tm, int &tn) {
+  const int total = a.batch * a.tiles_m * a.tiles_n;
+  const int round = a.round;
+  if (round > 0 && id < total / round * round) {
+    const int r = id / round, q = id - r * round;
+    id = r * round + (q & 7) * (round >> 3) + (q >> 3);
+  }
+  band_tile(id, a, b, tm, tn);
 }
 
 // Epilogue for a wave's TM x TN grid of 32x32 accumulator tiles whose

@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
   const int wm = wave >> 1, wn = wave & 1;
 
   int bidx, tm, tn;
-  tile_of(blockIdx.x, a, bidx, tm, tn);
+  round_tile_of(blockIdx.x, a, bidx, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
   DmaOperand oa, ob;
@@ -302,6 +302,10 @@ int32_t launch_gemm_dma(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool bk
   gemm::GemmArgs a = a_in;
   a.tiles_m = a.M / BM;
   a.tiles_n = a.N / BN;
+  // The kernel's 128 KB of LDS allows one workgroup per CU: a round is one
+  // workgroup per CU of the current device (8 XCDs, so a multiple of 8).
+  const int cus = device_cu_count();
+  a.round = (cus > 0 && cus % 8 == 0) ? cus : 0;
   if (in_dt == NOVA_HIP_DT_BF16) return launch_layout<NOVA_HIP_DT_BF16>(a, akc, bkc, s);
   return launch_layout<NOVA_HIP_DT_F16>(a, akc, bkc, s);
 }

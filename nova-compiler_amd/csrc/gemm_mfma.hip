@@ -300,6 +300,7 @@ int32_t launch_gemm_mfma(const GemmProblem &p, hipStream_t s) {
   a.out_dt = p.out_dt;
   a.bias_dt = p.bias_dt;
   a.epi = p.epi;
+  a.round = 0;
 
   // Byte extent of one batch slice of each operand: the buffer range the
   // kernel's loads are checked against.  Buffer offsets are 32-bit.

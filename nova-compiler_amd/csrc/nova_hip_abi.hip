@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <unordered_map>
 
@@ -37,6 +38,22 @@ int32_t fail(int32_t code, const char *fmt, ...) {
 void clear_error() { t_err[0] = 0; }
 
 hipStream_t current_stream() { return t_stream; }
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];  // 0: not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kMaxDevices) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c) return c > 0 ? c : 0;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0;
+  if (dev < kMaxDevices) cache[dev].store(cus > 0 ? cus : -1, std::memory_order_relaxed);
+  return cus > 0 ? cus : 0;
+}
 
 int32_t check_hip(hipError_t e, const char *what) {
   if (e == hipSuccess) return NOVA_HIP_SUCCESS;

@@ -15,6 +15,9 @@ namespace nova_hip {
 int32_t fail(int32_t code, const char *fmt, ...);
 void clear_error();
 hipStream_t current_stream();
+// Compute units of the current device (cached per device), or 0 if the
+// query fails.
+int device_cu_count();
 // Convert a HIP status into NOVA_HIP_EDEVICE with text, or success.
 int32_t check_hip(hipError_t e, const char *what);
 
