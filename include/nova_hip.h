@@ -17,7 +17,7 @@
  *   - memref data pointers are DEVICE pointers owned by the caller (the
  *     reference's address-space-1 convention, robust_driver.cpp:25-39);
  *     the library never allocates or frees caller buffers.  It owns only a
- *     cached per-stream workspace (SCE partial losses).
+ *     cached per-stream workspace (SCE row losses, column-sum partials).
  *   - offsets and strides are in elements and are honoured.  The innermost
  *     dimension of every operand must have unit stride, except where a GEMM
  *     operand is a transposed view (its second-to-last stride is 1 instead).
@@ -201,6 +201,72 @@ int32_t _mlir_ciface_nova_hip_sce_f32(const NovaMemRef2D *logits,
                                       NovaMemRef1D *loss,
                                       NovaMemRef2D *softmax);
 
+/* nova.sce forward and nova.sce_backward fused: the loss as
+ * _mlir_ciface_nova_hip_sce_f32 computes it, and grad [R, C] f32 =
+ * (softmax - onehot(labels)) * f32(1/R), bit-identical to feeding this
+ * library's softmax to _mlir_ciface_nova_hip_sce_backward_f32 but without
+ * writing and re-reading the softmax.  No reference counterpart as one op:
+ * it is the pair nova.sce (NovaToLinalgGeneric.cpp:801-1010) then
+ * nova.sce_backward (:1012-1137) on the sce's softmax result. */
+int32_t _mlir_ciface_nova_hip_sce_fwd_bwd_f32(const NovaMemRef2D *logits,
+                                              const NovaMemRef1D *labels,
+                                              NovaMemRef1D *loss,
+                                              NovaMemRef2D *grad);
+/* ------------------------------------------------------------------------
+ * Backward ops.
+ * ---------------------------------------------------------------------- */
+/* nova.sce_backward (NovaSceBackwardLowering, NovaToLinalgGeneric.cpp:
+ * 1012-1137), class dim last:
+ *   grad = (softmax + scatter(-1.0 at (r, labels[r]))) * f32(1.0 / R)
+ * (one multiply by the f32-rounded reciprocal, :1121-1128).
+ *   softmax, grad : [R, C] f32; labels : [R] i32.
+ * A label outside [0, C) makes that row's gradient NaN (the reference's
+ * scatter writes outside the row). */
+int32_t _mlir_ciface_nova_hip_sce_backward_f32(const NovaMemRef2D *softmax,
+                                               const NovaMemRef1D *labels,
+                                               NovaMemRef2D *grad);
+/* nova.layer_norm_backward (NovaLayerNormBackwardPattern,
+ * NovaToLinalgGeneric.cpp:2128-2371) with the forward's saved stats:
+ *   grad_y, x, dx : [R, D] f32; gamma, dgamma, dbeta : [D] f32;
+ *   mean_sum, rstd : [R] f32 (the forward's second and third results).
+ *   dx = ((gy*gamma - s1/D) - xhat * s2/D) * rstd, xhat = (x - S/D) * rstd,
+ *   s1 = sum_d gy*gamma, s2 = sum_d gy*gamma*xhat;
+ *   dgamma = sum_r gy*xhat, dbeta = sum_r gy.
+ * dx, dgamma, dbeta may each be NULL.  D <= 8192.  The column sums are
+ * deterministic (row blocks in order, then the blocks in order). */
+int32_t _mlir_ciface_nova_hip_layer_norm_backward_f32(
+    const NovaMemRef2D *grad_y, const NovaMemRef2D *x, const NovaMemRef1D *gamma,
+    const NovaMemRef1D *mean_sum, const NovaMemRef1D *rstd, NovaMemRef2D *dx,
+    NovaMemRef1D *dgamma, NovaMemRef1D *dbeta);
+/* nova.linear_backward (NovaLinearBackwardPattern, NovaToLinalgGeneric.cpp:
+ * 1824-1996) for weight [K, N] (the nova.linear convention):
+ *   grad_input [M, K] = grad_out [M, N] . weight^T        (:1867-1911)
+ *   grad_weight [K, N] = x^T . grad_out                    (:1913-1968)
+ *   grad_bias [N] = sum_m grad_out[m, :]                   (:1970-1989)
+ * Rank-3 inputs are passed flattened to [B*M, .], as the reference itself
+ * collapses them for grad_weight.  weight may be a transposed view
+ * (strides {1, K}); grad_weight may be a transposed view of a row-major
+ * [N, K] buffer, which is then written as grad_out^T . x.  Any of the three
+ * outputs may be NULL.  flags = NOVA_HIP_GEMM_FLAGS(in, out, NONE, 0): f32
+ * in -> exact f32 kernel; bf16/f16 in -> MFMA, f32 accumulate, outputs (and
+ * grad_bias) in the out dtype. */
+int32_t _mlir_ciface_nova_hip_linear_backward(const NovaMemRef2D *grad_out,
+                                              const NovaMemRef2D *x,
+                                              const NovaMemRef2D *weight,
+                                              NovaMemRef2D *grad_input,
+                                              NovaMemRef2D *grad_weight,
+                                              NovaMemRef1D *grad_bias,
+                                              int32_t flags);
+/* nova.matmul_backward (NovaMatmulBackwardPattern, NovaToLinalgGeneric.cpp:
+ * 160-239), rank 2: grad_a [M, K] = grad [M, N] . B^T, grad_b [K, N] =
+ * A^T . grad.  Outputs may be NULL or transposed views as above; flags as
+ * for _mlir_ciface_nova_hip_linear_backward. */
+int32_t _mlir_ciface_nova_hip_matmul_backward(const NovaMemRef2D *grad,
+                                              const NovaMemRef2D *A,
+                                              const NovaMemRef2D *B,
+                                              NovaMemRef2D *grad_a,
+                                              NovaMemRef2D *grad_b,
+                                              int32_t flags);
 /* ------------------------------------------------------------------------
  * Runtime.  The reference's host runtime is libmlir_cuda_runtime's mgpu*
  * calls plus cudaMallocAsync / cudaMemcpyAsync declared by FixGpuLaunch.cpp

@@ -1,0 +1,502 @@
+// Backward ops of the path for gfx950: nova.sce_backward, nova.layer_norm_
+// backward and the column sums of nova.linear_backward's bias gradient.  All
+// are HBM-bound streams (no MFMA): rows are read with coalesced 16-byte
+// loads, row reductions run inside one wave64 with cross-lane shuffles, and
+// column reductions over rows are deterministic -- each workgroup sums its
+// own contiguous block of rows in row order into per-workgroup partials,
+// which a second pass adds up in workgroup order -- so two runs give the
+// same bits.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "nova_hip_internal.h"
+
+namespace nova_hip {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// nova.sce_backward (NovaSceBackwardLowering, NovaToLinalgGeneric.cpp:
+// 1012-1137): grad = (softmax + scatter(-1 at the label)) * invN, with invN
+// the f32 rounding of 1.0 / rows (one multiply per element, :1121-1128).
+// A label outside [0, C) makes that row's gradient NaN.
+// Grid: x = chunks of kU * 256 float4s of a row, y = rows.
+// ---------------------------------------------------------------------------
+struct SceBwdArgs {
+  const float *softmax;
+  const int32_t *labels;
+  float *grad;
+  int64_t ss, sg;  // row strides (elements)
+  int rows, C;
+  float invN;
+};
+
+constexpr int kU = 4;
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void sce_backward_kernel(SceBwdArgs a) {
+  const int row = blockIdx.y;
+  const int t = a.labels[row];
+  const bool bad = t < 0 || t >= a.C;
+  const float nan = __builtin_nanf("");
+  const float *sr = a.softmax + (int64_t)row * a.ss;
+  float *gr = a.grad + (int64_t)row * a.sg;
+  if constexpr (VEC) {
+    const int n4 = a.C >> 2;
+    const f32x4 *s4 = reinterpret_cast<const f32x4 *>(sr);
+    f32x4 *g4 = reinterpret_cast<f32x4 *>(gr);
+    const int base = blockIdx.x * (256 * kU) + threadIdx.x;
+    f32x4 v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int c = base + 256 * u;
+      v[u] = c < n4 ? __builtin_nontemporal_load(s4 + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int c = base + 256 * u;
+      if (c < n4) {
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float d = (4 * c + e == t) ? v[u][e] + -1.0f : v[u][e];
+          o[e] = bad ? nan : d * a.invN;
+        }
+        __builtin_nontemporal_store(o, g4 + c);
+      }
+    }
+    // C % 4 tail: the first chunk's first threads.
+    if (blockIdx.x == 0 && threadIdx.x < (a.C & 3)) {
+      const int c = (n4 << 2) + threadIdx.x;
+      const float d = (c == t) ? sr[c] + -1.0f : sr[c];
+      gr[c] = bad ? nan : d * a.invN;
+    }
+  } else {
+    const int base = blockIdx.x * (256 * kU * 4) + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 4 * kU; ++u) {
+      const int c = base + 256 * u;
+      if (c < a.C) {
+        const float d = (c == t) ? sr[c] + -1.0f : sr[c];
+        gr[c] = bad ? nan : d * a.invN;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// nova.layer_norm_backward (NovaLayerNormBackwardPattern,
+// NovaToLinalgGeneric.cpp:2128-2371).  Per row, with the forward's saved
+// S (mean_sum) and rstd and invD = 1.0f / D:
+//   gg = gy * gamma; xh = (x - S*invD) * rstd
+//   s1 = sum gg, s2 = sum gg * xh                        (row reductions)
+//   dx = ((gg - s1*invD) - xh * (s2*invD)) * rstd        (reference op order)
+//   dgamma[d] = sum_r gy * xh, dbeta[d] = sum_r gy       (column reductions)
+// One wave per row with gy and x in registers (NV float4 per lane, D <=
+// 256 NV).  The column sums go into LDS accumulators: the workgroup's four
+// waves take four consecutive rows, and add them in row order (one barrier
+// per wave turn), so each column of a workgroup's partial is the sequential
+// sum of its contiguous row block.  Partials go to [grid][2][D].
+// ---------------------------------------------------------------------------
+struct LnBwdArgs {
+  const float *gy;
+  const float *x;
+  const float *gamma;
+  const float *mean_sum;
+  const float *rstd;
+  float *dx;       // may be null
+  float *partial;  // [grid][2][D]
+  int64_t sgy, sx, sdx;
+  int rows, D;
+  float invD;
+};
+
+template <int NV, bool FULL>
+__global__ __launch_bounds__(256) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
+#pragma clang fp contract(off)
+  __shared__ f32x4 sgam[64 * NV], acc_g[64 * NV], acc_b[64 * NV];
+  const int nv4 = a.D >> 2;
+  const f32x4 *gam4 = reinterpret_cast<const f32x4 *>(a.gamma);
+  for (int c = threadIdx.x; c < nv4; c += 256) {
+    sgam[c] = gam4[c];
+    acc_g[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc_b[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  auto in_row = [&](int c) __attribute__((always_inline)) { return FULL || c < nv4; };
+  const int per_wg = (a.rows + gridDim.x - 1) / gridDim.x;
+  const int row0 = min(a.rows, (int)blockIdx.x * per_wg);
+  const int row_end = min(a.rows, row0 + per_wg);
+  for (int rb = row0; rb < row_end; rb += 4) {
+    const int row = rb + wave;
+    const bool live = row < row_end;
+    f32x4 g[NV], xv[NV];
+    const f32x4 *gr = reinterpret_cast<const f32x4 *>(a.gy + (int64_t)(live ? row : row0) * a.sgy);
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)(live ? row : row0) * a.sx);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      const bool ok = live && in_row(c);
+      g[i] = ok ? __builtin_nontemporal_load(gr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      xv[i] = ok ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float mean = live ? a.mean_sum[row] * a.invD : 0.0f;
+    const float rs = live ? a.rstd[row] : 0.0f;
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const f32x4 gm = sgam[in_row(lane + 64 * i) ? lane + 64 * i : 0];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float gg = g[i][e] * gm[e];
+        const float xh = (xv[i][e] - mean) * rs;
+        s1 = s1 + gg;
+        s2 = s2 + gg * xh;
+      }
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    const float ms1 = s1 * a.invD, ms2 = s2 * a.invD;
+    if (live && a.dx) {
+      f32x4 *dr = reinterpret_cast<f32x4 *>(a.dx + (int64_t)row * a.sdx);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        if (in_row(c)) {
+          const f32x4 gm = sgam[c];
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float gg = g[i][e] * gm[e];
+            const float xh = (xv[i][e] - mean) * rs;
+            const float t1 = gg - ms1;
+            const float t2 = xh * ms2;
+            o[e] = (t1 - t2) * rs;
+          }
+          __builtin_nontemporal_store(o, dr + c);
+        }
+      }
+    }
+    // Column sums, in row order: wave w adds row rb + w on its turn.
+#pragma unroll 1
+    for (int turn = 0; turn < 4; ++turn) {
+      __syncthreads();
+      if (turn == wave && live) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int c = lane + 64 * i;
+          if (in_row(c)) {
+            f32x4 ag = acc_g[c], ab = acc_b[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float xh = (xv[i][e] - mean) * rs;
+              ag[e] = ag[e] + g[i][e] * xh;
+              ab[e] = ab[e] + g[i][e];
+            }
+            acc_g[c] = ag;
+            acc_b[c] = ab;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  f32x4 *pg = reinterpret_cast<f32x4 *>(a.partial + (int64_t)blockIdx.x * 2 * a.D);
+  f32x4 *pb = reinterpret_cast<f32x4 *>(a.partial + (int64_t)blockIdx.x * 2 * a.D + a.D);
+  for (int c = threadIdx.x; c < nv4; c += 256) {
+    pg[c] = acc_g[c];
+    pb[c] = acc_b[c];
+  }
+}
+
+// Any D (no alignment): one wave per row, elements strided by the lane; the
+// column sums go through the same ordered LDS accumulation (D <= 8192 so
+// the accumulators fit), two passes over the row (the second from cache).
+constexpr int kAnyMaxD = 8192;
+
+__global__ __launch_bounds__(256) void layer_norm_bwd_any_kernel(LnBwdArgs a) {
+#pragma clang fp contract(off)
+  __shared__ float acc_g[kAnyMaxD], acc_b[kAnyMaxD];
+  for (int d = threadIdx.x; d < a.D; d += 256) {
+    acc_g[d] = 0.0f;
+    acc_b[d] = 0.0f;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int per_wg = (a.rows + gridDim.x - 1) / gridDim.x;
+  const int row0 = min(a.rows, (int)blockIdx.x * per_wg);
+  const int row_end = min(a.rows, row0 + per_wg);
+  for (int rb = row0; rb < row_end; rb += 4) {
+    const int row = rb + wave;
+    const bool live = row < row_end;
+    const float *gr = a.gy + (int64_t)(live ? row : row0) * a.sgy;
+    const float *xr = a.x + (int64_t)(live ? row : row0) * a.sx;
+    const float mean = live ? a.mean_sum[row] * a.invD : 0.0f;
+    const float rs = live ? a.rstd[row] : 0.0f;
+    float s1 = 0.0f, s2 = 0.0f;
+    if (live) {
+      for (int d = lane; d < a.D; d += 64) {
+        const float gg = gr[d] * a.gamma[d];
+        const float xh = (xr[d] - mean) * rs;
+        s1 = s1 + gg;
+        s2 = s2 + gg * xh;
+      }
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    const float ms1 = s1 * a.invD, ms2 = s2 * a.invD;
+    if (live && a.dx) {
+      float *dr = a.dx + (int64_t)row * a.sdx;
+      for (int d = lane; d < a.D; d += 64) {
+        const float gg = gr[d] * a.gamma[d];
+        const float xh = (xr[d] - mean) * rs;
+        const float t1 = gg - ms1;
+        const float t2 = xh * ms2;
+        dr[d] = (t1 - t2) * rs;
+      }
+    }
+#pragma unroll 1
+    for (int turn = 0; turn < 4; ++turn) {
+      __syncthreads();
+      if (turn == wave && live) {
+        for (int d = lane; d < a.D; d += 64) {
+          const float xh = (xr[d] - mean) * rs;
+          acc_g[d] = acc_g[d] + gr[d] * xh;
+          acc_b[d] = acc_b[d] + gr[d];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  float *pg = a.partial + (int64_t)blockIdx.x * 2 * a.D;
+  for (int d = threadIdx.x; d < a.D; d += 256) {
+    pg[d] = acc_g[d];
+    pg[a.D + d] = acc_b[d];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Column sums of a [rows, cols] matrix (f32 / bf16 / f16), stage 1: workgroup
+// (x, y) sums rows [y*chunk, (y+1)*chunk) of columns [256x, 256x+256) in row
+// order, one column per thread, into part[y][cols] (f32).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void col_sum_partial_kernel(const void *in, int64_t ld, int rows,
+                                                              int cols, int chunk, float *part) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  const int r0 = blockIdx.y * chunk;
+  const int r1 = min(rows, r0 + chunk);
+  float acc = 0.0f;
+  for (int r = r0; r < r1; ++r) {
+    const int64_t i = (int64_t)r * ld + c;
+    float v;
+    if constexpr (DT == NOVA_HIP_DT_F32) {
+      v = static_cast<const float *>(in)[i];
+    } else {
+      const uint16_t h = static_cast<const uint16_t *>(in)[i];
+      if constexpr (DT == NOVA_HIP_DT_BF16) v = __uint_as_float((uint32_t)h << 16);
+      else v = (float)__builtin_bit_cast(_Float16, h);
+    }
+    acc = v + acc;
+  }
+  part[(int64_t)blockIdx.y * cols + c] = acc;
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Stage 2 (shared by the LayerNorm and bias gradients): out_k[c] =
+// sum_p part[p][k][c] over the np partials in order, for the nk outputs k
+// of each partial (stride np_stride elements between partials), stored in
+// dtype odt.  Thread per (k, c).
+__global__ __launch_bounds__(256) void col_reduce_kernel(const float *part, int np, int nk,
+                                                         int cols, int64_t p_stride, void *out0,
+                                                         void *out1, int odt) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= nk * cols) return;
+  const int k = idx / cols, c = idx - k * cols;
+  const float *p = part + (int64_t)k * cols + c;
+  float acc = 0.0f;
+  int i = 0;
+  // Loads issued eight ahead; the sum stays sequential in partial order.
+  for (; i + 8 <= np; i += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(i + u) * p_stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = acc + v[u];
+  }
+  for (; i < np; ++i) acc = acc + p[(int64_t)i * p_stride];
+  void *out = k == 0 ? out0 : out1;
+  if (!out) return;
+  if (odt == NOVA_HIP_DT_F32) static_cast<float *>(out)[c] = acc;
+  else if (odt == NOVA_HIP_DT_BF16) static_cast<uint16_t *>(out)[c] = f32_to_bf16(acc);
+  else static_cast<uint16_t *>(out)[c] = __builtin_bit_cast(uint16_t, (_Float16)acc);
+}
+
+// Two-level reduction of np partials when np is large: groups of kGroup
+// partials are summed in order into np / kGroup second-level partials.
+constexpr int kGroup = 32;
+
+__global__ __launch_bounds__(256) void col_group_kernel(const float *part, int np, int width,
+                                                        float *out) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= width) return;
+  const int g = blockIdx.y;
+  const int p0 = g * kGroup, p1 = min(np, p0 + kGroup);
+  float acc = 0.0f;
+  for (int p = p0; p < p1; ++p) acc = acc + part[(int64_t)p * width + idx];
+  out[(int64_t)g * width + idx] = acc;
+}
+
+// Final column reduction of np partials, each `width` = nk * cols floats
+// ([np][nk][cols]); uses ws2 (np / kGroup + 1) * width floats when np is
+// large.
+int32_t reduce_partials(const float *part, int np, int nk, int cols, void *out0, void *out1,
+                        int odt, float *ws2, hipStream_t s) {
+  const int width = nk * cols;
+  const unsigned blocks = (unsigned)((width + 255) / 256);
+  if (np > 2 * kGroup) {
+    const int ng = (np + kGroup - 1) / kGroup;
+    hipLaunchKernelGGL(col_group_kernel, dim3(blocks, (unsigned)ng), dim3(256), 0, s, part, np,
+                       width, ws2);
+    int32_t rc = check_hip(hipGetLastError(), "column group launch");
+    if (rc) return rc;
+    part = ws2;
+    np = ng;
+  }
+  hipLaunchKernelGGL(col_reduce_kernel, dim3(blocks), dim3(256), 0, s, part, np, nk, cols,
+                     (int64_t)width, out0, out1, odt);
+  return check_hip(hipGetLastError(), "column reduce launch");
+}
+
+}  // namespace
+
+int32_t launch_sce_backward(const SceBackwardProblem &p, hipStream_t s) {
+  if (p.rows == 0) return NOVA_HIP_SUCCESS;
+  if (p.rows > 0x7fffffff || p.C > 0x7fffffff - 4096)
+    return fail(NOVA_HIP_ERANGE, "sce_backward: size exceeds 2^31-1");
+  SceBwdArgs a;
+  a.softmax = p.softmax;
+  a.labels = p.labels;
+  a.grad = p.grad;
+  a.ss = p.ss;
+  a.sg = p.sg;
+  a.rows = (int)p.rows;
+  a.C = (int)p.C;
+  a.invN = (float)(1.0 / (double)p.rows);
+  const bool vec = aligned16(p.softmax) && aligned16(p.grad) && p.ss % 4 == 0 && p.sg % 4 == 0;
+  // Rows beyond 65535 go in several launches (grid y limit).
+  for (int64_t r0 = 0; r0 < p.rows; r0 += 65535) {
+    const int64_t nr = p.rows - r0 < 65535 ? p.rows - r0 : 65535;
+    SceBwdArgs b = a;
+    b.softmax = p.softmax + r0 * p.ss;
+    b.grad = p.grad + r0 * p.sg;
+    b.labels = p.labels + r0;
+    if (vec) {
+      const unsigned gx = (unsigned)((p.C / 4 + 256 * kU - 1) / (256 * kU));
+      hipLaunchKernelGGL(sce_backward_kernel<true>, dim3(gx > 0 ? gx : 1, (unsigned)nr),
+                         dim3(256), 0, s, b);
+    } else {
+      const unsigned gx = (unsigned)((p.C + 256 * kU * 4 - 1) / (256 * kU * 4));
+      hipLaunchKernelGGL(sce_backward_kernel<false>, dim3(gx, (unsigned)nr), dim3(256), 0, s, b);
+    }
+    int32_t rc = check_hip(hipGetLastError(), "sce_backward launch");
+    if (rc) return rc;
+  }
+  return NOVA_HIP_SUCCESS;
+}
+
+int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_t s) {
+  // The column accumulators of a workgroup live in LDS: rows up to 8192.
+  if (p.rows > 0x7fffffff - 4 || p.D > kAnyMaxD)
+    return fail(NOVA_HIP_ERANGE, "layer_norm_backward: D = %lld exceeds %d", (long long)p.D,
+                kAnyMaxD);
+  const bool vec = p.D % 4 == 0 && p.sgy % 4 == 0 && p.sx % 4 == 0 && (!p.dx || p.sdx % 4 == 0) &&
+                   aligned16(p.gy) && aligned16(p.x) && aligned16(p.gamma) &&
+                   (!p.dx || aligned16(p.dx));
+  // Persistent grid: 3 workgroups per CU (registers: gy and x rows), each
+  // one contiguous row block.
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const int64_t want = (p.rows + 3) / 4;
+  const int grid = (int)(want < 3 * cus ? (want > 0 ? want : 1) : 3 * cus);
+  const int ng = (grid + kGroup - 1) / kGroup;
+  const size_t part_floats = (size_t)grid * 2 * p.D;
+  const size_t ws_floats = part_floats + (size_t)(ng + 1) * 2 * p.D;
+  float *ws = static_cast<float *>(workspace(s, ws_floats * 4));
+  if (!ws) return NOVA_HIP_ENOMEM;
+  LnBwdArgs a;
+  a.gy = p.gy;
+  a.x = p.x;
+  a.gamma = p.gamma;
+  a.mean_sum = p.mean_sum;
+  a.rstd = p.rstd;
+  a.dx = p.dx;
+  a.partial = ws;
+  a.sgy = p.sgy;
+  a.sx = p.sx;
+  a.sdx = p.sdx;
+  a.rows = (int)p.rows;
+  a.D = (int)p.D;
+  a.invD = 1.0f / (float)p.D;
+  if (vec && p.D == 1024)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<4, true>), dim3(grid), dim3(256), 0, s, a);
+  else if (vec && p.D <= 1024)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<4, false>), dim3(grid), dim3(256), 0, s, a);
+  else if (vec && p.D == 4096)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<16, true>), dim3(grid), dim3(256), 0, s, a);
+  else if (vec && p.D <= 4096)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<16, false>), dim3(grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(layer_norm_bwd_any_kernel, dim3(grid), dim3(256), 0, s, a);
+  int32_t rc = check_hip(hipGetLastError(), "layer_norm_backward launch");
+  if (rc) return rc;
+  if (!p.dgamma && !p.dbeta) return NOVA_HIP_SUCCESS;
+  return reduce_partials(ws, grid, 2, (int)p.D, p.dgamma, p.dbeta, NOVA_HIP_DT_F32,
+                         ws + part_floats, s);
+}
+
+int32_t launch_col_sum(const ColSumProblem &p, hipStream_t s) {
+  if (p.cols == 0) return NOVA_HIP_SUCCESS;
+  if (p.rows > 0x7fffffff || p.cols > 0x7fffffff - 256)
+    return fail(NOVA_HIP_ERANGE, "column sum: size exceeds 2^31-1");
+  // Row chunks of 64 (at most 65535 of them).
+  int64_t chunk = 64;
+  while ((p.rows + chunk - 1) / chunk > 65535) chunk *= 2;
+  const int nch = (int)((p.rows + chunk - 1) / chunk > 0 ? (p.rows + chunk - 1) / chunk : 1);
+  const int ng = (nch + kGroup - 1) / kGroup;
+  const size_t part_floats = (size_t)nch * p.cols;
+  float *ws = static_cast<float *>(workspace(s, (part_floats + (size_t)(ng + 1) * p.cols) * 4));
+  if (!ws) return NOVA_HIP_ENOMEM;
+  const dim3 g1((unsigned)((p.cols + 255) / 256), (unsigned)nch);
+  if (p.in_dt == NOVA_HIP_DT_F32)
+    hipLaunchKernelGGL(col_sum_partial_kernel<NOVA_HIP_DT_F32>, g1, dim3(256), 0, s, p.in, p.ld,
+                       (int)p.rows, (int)p.cols, (int)chunk, ws);
+  else if (p.in_dt == NOVA_HIP_DT_BF16)
+    hipLaunchKernelGGL(col_sum_partial_kernel<NOVA_HIP_DT_BF16>, g1, dim3(256), 0, s, p.in, p.ld,
+                       (int)p.rows, (int)p.cols, (int)chunk, ws);
+  else
+    hipLaunchKernelGGL(col_sum_partial_kernel<NOVA_HIP_DT_F16>, g1, dim3(256), 0, s, p.in, p.ld,
+                       (int)p.rows, (int)p.cols, (int)chunk, ws);
+  int32_t rc = check_hip(hipGetLastError(), "column sum launch");
+  if (rc) return rc;
+  return reduce_partials(ws, nch, 1, (int)p.cols, p.out, nullptr, p.out_dt, ws + part_floats, s);
+}
+
+}  // namespace nova_hip

@@ -234,6 +234,83 @@ int32_t gemm2d(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C,
   return gemm_core(&a, &b, &c, bias, flags);
 }
 
+NovaMemRef2D transposed(const NovaMemRef2D *d) {
+  NovaMemRef2D r = *d;
+  r.sizes[0] = d->sizes[1];
+  r.sizes[1] = d->sizes[0];
+  r.strides[0] = d->strides[1];
+  r.strides[1] = d->strides[0];
+  return r;
+}
+
+// C = A . B into C as laid out: row-major C directly; a transposed view of
+// a row-major buffer (unit stride on dim 0) as C^T = B^T . A^T into that
+// buffer, since the kernels store rows with unit stride.
+int32_t gemm2d_to(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C, int32_t flags) {
+  if (C && C->strides[1] != 1 && C->sizes[1] > 1 && (C->strides[0] == 1 || C->sizes[0] <= 1)) {
+    NovaMemRef2D at = transposed(A), bt = transposed(B), ct = transposed(C);
+    return gemm2d(&bt, &at, &ct, nullptr, flags);
+  }
+  return gemm2d(A, B, C, nullptr, flags);
+}
+
+// Flags of the backward GEMM entry points: dtypes only, no epilogue.
+int32_t backward_flags(int32_t flags, int &in_dt, int &out_dt, const char *what) {
+  int epi, bias_dt;
+  int32_t rc = decode_flags(flags, in_dt, out_dt, epi, bias_dt);
+  if (rc) return rc;
+  if (epi != NOVA_HIP_EPI_NONE)
+    return fail(NOVA_HIP_EINVAL, "%s: flags carry an epilogue (0x%x)", what, flags);
+  return NOVA_HIP_SUCCESS;
+}
+
+// Shared validation of the SCE forward entry points (optional softmax and
+// fused gradient outputs).
+int32_t sce_common(const NovaMemRef2D *logits, const NovaMemRef1D *labels, NovaMemRef1D *loss,
+                   NovaMemRef2D *softmax, NovaMemRef2D *grad, const char *what) {
+  clear_error();
+  if (!logits || !labels || !loss) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", what);
+  const int64_t R = logits->sizes[0], C = logits->sizes[1];
+  if (R < 0 || C < 0) return fail(NOVA_HIP_ESHAPE, "%s: negative size", what);
+  if (labels->sizes[0] != R) return fail(NOVA_HIP_ESHAPE, "%s: labels size != rows", what);
+  if (loss->sizes[0] != 1) return fail(NOVA_HIP_ESHAPE, "%s: loss must have shape [1]", what);
+  if (softmax && (softmax->sizes[0] != R || softmax->sizes[1] != C))
+    return fail(NOVA_HIP_ESHAPE, "%s: softmax shape differs from logits", what);
+  if (grad && (grad->sizes[0] != R || grad->sizes[1] != C))
+    return fail(NOVA_HIP_ESHAPE, "%s: grad shape differs from logits", what);
+  if (C == 0 && R > 0) return fail(NOVA_HIP_ESHAPE, "%s: zero classes", what);
+  if ((logits->strides[1] != 1 && C > 1) || (labels->strides[0] != 1 && R > 1) ||
+      (softmax && softmax->strides[1] != 1 && C > 1) || (grad && grad->strides[1] != 1 && C > 1))
+    return fail(NOVA_HIP_ESTRIDE, "%s: last dim must be contiguous", what);
+  if (R > 1 && (logits->strides[0] < C || (softmax && softmax->strides[0] < C) ||
+                (grad && grad->strides[0] < C)))
+    return fail(NOVA_HIP_ESTRIDE, "%s: rows overlap", what);
+  if (!loss->aligned || (R > 0 && (!logits->aligned || !labels->aligned)) ||
+      (softmax && !softmax->aligned) || (grad && !grad->aligned))
+    return fail(NOVA_HIP_EINVAL, "%s: null data pointer", what);
+  SceProblem p;
+  p.logits = reinterpret_cast<const float *>(data_of(logits)) + logits->offset;
+  p.labels = reinterpret_cast<const int32_t *>(data_of(labels)) + labels->offset;
+  p.loss = reinterpret_cast<float *>(const_cast<char *>(data_of(loss))) + loss->offset;
+  p.softmax = softmax ? reinterpret_cast<float *>(const_cast<char *>(data_of(softmax))) + softmax->offset : nullptr;
+  p.grad = grad ? reinterpret_cast<float *>(const_cast<char *>(data_of(grad))) + grad->offset : nullptr;
+  p.rows = R;
+  p.C = C;
+  p.sx = logits->strides[0];
+  p.ssm = softmax ? softmax->strides[0] : 0;
+  p.sg = grad ? grad->strides[0] : 0;
+  return launch_sce(p, current_stream());
+}
+
+template <typename D>
+float *out_f32(D *d) {
+  return reinterpret_cast<float *>(const_cast<char *>(data_of(d))) + d->offset;
+}
+template <typename D>
+const float *in_f32(const D *d) {
+  return reinterpret_cast<const float *>(data_of(d)) + d->offset;
+}
+
 }  // namespace
 }  // namespace nova_hip
 
@@ -343,33 +420,168 @@ int32_t _mlir_ciface_nova_hip_layer_norm_f32(const NovaMemRef2D *x, const NovaMe
 
 int32_t _mlir_ciface_nova_hip_sce_f32(const NovaMemRef2D *logits, const NovaMemRef1D *labels,
                                       NovaMemRef1D *loss, NovaMemRef2D *softmax) {
+  return sce_common(logits, labels, loss, softmax, nullptr, "sce");
+}
+
+int32_t _mlir_ciface_nova_hip_sce_fwd_bwd_f32(const NovaMemRef2D *logits,
+                                              const NovaMemRef1D *labels, NovaMemRef1D *loss,
+                                              NovaMemRef2D *grad) {
+  if (!grad) {
+    clear_error();
+    return fail(NOVA_HIP_EINVAL, "sce_fwd_bwd: null grad descriptor");
+  }
+  return sce_common(logits, labels, loss, nullptr, grad, "sce_fwd_bwd");
+}
+
+int32_t _mlir_ciface_nova_hip_sce_backward_f32(const NovaMemRef2D *softmax,
+                                               const NovaMemRef1D *labels, NovaMemRef2D *grad) {
   clear_error();
-  if (!logits || !labels || !loss) return fail(NOVA_HIP_EINVAL, "sce: null descriptor");
-  const int64_t R = logits->sizes[0], C = logits->sizes[1];
-  if (R < 0 || C < 0) return fail(NOVA_HIP_ESHAPE, "sce: negative size");
-  if (labels->sizes[0] != R) return fail(NOVA_HIP_ESHAPE, "sce: labels size != rows");
-  if (loss->sizes[0] != 1) return fail(NOVA_HIP_ESHAPE, "sce: loss must have shape [1]");
-  if (softmax && (softmax->sizes[0] != R || softmax->sizes[1] != C))
-    return fail(NOVA_HIP_ESHAPE, "sce: softmax shape differs from logits");
-  if (C == 0 && R > 0) return fail(NOVA_HIP_ESHAPE, "sce: zero classes");
-  if ((logits->strides[1] != 1 && C > 1) || (labels->strides[0] != 1 && R > 1) ||
-      (softmax && softmax->strides[1] != 1 && C > 1))
-    return fail(NOVA_HIP_ESTRIDE, "sce: last dim must be contiguous");
-  if (R > 1 && (logits->strides[0] < C || (softmax && softmax->strides[0] < C)))
-    return fail(NOVA_HIP_ESTRIDE, "sce: rows overlap");
-  if (!loss->aligned || (R > 0 && (!logits->aligned || !labels->aligned)) ||
-      (softmax && !softmax->aligned))
-    return fail(NOVA_HIP_EINVAL, "sce: null data pointer");
-  SceProblem p;
-  p.logits = reinterpret_cast<const float *>(data_of(logits)) + logits->offset;
+  if (!softmax || !labels || !grad) return fail(NOVA_HIP_EINVAL, "sce_backward: null descriptor");
+  const int64_t R = softmax->sizes[0], C = softmax->sizes[1];
+  if (R < 0 || C < 0) return fail(NOVA_HIP_ESHAPE, "sce_backward: negative size");
+  if (labels->sizes[0] != R) return fail(NOVA_HIP_ESHAPE, "sce_backward: labels size != rows");
+  if (grad->sizes[0] != R || grad->sizes[1] != C)
+    return fail(NOVA_HIP_ESHAPE, "sce_backward: grad shape differs from softmax");
+  if (R == 0 || C == 0) return NOVA_HIP_SUCCESS;
+  if ((softmax->strides[1] != 1 && C > 1) || (grad->strides[1] != 1 && C > 1) ||
+      (labels->strides[0] != 1 && R > 1))
+    return fail(NOVA_HIP_ESTRIDE, "sce_backward: last dim must be contiguous");
+  if (R > 1 && (softmax->strides[0] < C || grad->strides[0] < C))
+    return fail(NOVA_HIP_ESTRIDE, "sce_backward: rows overlap");
+  if (!softmax->aligned || !labels->aligned || !grad->aligned)
+    return fail(NOVA_HIP_EINVAL, "sce_backward: null data pointer");
+  SceBackwardProblem p;
+  p.softmax = in_f32(softmax);
   p.labels = reinterpret_cast<const int32_t *>(data_of(labels)) + labels->offset;
-  p.loss = reinterpret_cast<float *>(const_cast<char *>(data_of(loss))) + loss->offset;
-  p.softmax = softmax ? reinterpret_cast<float *>(const_cast<char *>(data_of(softmax))) + softmax->offset : nullptr;
+  p.grad = out_f32(grad);
   p.rows = R;
   p.C = C;
-  p.sx = logits->strides[0];
-  p.ssm = softmax ? softmax->strides[0] : 0;
-  return launch_sce(p, current_stream());
+  p.ss = softmax->strides[0];
+  p.sg = grad->strides[0];
+  return launch_sce_backward(p, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_layer_norm_backward_f32(
+    const NovaMemRef2D *grad_y, const NovaMemRef2D *x, const NovaMemRef1D *gamma,
+    const NovaMemRef1D *mean_sum, const NovaMemRef1D *rstd, NovaMemRef2D *dx,
+    NovaMemRef1D *dgamma, NovaMemRef1D *dbeta) {
+  clear_error();
+  const char *w = "layer_norm_backward";
+  if (!grad_y || !x || !gamma || !mean_sum || !rstd)
+    return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  const int64_t R = x->sizes[0], D = x->sizes[1];
+  if (R < 0 || D < 0) return fail(NOVA_HIP_ESHAPE, "%s: negative size", w);
+  if (grad_y->sizes[0] != R || grad_y->sizes[1] != D || (dx && (dx->sizes[0] != R || dx->sizes[1] != D)))
+    return fail(NOVA_HIP_ESHAPE, "%s: grad_y / dx shape differs from x", w);
+  if (gamma->sizes[0] != D || (dgamma && dgamma->sizes[0] != D) || (dbeta && dbeta->sizes[0] != D))
+    return fail(NOVA_HIP_ESHAPE, "%s: gamma / dgamma / dbeta size != D", w);
+  if (mean_sum->sizes[0] != R || rstd->sizes[0] != R)
+    return fail(NOVA_HIP_ESHAPE, "%s: mean_sum / rstd size != rows", w);
+  if (D == 0) return fail(NOVA_HIP_ESHAPE, "%s: empty normalised dim", w);
+  if ((x->strides[1] != 1 && D > 1) || (grad_y->strides[1] != 1 && D > 1) ||
+      (dx && dx->strides[1] != 1 && D > 1) || (gamma->strides[0] != 1 && D > 1) ||
+      (dgamma && dgamma->strides[0] != 1 && D > 1) || (dbeta && dbeta->strides[0] != 1 && D > 1))
+    return fail(NOVA_HIP_ESTRIDE, "%s: last dim must be contiguous", w);
+  if ((mean_sum->strides[0] != 1 || rstd->strides[0] != 1) && R > 1)
+    return fail(NOVA_HIP_ESTRIDE, "%s: stats must be contiguous", w);
+  if (R > 1 && (x->strides[0] < D || grad_y->strides[0] < D || (dx && dx->strides[0] < D)))
+    return fail(NOVA_HIP_ESTRIDE, "%s: rows overlap", w);
+  if (!gamma->aligned || (dgamma && !dgamma->aligned) || (dbeta && !dbeta->aligned) ||
+      (R > 0 && (!x->aligned || !grad_y->aligned || !mean_sum->aligned || !rstd->aligned ||
+                 (dx && !dx->aligned))))
+    return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+  LayerNormBackwardProblem p;
+  p.gy = in_f32(grad_y);
+  p.x = in_f32(x);
+  p.gamma = in_f32(gamma);
+  p.mean_sum = in_f32(mean_sum);
+  p.rstd = in_f32(rstd);
+  p.dx = dx ? out_f32(dx) : nullptr;
+  p.dgamma = dgamma ? out_f32(dgamma) : nullptr;
+  p.dbeta = dbeta ? out_f32(dbeta) : nullptr;
+  p.rows = R;
+  p.D = D;
+  p.sgy = grad_y->strides[0];
+  p.sx = x->strides[0];
+  p.sdx = dx ? dx->strides[0] : 0;
+  return launch_layer_norm_backward(p, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_linear_backward(const NovaMemRef2D *grad_out, const NovaMemRef2D *x,
+                                              const NovaMemRef2D *weight,
+                                              NovaMemRef2D *grad_input,
+                                              NovaMemRef2D *grad_weight,
+                                              NovaMemRef1D *grad_bias, int32_t flags) {
+  clear_error();
+  const char *w = "linear_backward";
+  if (!grad_out || !x || !weight) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  int in_dt, out_dt;
+  int32_t rc = backward_flags(flags, in_dt, out_dt, w);
+  if (rc) return rc;
+  const int64_t M = x->sizes[0], K = x->sizes[1], N = weight->sizes[1];
+  if (weight->sizes[0] != K || grad_out->sizes[0] != M || grad_out->sizes[1] != N)
+    return fail(NOVA_HIP_ESHAPE, "%s: x [%lld,%lld], weight [%lld,%lld], grad_out [%lld,%lld]",
+                w, (long long)M, (long long)K, (long long)weight->sizes[0], (long long)N,
+                (long long)grad_out->sizes[0], (long long)grad_out->sizes[1]);
+  // grad_input [M,K] = grad_out . weight^T  (NovaToLinalgGeneric.cpp:1867-1911)
+  if (grad_input) {
+    NovaMemRef2D wt = transposed(weight);
+    if ((rc = gemm2d_to(grad_out, &wt, grad_input, flags))) return rc;
+  }
+  // grad_weight [K,N] = x^T . grad_out  (:1913-1968)
+  if (grad_weight) {
+    NovaMemRef2D xt = transposed(x);
+    if ((rc = gemm2d_to(&xt, grad_out, grad_weight, flags))) return rc;
+  }
+  // grad_bias [N] = column sums of grad_out  (:1970-1989)
+  if (grad_bias) {
+    clear_error();
+    if (grad_bias->sizes[0] != N) return fail(NOVA_HIP_ESHAPE, "%s: grad_bias size != N", w);
+    if (grad_bias->strides[0] != 1 && N > 1)
+      return fail(NOVA_HIP_ESTRIDE, "%s: grad_bias must be contiguous", w);
+    if (grad_out->strides[1] != 1 && N > 1)
+      return fail(NOVA_HIP_ESTRIDE, "%s: grad_out must have unit stride on N for grad_bias", w);
+    if (M > 1 && grad_out->strides[0] < N) return fail(NOVA_HIP_ESTRIDE, "%s: grad_out rows overlap", w);
+    if (N > 0 && (!grad_bias->aligned || (M > 0 && !grad_out->aligned)))
+      return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+    ColSumProblem p;
+    p.in = data_of(grad_out) + grad_out->offset * dtype_size(in_dt);
+    p.out = const_cast<char *>(data_of(grad_bias)) + grad_bias->offset * dtype_size(out_dt);
+    p.rows = M;
+    p.cols = N;
+    p.ld = grad_out->strides[0];
+    p.in_dt = in_dt;
+    p.out_dt = out_dt;
+    if ((rc = launch_col_sum(p, current_stream()))) return rc;
+  }
+  return NOVA_HIP_SUCCESS;
+}
+
+int32_t _mlir_ciface_nova_hip_matmul_backward(const NovaMemRef2D *grad, const NovaMemRef2D *A,
+                                              const NovaMemRef2D *B, NovaMemRef2D *grad_a,
+                                              NovaMemRef2D *grad_b, int32_t flags) {
+  clear_error();
+  const char *w = "matmul_backward";
+  if (!grad || !A || !B) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  int in_dt, out_dt;
+  int32_t rc = backward_flags(flags, in_dt, out_dt, w);
+  if (rc) return rc;
+  const int64_t M = A->sizes[0], K = A->sizes[1], N = B->sizes[1];
+  if (B->sizes[0] != K || grad->sizes[0] != M || grad->sizes[1] != N)
+    return fail(NOVA_HIP_ESHAPE, "%s: A [%lld,%lld], B [%lld,%lld], grad [%lld,%lld]", w,
+                (long long)M, (long long)K, (long long)B->sizes[0], (long long)N,
+                (long long)grad->sizes[0], (long long)grad->sizes[1]);
+  // grad_a [M,K] = grad . B^T; grad_b [K,N] = A^T . grad
+  // (NovaMatmulBackwardPattern, NovaToLinalgGeneric.cpp:160-239)
+  if (grad_a) {
+    NovaMemRef2D bt = transposed(B);
+    if ((rc = gemm2d_to(grad, &bt, grad_a, flags))) return rc;
+  }
+  if (grad_b) {
+    NovaMemRef2D at = transposed(A);
+    if ((rc = gemm2d_to(&at, grad, grad_b, flags))) return rc;
+  }
+  return NOVA_HIP_SUCCESS;
 }
 
 void nova_hip_set_stream(void *stream) { t_stream = static_cast<hipStream_t>(stream); }

@@ -65,10 +65,45 @@ struct SceProblem {
   const int32_t *labels;
   float *loss;
   float *softmax;  // may be null
+  float *grad;     // may be null: (softmax - onehot) / rows, the fused backward
   int64_t rows, C;
-  int64_t sx, ssm;  // row strides (elements)
+  int64_t sx, ssm, sg;  // row strides (elements)
 };
 int32_t launch_sce(const SceProblem &p, hipStream_t s);
+
+// ---- backward (backward.hip) ------------------------------------------------
+struct SceBackwardProblem {
+  const float *softmax;
+  const int32_t *labels;
+  float *grad;
+  int64_t rows, C;
+  int64_t ss, sg;  // row strides (elements)
+};
+int32_t launch_sce_backward(const SceBackwardProblem &p, hipStream_t s);
+
+struct LayerNormBackwardProblem {
+  const float *gy;
+  const float *x;
+  const float *gamma;
+  const float *mean_sum;
+  const float *rstd;
+  float *dx;      // may be null
+  float *dgamma;  // may be null
+  float *dbeta;   // may be null
+  int64_t rows, D;
+  int64_t sgy, sx, sdx;  // row strides (elements)
+};
+int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_t s);
+
+// out[c] = sum_r in[r, c] (rows in order within chunks, chunks in order),
+// in of dtype in_dt with row stride ld, out of dtype out_dt.
+struct ColSumProblem {
+  const void *in;
+  void *out;
+  int64_t rows, cols, ld;
+  int in_dt, out_dt;
+};
+int32_t launch_col_sum(const ColSumProblem &p, hipStream_t s);
 
 // Per-stream device workspace owned by the library.  Returns null and sets
 // the error text on failure.  The pointer stays valid until the next call

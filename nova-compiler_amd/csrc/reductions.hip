@@ -157,10 +157,21 @@ struct SceArgs {
   const int32_t *labels;
   float *loss;
   float *softmax;
+  float *grad;          // fused nova.sce_backward output, or null
   float *row_loss;      // workspace [rows]
-  int64_t sx, ssm;
+  int64_t sx, ssm, sg;
   int rows, C;
+  float invN;           // f32 rounding of 1.0 / rows (NovaToLinalgGeneric.cpp:1121-1125)
 };
+
+// Gradient of the mean loss for one element from its softmax value sm:
+// (sm + (-1 at the label)) * invN, the arithmetic of nova.sce_backward
+// (NovaToLinalgGeneric.cpp:1102-1128) applied to the softmax this kernel
+// would store.  A label outside [0, C) gives NaN.
+__device__ __forceinline__ float sce_grad(float sm, bool at_label, bool bad, float invN) {
+  const float d = at_label ? sm + -1.0f : sm;
+  return bad ? __builtin_nanf("") : d * invN;
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -236,6 +247,13 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
     if (a.softmax) {
       float *sr = a.softmax + (int64_t)row * a.ssm;
       for (int c = lane; c < a.C; c += 64) sr[c] = exp_shifted(xr[c], gm) / safe;
+    }
+    if (a.grad) {
+      const int t = a.labels[row];
+      const bool bad = t < 0 || t >= a.C;
+      float *gr = a.grad + (int64_t)row * a.sg;
+      for (int c = lane; c < a.C; c += 64)
+        gr[c] = sce_grad(exp_shifted(xr[c], gm) / safe, c == t, bad, a.invN);
     }
     if (lane == 0) {
       const int t = a.labels[row];
@@ -324,6 +342,26 @@ __global__ __launch_bounds__(kRowThreads) void sce_row_kernel(SceArgs a) {
     if (tid == 0)
       for (int c = n4 * 4; c < a.C; ++c) sr[c] = exp_shifted(xr[c], gm) / safe;
   }
+  if (a.grad) {
+    const int t = a.labels[row];
+    const bool bad = t < 0 || t >= a.C;
+    float *gr = a.grad + (int64_t)row * a.sg;
+    f32x4 *g4 = reinterpret_cast<f32x4 *>(gr);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = tid + kRowThreads * i;
+      if (c < n4) {
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = sce_grad(exp_shifted(v[i][e], gm) / safe, 4 * c + e == t, bad, a.invN);
+        __builtin_nontemporal_store(o, g4 + c);
+      }
+    }
+    if (tid == 0)
+      for (int c = n4 * 4; c < a.C; ++c)
+        gr[c] = sce_grad(exp_shifted(xr[c], gm) / safe, c == t, bad, a.invN);
+  }
   if (tid == 0) {
     const int t = a.labels[row];
     float lr;
@@ -385,19 +423,23 @@ int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
   const bool vec = (p.D % 4 == 0) && (p.sx % 4 == 0) && (p.sy % 4 == 0) &&
                    aligned16(p.x) && aligned16(p.y) && aligned16(p.gamma) &&
                    aligned16(p.beta);
-  // Persistent grid for the register kernels: 4 workgroups per CU (2 for
-  // the widest rows, whose registers allow only that many), never more
-  // than one row per wave.
-  const unsigned pgrid4 = grid < 1024u ? grid : 1024u;
-  const unsigned pgrid2 = grid < 512u ? grid : 512u;
+  // Persistent grid for the register kernels: 8 workgroups per CU (2 for
+  // the widest rows), never more than one row per wave.  More workgroups
+  // than fit at once keep rows queued behind the resident ones: each row's
+  // stores wait for all of its loads (the reduction sits between them), and
+  // the queued waves cover that gap.  At D = 4096 on MI355X, 8 per CU ran
+  // ~2% faster than 4 per CU.
+  const unsigned cus = (unsigned)(device_cu_count() > 0 ? device_cu_count() : 256);
+  const unsigned pgrid8 = grid < 8u * cus ? grid : 8u * cus;
+  const unsigned pgrid2 = grid < 2u * cus ? grid : 2u * cus;
   if (vec && p.D == 256 * 4)
-    hipLaunchKernelGGL((layer_norm_reg_kernel<4, true>), dim3(pgrid4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<4, true>), dim3(pgrid8), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 4)
-    hipLaunchKernelGGL((layer_norm_reg_kernel<4, false>), dim3(pgrid4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<4, false>), dim3(pgrid8), dim3(256), 0, s, a);
   else if (vec && p.D == 256 * 16)
-    hipLaunchKernelGGL((layer_norm_reg_kernel<16, true>), dim3(pgrid4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<16, true>), dim3(pgrid8), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 16)
-    hipLaunchKernelGGL((layer_norm_reg_kernel<16, false>), dim3(pgrid4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<16, false>), dim3(pgrid8), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 32)
     hipLaunchKernelGGL((layer_norm_reg_kernel<32, false>), dim3(pgrid2), dim3(256), 0, s, a);
   else
@@ -416,14 +458,18 @@ int32_t launch_sce(const SceProblem &p, hipStream_t s) {
   a.labels = p.labels;
   a.loss = p.loss;
   a.softmax = p.softmax;
+  a.grad = p.grad;
   a.row_loss = ws;
   a.sx = p.sx;
   a.ssm = p.ssm;
+  a.sg = p.sg;
+  a.invN = p.rows > 0 ? (float)(1.0 / (double)p.rows) : 0.0f;
   a.rows = (int)p.rows;
   a.C = (int)p.C;
   const unsigned grid = (unsigned)((p.rows + kWaves - 1) / kWaves);
   const bool vec = (p.sx % 4 == 0) && aligned16(p.logits) &&
-                   (!p.softmax || (p.ssm % 4 == 0 && aligned16(p.softmax)));
+                   (!p.softmax || (p.ssm % 4 == 0 && aligned16(p.softmax))) &&
+                   (!p.grad || (p.sg % 4 == 0 && aligned16(p.grad)));
   // Rows of 2K..32K classes: one workgroup per row, row in registers.
   const int64_t n4 = p.C / 4;
   if (vec && p.rows > 0 && p.C > 2048 && n4 <= (int64_t)kRowThreads * 16) {

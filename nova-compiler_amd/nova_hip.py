@@ -45,6 +45,11 @@ EXPORTS = (
     "_mlir_ciface_nova_hip_linear_bf16_bias_gelu",
     "_mlir_ciface_nova_hip_layer_norm_f32",
     "_mlir_ciface_nova_hip_sce_f32",
+    "_mlir_ciface_nova_hip_sce_fwd_bwd_f32",
+    "_mlir_ciface_nova_hip_sce_backward_f32",
+    "_mlir_ciface_nova_hip_layer_norm_backward_f32",
+    "_mlir_ciface_nova_hip_linear_backward",
+    "_mlir_ciface_nova_hip_matmul_backward",
     "nova_hip_set_stream",
     "nova_hip_get_stream",
     "nova_hip_synchronize",
@@ -121,6 +126,11 @@ def lib() -> ctypes.CDLL:
         getattr(L, "_mlir_ciface_nova_hip_" + n).argtypes = [P, P, P]
     L._mlir_ciface_nova_hip_layer_norm_f32.argtypes = [P, P, P, P, P, P, ctypes.c_float]
     L._mlir_ciface_nova_hip_sce_f32.argtypes = [P, P, P, P]
+    L._mlir_ciface_nova_hip_sce_fwd_bwd_f32.argtypes = [P, P, P, P]
+    L._mlir_ciface_nova_hip_sce_backward_f32.argtypes = [P, P, P]
+    L._mlir_ciface_nova_hip_layer_norm_backward_f32.argtypes = [P, P, P, P, P, P, P, P]
+    L._mlir_ciface_nova_hip_linear_backward.argtypes = [P, P, P, P, P, P, ctypes.c_int32]
+    L._mlir_ciface_nova_hip_matmul_backward.argtypes = [P, P, P, P, P, ctypes.c_int32]
     for name in EXPORTS:
         if name.startswith("_mlir_ciface_"):
             getattr(L, name).restype = ctypes.c_int32
@@ -274,3 +284,84 @@ def synchronize() -> None:
 
 def version() -> str:
     return lib().nova_hip_version().decode()
+
+
+def sce_fwd_bwd(logits, labels, *, loss=None, grad=None):
+    """nova.sce then nova.sce_backward in one pass: returns (loss[1], grad)."""
+    torch = _torch()
+    if loss is None:
+        loss = torch.empty(1, dtype=torch.float32, device=logits.device)
+    if grad is None:
+        grad = torch.empty_like(logits)
+    d = [memref_of(t) for t in (logits, labels, loss, grad)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_sce_fwd_bwd_f32(*[ref(v) for v in d]))
+    return loss, grad
+
+
+def sce_backward(softmax, labels, *, grad=None):
+    """nova.sce_backward: (softmax - onehot(labels)) * f32(1 / rows)."""
+    torch = _torch()
+    if grad is None:
+        grad = torch.empty_like(softmax)
+    d = [memref_of(t) for t in (softmax, labels, grad)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_sce_backward_f32(*[ref(v) for v in d]))
+    return grad
+
+
+def layer_norm_backward(grad_y, x, gamma, mean_sum, rstd, *, dx=None, dgamma=None, dbeta=None,
+                        want=(True, True, True)):
+    """nova.layer_norm_backward: returns (dx, dgamma, dbeta); an output
+    whose ``want`` flag is False is not computed (None)."""
+    torch = _torch()
+    shape = x.shape
+    x2, g2 = x.reshape(-1, shape[-1]), grad_y.reshape(-1, shape[-1])
+    if dx is None and want[0]:
+        dx = torch.empty_like(x2)
+    if dgamma is None and want[1]:
+        dgamma = torch.empty(shape[-1], dtype=torch.float32, device=x.device)
+    if dbeta is None and want[2]:
+        dbeta = torch.empty(shape[-1], dtype=torch.float32, device=x.device)
+    d = [memref_of(t) if t is not None else None
+         for t in (g2, x2, gamma, mean_sum.reshape(-1), rstd.reshape(-1), dx, dgamma, dbeta)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_layer_norm_backward_f32(*[ref(v) for v in d]))
+    return (dx.reshape(shape) if dx is not None else None), dgamma, dbeta
+
+
+def linear_backward(grad_out, x, weight, *, out_dtype=None, grad_input=None, grad_weight=None,
+                    grad_bias=None, want=(True, True, True)):
+    """nova.linear_backward for weight [K, N]: returns (grad_input [M,K],
+    grad_weight [K,N], grad_bias [N]).  ``grad_weight`` may be passed as a
+    transposed view of a row-major [N, K] tensor."""
+    torch = _torch()
+    od = out_dtype if out_dtype is not None else torch.float32
+    M, K, N = x.shape[0], x.shape[1], weight.shape[1]
+    if grad_input is None and want[0]:
+        grad_input = torch.empty((M, K), dtype=od, device=x.device)
+    if grad_weight is None and want[1]:
+        grad_weight = torch.empty((K, N), dtype=od, device=x.device)
+    if grad_bias is None and want[2]:
+        grad_bias = torch.empty(N, dtype=od, device=x.device)
+    flags = gemm_flags(_dt(x), _dt(torch.empty(0, dtype=od)))
+    d = [memref_of(t) if t is not None else None
+         for t in (grad_out, x, weight, grad_input, grad_weight, grad_bias)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_linear_backward(*[ref(v) for v in d], flags))
+    return grad_input, grad_weight, grad_bias
+
+
+def matmul_backward(grad, A, B, *, out_dtype=None, grad_a=None, grad_b=None):
+    """nova.matmul_backward (rank 2): returns (grad . B^T, A^T . grad)."""
+    torch = _torch()
+    od = out_dtype if out_dtype is not None else torch.float32
+    if grad_a is None:
+        grad_a = torch.empty(tuple(A.shape), dtype=od, device=A.device)
+    if grad_b is None:
+        grad_b = torch.empty(tuple(B.shape), dtype=od, device=A.device)
+    flags = gemm_flags(_dt(A), _dt(torch.empty(0, dtype=od)))
+    d = [memref_of(t) for t in (grad, A, B, grad_a, grad_b)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_matmul_backward(*[ref(v) for v in d], flags))
+    return grad_a, grad_b

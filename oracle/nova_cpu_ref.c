@@ -327,3 +327,124 @@ int nova_ref_sce_f32(const float *logits, const int32_t *labels, int64_t rows,
   free(tmp);
   return 0;
 }
+
+/*
+ * Softmax cross-entropy backward (NovaSceBackwardLowering,
+ * NovaToLinalgGeneric.cpp:1012-1137) for rank 2 with the class dim last:
+ *   diff = softmax with -1.0 scatter-added at (r, label_r)      (:1102-1113)
+ *   grad = diff * invN, invN = 1.0 / N formed in double and rounded to f32
+ *          by getFloatAttr (:1121-1125), N = product of the non-class dims
+ *          = rows (:1054-1063), one f32 multiply per element (:1127-1128).
+ * Elements off the label are softmax * invN (scatter_add leaves them as is).
+ * A label outside [0, C) has no defined result in the reference (the
+ * scatter index leaves the row); the oracle returns -2 for it.
+ */
+int nova_ref_sce_backward_f32(const float *softmax, const int32_t *labels,
+                              int64_t rows, int64_t C, float *grad) {
+  if (!softmax || !labels || !grad || rows <= 0 || C <= 0) return -1;
+  const float invN = (float)(1.0 / (double)rows);
+  for (int64_t r = 0; r < rows; ++r) {
+    const int32_t t = labels[r];
+    if (t < 0 || (int64_t)t >= C) return -2;
+    const float *sr = softmax + r * C;
+    float *gr = grad + r * C;
+    for (int64_t c = 0; c < C; ++c) {
+      float d = sr[c];
+      if (c == t) d = d + -1.0f;
+      gr[c] = d * invN;
+    }
+  }
+  return 0;
+}
+
+/*
+ * LayerNorm backward (NovaLayerNormBackwardPattern,
+ * NovaToLinalgGeneric.cpp:2128-2371): given gy, x, gamma and the forward's
+ * saved (mean_sum S, rstd), with invD = 1.0f / (float)D (:2159):
+ *   gyGamma = gy * gamma; mean = S * invD; xHat = (x - mean) * rstd
+ *   s1 = sum_d gyGamma, s2 = sum_d gyGamma * xHat   (sequential over d,
+ *                                                    :2236-2258)
+ *   dx = ((gyGamma - s1*invD) - xHat * (s2*invD)) * rstd        (:2264-2288)
+ *   dgamma[d] = sum_r gy * xHat, dbeta[d] = sum_r gy  (sequential over rows,
+ *                                                    :2345-2366)
+ * Any of dx, dgamma, dbeta may be NULL.
+ */
+int nova_ref_layer_norm_backward_f32(const float *gy, const float *x,
+                                     const float *gamma, const float *mean_sum,
+                                     const float *rstd, float *dx,
+                                     float *dgamma, float *dbeta, int64_t rows,
+                                     int64_t D) {
+  if (!gy || !x || !gamma || !mean_sum || !rstd || rows < 0 || D <= 0) return -1;
+  const float invD = 1.0f / (float)D;
+  if (dx) {
+    for (int64_t r = 0; r < rows; ++r) {
+      const float *gr = gy + r * D, *xr = x + r * D;
+      const float mean = mean_sum[r] * invD;
+      const float rs = rstd[r];
+      float s1 = 0.0f, s2 = 0.0f;
+      for (int64_t d = 0; d < D; ++d) {
+        float gg = gr[d] * gamma[d];
+        float diff = xr[d] - mean;
+        float xh = diff * rs;
+        float ggx = gg * xh;
+        s1 = gg + s1;
+        s2 = ggx + s2;
+      }
+      const float ms1 = s1 * invD, ms2 = s2 * invD;
+      float *dr = dx + r * D;
+      for (int64_t d = 0; d < D; ++d) {
+        float gg = gr[d] * gamma[d];
+        float diff = xr[d] - mean;
+        float xh = diff * rs;
+        float t1 = gg - ms1;
+        float t2 = xh * ms2;
+        float t3 = t1 - t2;
+        dr[d] = t3 * rs;
+      }
+    }
+  }
+  if (dgamma || dbeta) {
+    /* Row-outer traversal with one accumulator per column: each column
+     * still sums its rows in order (the reference's loop nest), only the
+     * memory walk is row-major. */
+    float *ag = (float *)calloc((size_t)D, sizeof(float));
+    float *ab = (float *)calloc((size_t)D, sizeof(float));
+    if (!ag || !ab) {
+      free(ag);
+      free(ab);
+      return -1;
+    }
+    for (int64_t r = 0; r < rows; ++r) {
+      const float mean = mean_sum[r] * invD;
+      const float rs = rstd[r];
+      for (int64_t d = 0; d < D; ++d) {
+        float diff = x[r * D + d] - mean;
+        float xh = diff * rs;
+        float gxh = gy[r * D + d] * xh;
+        ag[d] = ag[d] + gxh;
+        ab[d] = ab[d] + gy[r * D + d];
+      }
+    }
+    if (dgamma) memcpy(dgamma, ag, (size_t)D * sizeof(float));
+    if (dbeta) memcpy(dbeta, ab, (size_t)D * sizeof(float));
+    free(ag);
+    free(ab);
+  }
+  return 0;
+}
+
+/*
+ * Column sums out[c] = sum_r in[r, c], sequential over rows in the
+ * accumulator's f32 (the grad_bias reduction of NovaLinearBackwardPattern,
+ * NovaToLinalgGeneric.cpp:1970-1989, body in + acc at :1861-1865).  `in` is [rows, cols]
+ * of dtype dt with row stride ld (elements).
+ */
+int nova_ref_col_sum(const void *in, int dt, int64_t rows, int64_t cols,
+                     int64_t ld, float *out) {
+  if (!in || !out || rows < 0 || cols < 0) return -1;
+  /* Row-outer walk, one accumulator per column, rows in order. */
+  for (int64_t c = 0; c < cols; ++c) out[c] = 0.0f;
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) out[c] = load_as_f32(in, dt, r * ld + c) + out[c];
+  return 0;
+}

@@ -42,6 +42,12 @@ def lib() -> ctypes.CDLL:
         L.nova_ref_mean_f32.restype = ctypes.c_float
         L.nova_ref_sce_f32.argtypes = [P, P, I64, I64, P, P, P]
         L.nova_ref_sce_f32.restype = I
+        L.nova_ref_sce_backward_f32.argtypes = [P, P, I64, I64, P]
+        L.nova_ref_sce_backward_f32.restype = I
+        L.nova_ref_layer_norm_backward_f32.argtypes = [P, P, P, P, P, P, P, P, I64, I64]
+        L.nova_ref_layer_norm_backward_f32.restype = I
+        L.nova_ref_col_sum.argtypes = [P, I, I64, I64, I64, P]
+        L.nova_ref_col_sum.restype = I
         L.nova_ref_f32_to_bf16.argtypes = [ctypes.c_float]
         L.nova_ref_f32_to_bf16.restype = ctypes.c_uint16
         L.nova_ref_f32_to_f16.argtypes = [ctypes.c_float]
@@ -155,3 +161,60 @@ def sce(logits: np.ndarray, labels: np.ndarray, softmax: bool = False):
         raise ValueError("label outside [0, C)")
     assert rc == 0
     return sm, loss, lr
+
+
+def sce_backward(softmax: np.ndarray, labels: np.ndarray) -> np.ndarray:
+    """nova.sce_backward: (softmax - onehot(labels)) * float(1/rows)."""
+    sm = np.ascontiguousarray(softmax, dtype=np.float32)
+    t = np.ascontiguousarray(labels, dtype=np.int32)
+    R, C = sm.shape
+    g = np.empty_like(sm)
+    rc = lib().nova_ref_sce_backward_f32(sm.ctypes.data, t.ctypes.data, R, C, g.ctypes.data)
+    if rc == -2:
+        raise ValueError("label outside [0, C)")
+    assert rc == 0
+    return g
+
+
+def layer_norm_backward(gy, x, gamma, mean_sum, rstd):
+    """nova.layer_norm_backward: returns (dx, dgamma, dbeta)."""
+    gy = np.ascontiguousarray(gy, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = np.ascontiguousarray(gamma, dtype=np.float32)
+    S = np.ascontiguousarray(mean_sum, dtype=np.float32)
+    r = np.ascontiguousarray(rstd, dtype=np.float32)
+    R, D = x.shape
+    dx = np.empty_like(x)
+    dg = np.empty(D, dtype=np.float32)
+    db = np.empty(D, dtype=np.float32)
+    rc = lib().nova_ref_layer_norm_backward_f32(gy.ctypes.data, x.ctypes.data, g.ctypes.data,
+                                                S.ctypes.data, r.ctypes.data, dx.ctypes.data,
+                                                dg.ctypes.data, db.ctypes.data, R, D)
+    assert rc == 0
+    return dx, dg, db
+
+
+def col_sum(a: np.ndarray, dt=None) -> np.ndarray:
+    """Sequential column sums of a 2-D array (f32, or uint16 bits with dt)."""
+    a = np.ascontiguousarray(a)
+    R, C = a.shape
+    out = np.empty(C, dtype=np.float32)
+    rc = lib().nova_ref_col_sum(a.ctypes.data, _dtcode(a, dt), R, C, C, out.ctypes.data)
+    assert rc == 0
+    return out
+
+
+def linear_backward(grad_out, x, weight, *, dt=None):
+    """nova.linear_backward with weight [K, N]: returns (grad_input [M,K],
+    grad_weight [K,N], grad_bias [N]) in f32 (inputs f32, or uint16 bits with
+    dt = BF16 / F16; f32 accumulate)."""
+    gi = gemm(grad_out, weight.T, adt=dt, bdt=dt)[0]
+    gw = gemm(x.T, grad_out, adt=dt, bdt=dt)[0]
+    gb = col_sum(grad_out, dt)
+    return gi, gw, gb
+
+
+def matmul_backward(grad, A, B, *, dt=None):
+    """nova.matmul_backward (rank 2): returns (grad_a = grad . B^T,
+    grad_b = A^T . grad) in f32."""
+    return gemm(grad, B.T, adt=dt, bdt=dt)[0], gemm(A.T, grad, adt=dt, bdt=dt)[0]

@@ -180,3 +180,88 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(nh, "_lib", None)
     with pytest.raises(ImportError, match="no fallback"):
         nh.lib()
+
+
+# ---- backward entry points: host validation only (no call reaches HIP) ----
+
+def test_sce_backward_validation():
+    L = nh.lib()
+    f = lambda sm, t, g: L._mlir_ciface_nova_hip_sce_backward_f32(nh.ref(sm), nh.ref(t), nh.ref(g))
+    assert f(None, d1(4), d2((4, 10))) == 1
+    assert f(d2((4, 10)), d1(3), d2((4, 10))) == 2
+    assert f(d2((4, 10)), d1(4), d2((4, 9))) == 2
+    assert f(d2((4, 10), (10, 2)), d1(4), d2((4, 10))) == 3
+    assert f(d2((4, 10), (5, 1)), d1(4), d2((4, 10))) == 3
+    assert f(d2((0, 10)), d1(0), d2((0, 10))) == 0
+
+
+def test_sce_fwd_bwd_validation():
+    L = nh.lib()
+    f = lambda x, t, loss, g: L._mlir_ciface_nova_hip_sce_fwd_bwd_f32(
+        nh.ref(x), nh.ref(t), nh.ref(loss), nh.ref(g))
+    assert f(d2((4, 10)), d1(4), d1(1), None) == 1
+    assert f(d2((4, 10)), d1(4), d1(1), d2((4, 11))) == 2
+    assert f(d2((4, 10)), d1(4), d1(1), d2((4, 10), (10, 2))) == 3
+    assert f(d2((4, 10)), d1(4), d1(2), d2((4, 10))) == 2
+
+
+def ln_bwd_rc(gy, x, g, S, r, dx=None, dg=None, db=None):
+    L = nh.lib()
+    return L._mlir_ciface_nova_hip_layer_norm_backward_f32(
+        nh.ref(gy), nh.ref(x), nh.ref(g), nh.ref(S), nh.ref(r), nh.ref(dx), nh.ref(dg), nh.ref(db))
+
+
+def test_layer_norm_backward_validation():
+    x = d2((4, 64))
+    assert ln_bwd_rc(None, x, d1(64), d1(4), d1(4)) == 1
+    assert ln_bwd_rc(d2((4, 63)), x, d1(64), d1(4), d1(4)) == 2
+    assert ln_bwd_rc(x, x, d1(63), d1(4), d1(4)) == 2
+    assert ln_bwd_rc(x, x, d1(64), d1(3), d1(4)) == 2
+    assert ln_bwd_rc(x, x, d1(64), d1(4), d1(4), d2((4, 32))) == 2
+    assert ln_bwd_rc(x, x, d1(64), d1(4), d1(4), None, d1(32)) == 2
+    assert ln_bwd_rc(x, d2((4, 64), (64, 2)), d1(64), d1(4), d1(4)) == 3
+    assert ln_bwd_rc(x, x, d1(64), d1(4, 2), d1(4)) == 3
+    assert ln_bwd_rc(d2((4, 0)), d2((4, 0)), d1(0), d1(4), d1(4)) == 2
+    # rows longer than the LDS column accumulators hold: refused before any launch
+    big = d2((4, 8193))
+    assert ln_bwd_rc(big, big, d1(8193), d1(4), d1(4)) == 5
+
+
+def test_linear_backward_validation():
+    L = nh.lib()
+    fl = nh.gemm_flags(nh.DT_BF16, nh.DT_F32)
+
+    def f(go, x, w, gi=None, gw=None, gb=None, flags=fl):
+        return L._mlir_ciface_nova_hip_linear_backward(nh.ref(go), nh.ref(x), nh.ref(w), nh.ref(gi),
+                                                       nh.ref(gw), nh.ref(gb), flags)
+
+    go, x, w = d2((8, 16)), d2((8, 32)), d2((32, 16))
+    assert f(None, x, w) == 1
+    assert f(go, x, w, flags=nh.gemm_flags(nh.DT_BF16, nh.DT_F32, nh.EPI_BIAS)) == 1
+    assert f(go, x, w, flags=0x10000) == 1
+    assert f(go, x, d2((31, 16))) == 2
+    assert f(d2((8, 15)), x, w) == 2
+    assert f(go, x, w, gi=d2((8, 31))) == 2          # grad_input must be [M, K]
+    assert f(go, x, w, gw=d2((32, 15))) == 2         # grad_weight must be [K, N]
+    assert f(go, x, w, gb=d1(15)) == 2
+    assert f(go, x, w, gb=d1(16, 2)) == 3
+    assert f(d2((8, 16), (1, 8)), x, w, gb=d1(16)) == 3  # column sums need unit stride on N
+    # empty batch: both GEMMs are no-ops, and no bias gradient asked for
+    assert f(d2((0, 16)), d2((0, 32)), w, gi=d2((0, 32))) == 0
+
+
+def test_matmul_backward_validation():
+    L = nh.lib()
+    fl = nh.gemm_flags(nh.DT_F32, nh.DT_F32)
+
+    def f(g, A, B, ga=None, gb=None, flags=fl):
+        return L._mlir_ciface_nova_hip_matmul_backward(nh.ref(g), nh.ref(A), nh.ref(B), nh.ref(ga),
+                                                       nh.ref(gb), flags)
+
+    g, A, B = d2((8, 16)), d2((8, 32)), d2((32, 16))
+    assert f(None, A, B) == 1
+    assert f(g, A, d2((30, 16))) == 2
+    assert f(d2((9, 16)), A, B) == 2
+    assert f(g, A, B, flags=nh.gemm_flags(nh.DT_F32, nh.DT_BF16)) == 4
+    assert f(g, A, B, flags=nh.gemm_flags(nh.DT_F32, nh.DT_F32, nh.EPI_GELU)) == 1
+    assert f(g, A, B, ga=d2((8, 31))) == 2
