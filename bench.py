@@ -36,6 +36,12 @@ C4A_BYTES = 19_744_128
 C4B_BYTES = 14_713_536
 LN_BYTES = 16384 * 4096 * 4 * 2 + 4096 * 4 * 2 + 16384 * 4 * 2   # 537,034,752
 SCE_BYTES = 4096 * 32000 * 4 + 4096 * 4 + 4                     # 524,304,388
+# Backward ops at the same config-5 / config-3 shapes (algorithmic bytes /
+# FLOP; workspace partials excluded).
+SCE_BWD_BYTES = 2 * 4096 * 32000 * 4 + 4096 * 4                 # 1,048,592,384
+SCE_FWD_BWD_BYTES = 2 * 4096 * 32000 * 4 + 4096 * 4 + 4         # 1,048,592,388
+LN_BWD_BYTES = 3 * 16384 * 4096 * 4 + 4096 * 4 * 3 + 16384 * 4 * 2  # 805,486,592
+C3_BWD_FLOP = 2 * C3_FLOP                                       # grad_input + grad_weight
 
 
 def parse():
@@ -46,7 +52,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (cpu_baseline becomes null)")
     ap.add_argument("--only", default="",
-                    help="comma list of configs to run (c2,c3,c4,ln,sce; copy = HBM copy calibration)")
+                    help="comma list of configs to run (c2,c3,c4,ln,sce,sce_bwd,sce_fwd_bwd,ln_bwd,"
+                         "c3_bwd; copy = HBM copy calibration)")
     return ap.parse_args()
 
 
@@ -196,6 +203,92 @@ def bench_sce(args, torch, nh, S):
             "loss": float(sets[0][1][2].cpu()[0])}
 
 
+def bench_sce_bwd(args, torch, nh, S, fused):
+    """nova.sce_backward on the config-5 SCE shape (softmax in, grad out),
+    or the fused forward + backward (logits in, loss and grad out)."""
+    inp = S.config_inputs("c5_sce")
+    sets = []
+    for _ in range(3):
+        x = to_dev(inp["logits"], S.F32, torch)
+        t = torch.from_numpy(inp["labels"]).cuda()
+        g = torch.empty_like(x)
+        loss = torch.empty(1, device="cuda")
+        d = (x, t, loss, g) if fused else (x, t, g)
+        sets.append(([nh.ref(nh.memref_of(v)) for v in d], d))
+    del inp
+    f_ = (nh.lib()._mlir_ciface_nova_hip_sce_fwd_bwd_f32 if fused
+          else nh.lib()._mlir_ciface_nova_hip_sce_backward_f32)
+
+    def fn(i):
+        rc = f_(*sets[i % 3][0])
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, args.steps * 2, args.warmup, torch)
+    nbytes = SCE_FWD_BWD_BYTES if fused else SCE_BWD_BYTES
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": ms, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "bytes": nbytes}
+
+
+def bench_ln_bwd(args, torch, nh, S):
+    """nova.layer_norm_backward on the config-5 LayerNorm shape."""
+    inp = S.config_inputs("c5_ln")
+    g = to_dev(inp["gamma"], S.F32, torch)
+    x0 = to_dev(inp["x"], S.F32, torch)
+    y, Sm, rs = nh.layer_norm(x0, g, to_dev(inp["beta"], S.F32, torch))
+    del y
+    sets = []
+    for i in range(3):
+        x = x0 if i == 0 else x0.clone()
+        gy = torch.randn_like(x0)
+        dx = torch.empty_like(x0)
+        dg = torch.empty(4096, device="cuda")
+        db = torch.empty(4096, device="cuda")
+        d = (gy, x, g, Sm, rs, dx, dg, db)
+        sets.append(([nh.ref(nh.memref_of(v)) for v in d], d))
+    del inp
+    f_ = nh.lib()._mlir_ciface_nova_hip_layer_norm_backward_f32
+
+    def fn(i):
+        rc = f_(*sets[i % 3][0])
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, args.steps * 2, args.warmup, torch)
+    gbs = LN_BWD_BYTES / (ms * 1e-3) / 1e9
+    return {"ms": ms, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "bytes": LN_BWD_BYTES}
+
+
+def bench_c3_bwd(args, torch, nh, S):
+    """nova.linear_backward of config 3 (bf16 in, f32 accumulate, f32
+    grads): grad_input = go . W, grad_weight written in W's [11008, 4096]
+    layout, grad_bias; TFLOP/s over the two GEMMs."""
+    inp = S.config_inputs("c3")
+    x = to_dev(inp["x"], S.BF16, torch)
+    W = to_dev(inp["W"], S.BF16, torch)
+    del inp
+    go = torch.randn(4096, 11008, device="cuda").to(torch.bfloat16)
+    gi = torch.empty(4096, 4096, device="cuda")
+    gw = torch.empty(11008, 4096, device="cuda")
+    gb = torch.empty(11008, device="cuda")
+    d = [nh.memref_of(t) for t in (go, x, W.t(), gi, gw.t(), gb)]
+    p = [nh.ref(v) for v in d]
+    flags = nh.gemm_flags(nh.DT_BF16, nh.DT_F32)
+    f_ = nh.lib()._mlir_ciface_nova_hip_linear_backward
+
+    def fn(_):
+        rc = f_(*p, flags)
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, max(args.steps // 2, 5), max(args.warmup // 2, 2), torch)
+    tf = C3_BWD_FLOP / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS}
+
+
 def bench_copy(args, torch):
     """A plain device copy of 256 MiB (torch's copy kernel): the practical
     read+write HBM ceiling the reductions are compared with, and the known
@@ -253,7 +346,8 @@ def main():
         sys.exit(1)
     torch.cuda.set_device(0)
     nh.lib()
-    only = set(args.only.split(",")) if args.only else {"c2", "c3", "c4", "ln", "sce"}
+    only = (set(args.only.split(",")) if args.only else
+            {"c2", "c3", "c4", "ln", "sce", "sce_bwd", "sce_fwd_bwd", "ln_bwd", "c3_bwd"})
     cfg = {}
 
     def stage(name, f):
@@ -275,6 +369,17 @@ def main():
         cfg["c5_layer_norm_f32_16384x4096"] = stage("ln", lambda: bench_ln(args, torch, nh, S))
     if "sce" in only:
         cfg["c5_sce_f32_4096x32000"] = stage("sce", lambda: bench_sce(args, torch, nh, S))
+    if "sce_bwd" in only:
+        cfg["c5_sce_backward_f32_4096x32000"] = stage(
+            "sce_bwd", lambda: bench_sce_bwd(args, torch, nh, S, False))
+    if "sce_fwd_bwd" in only:
+        cfg["c5_sce_fwd_bwd_f32_4096x32000"] = stage(
+            "sce_fwd_bwd", lambda: bench_sce_bwd(args, torch, nh, S, True))
+    if "ln_bwd" in only:
+        cfg["c5_layer_norm_backward_f32_16384x4096"] = stage(
+            "ln_bwd", lambda: bench_ln_bwd(args, torch, nh, S))
+    if "c3_bwd" in only:
+        cfg["c3_linear_backward_bf16_f32"] = stage("c3_bwd", lambda: bench_c3_bwd(args, torch, nh, S))
     if "copy" in only:  # calibration only; not part of the default run
         cfg["hbm_copy_256MiB"] = stage("copy", lambda: bench_copy(args, torch))
 

@@ -94,6 +94,39 @@ __global__ __launch_bounds__(256) void sce_backward_kernel(SceBwdArgs a) {
   }
 }
 
+// Contiguous rows (row strides == C, C % 4 == 0, aligned): the matrix is one
+// flat stream of float4 chunks, chunk c in row c / (C/4), so no block is
+// left partly idle at a row's end.
+__global__ __launch_bounds__(256) void sce_backward_flat_kernel(SceBwdArgs a, int total4) {
+  const int n4 = a.C >> 2;
+  const f32x4 *s4 = reinterpret_cast<const f32x4 *>(a.softmax);
+  f32x4 *g4 = reinterpret_cast<f32x4 *>(a.grad);
+  const int base = blockIdx.x * (256 * kU) + threadIdx.x;
+  f32x4 v[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int c = base + 256 * u;
+    v[u] = c < total4 ? __builtin_nontemporal_load(s4 + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int c = base + 256 * u;
+    if (c < total4) {
+      const int row = c / n4;
+      const int t = a.labels[row];
+      const bool bad = t < 0 || t >= a.C;
+      const int e0 = 4 * (c - row * n4);
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = (e0 + e == t) ? v[u][e] + -1.0f : v[u][e];
+        o[e] = bad ? __builtin_nanf("") : d * a.invN;
+      }
+      __builtin_nontemporal_store(o, g4 + c);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // nova.layer_norm_backward (NovaLayerNormBackwardPattern,
 // NovaToLinalgGeneric.cpp:2128-2371).  Per row, with the forward's saved
@@ -102,11 +135,9 @@ __global__ __launch_bounds__(256) void sce_backward_kernel(SceBwdArgs a) {
 //   s1 = sum gg, s2 = sum gg * xh                        (row reductions)
 //   dx = ((gg - s1*invD) - xh * (s2*invD)) * rstd        (reference op order)
 //   dgamma[d] = sum_r gy * xh, dbeta[d] = sum_r gy       (column reductions)
-// One wave per row with gy and x in registers (NV float4 per lane, D <=
-// 256 NV).  The column sums go into LDS accumulators: the workgroup's four
-// waves take four consecutive rows, and add them in row order (one barrier
-// per wave turn), so each column of a workgroup's partial is the sequential
-// sum of its contiguous row block.  Partials go to [grid][2][D].
+// Each workgroup takes one contiguous block of rows and writes its column
+// sums as one partial [2][D] to [grid][2][D]; reduce_partials adds the
+// partials in workgroup order.
 // ---------------------------------------------------------------------------
 struct LnBwdArgs {
   const float *gy;
@@ -121,32 +152,45 @@ struct LnBwdArgs {
   float invD;
 };
 
-template <int NV, bool FULL>
-__global__ __launch_bounds__(256) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
+// Each row is split over a group of four waves, wave q holding float4
+// chunks [q*64*NQ, (q+1)*64*NQ) of gy and x (NQ per lane) and register
+// accumulators for the same columns, so the column sums need no LDS
+// traffic and no turn-taking; the row reductions s1, s2 combine the four
+// waves' partials through LDS in wave order (one barrier per row).  A
+// 512-thread workgroup runs two such groups on alternate rows of its
+// contiguous row block; at the end group 1's column sums are added to group
+// 0's through LDS, and the workgroup writes one partial [2][D].
+template <int NQ, bool FULL>
+__global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
 #pragma clang fp contract(off)
-  __shared__ f32x4 sgam[64 * NV], acc_g[64 * NV], acc_b[64 * NV];
+  __shared__ float red[2][8][2];
+  __shared__ f32x4 xfer[2][256 * NQ];
   const int nv4 = a.D >> 2;
-  const f32x4 *gam4 = reinterpret_cast<const f32x4 *>(a.gamma);
-  for (int c = threadIdx.x; c < nv4; c += 256) {
-    sgam[c] = gam4[c];
-    acc_g[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc_b[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave >> 2, q = wave & 3;
   auto in_row = [&](int c) __attribute__((always_inline)) { return FULL || c < nv4; };
+  const f32x4 *gam4 = reinterpret_cast<const f32x4 *>(a.gamma);
+  f32x4 gm[NQ], acc_g[NQ], acc_b[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int c = q * 64 * NQ + lane + 64 * i;
+    gm[i] = in_row(c) ? gam4[c] : f32x4{0.f, 0.f, 0.f, 0.f};
+    acc_g[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc_b[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   const int per_wg = (a.rows + gridDim.x - 1) / gridDim.x;
   const int row0 = min(a.rows, (int)blockIdx.x * per_wg);
   const int row_end = min(a.rows, row0 + per_wg);
-  for (int rb = row0; rb < row_end; rb += 4) {
-    const int row = rb + wave;
+  int it = 0;
+  for (int rb = row0; rb < row_end; rb += 2, ++it) {
+    const int row = rb + grp;
     const bool live = row < row_end;
-    f32x4 g[NV], xv[NV];
     const f32x4 *gr = reinterpret_cast<const f32x4 *>(a.gy + (int64_t)(live ? row : row0) * a.sgy);
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)(live ? row : row0) * a.sx);
+    f32x4 g[NQ], xv[NQ];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = lane + 64 * i;
+    for (int i = 0; i < NQ; ++i) {
+      const int c = q * 64 * NQ + lane + 64 * i;
       const bool ok = live && in_row(c);
       g[i] = ok ? __builtin_nontemporal_load(gr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
       xv[i] = ok ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -155,68 +199,71 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
     const float rs = live ? a.rstd[row] : 0.0f;
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const f32x4 gm = sgam[in_row(lane + 64 * i) ? lane + 64 * i : 0];
+    for (int i = 0; i < NQ; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float gg = g[i][e] * gm[e];
+        const float gg = g[i][e] * gm[i][e];
         const float xh = (xv[i][e] - mean) * rs;
         s1 = s1 + gg;
         s2 = s2 + gg * xh;
       }
-    }
     s1 = wave_sum(s1);
     s2 = wave_sum(s2);
+    const int pb = it & 1;
+    if (lane == 0) {
+      red[pb][wave][0] = s1;
+      red[pb][wave][1] = s2;
+    }
+    __syncthreads();
+    s1 = 0.0f;
+    s2 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      s1 = s1 + red[pb][grp * 4 + w][0];
+      s2 = s2 + red[pb][grp * 4 + w][1];
+    }
     const float ms1 = s1 * a.invD, ms2 = s2 * a.invD;
-    if (live && a.dx) {
+    if (live) {
       f32x4 *dr = reinterpret_cast<f32x4 *>(a.dx + (int64_t)row * a.sdx);
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
-        if (in_row(c)) {
-          const f32x4 gm = sgam[c];
-          f32x4 o;
+      for (int i = 0; i < NQ; ++i) {
+        const int c = q * 64 * NQ + lane + 64 * i;
+        f32x4 o;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float gg = g[i][e] * gm[e];
-            const float xh = (xv[i][e] - mean) * rs;
-            const float t1 = gg - ms1;
-            const float t2 = xh * ms2;
-            o[e] = (t1 - t2) * rs;
-          }
-          __builtin_nontemporal_store(o, dr + c);
+        for (int e = 0; e < 4; ++e) {
+          const float gg = g[i][e] * gm[i][e];
+          const float xh = (xv[i][e] - mean) * rs;
+          const float t1 = gg - ms1;
+          const float t2 = xh * ms2;
+          o[e] = (t1 - t2) * rs;
+          acc_g[i][e] = acc_g[i][e] + g[i][e] * xh;
+          acc_b[i][e] = acc_b[i][e] + g[i][e];
         }
-      }
-    }
-    // Column sums, in row order: wave w adds row rb + w on its turn.
-#pragma unroll 1
-    for (int turn = 0; turn < 4; ++turn) {
-      __syncthreads();
-      if (turn == wave && live) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int c = lane + 64 * i;
-          if (in_row(c)) {
-            f32x4 ag = acc_g[c], ab = acc_b[c];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float xh = (xv[i][e] - mean) * rs;
-              ag[e] = ag[e] + g[i][e] * xh;
-              ab[e] = ab[e] + g[i][e];
-            }
-            acc_g[c] = ag;
-            acc_b[c] = ab;
-          }
-        }
+        if (a.dx && in_row(c)) __builtin_nontemporal_store(o, dr + c);
       }
     }
   }
+  // Group 1's column sums join group 0's (group 0 held the earlier row of
+  // every pair), then group 0 writes the workgroup's partial.
+  if (grp == 1) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      xfer[0][q * 64 * NQ + lane + 64 * i] = acc_g[i];
+      xfer[1][q * 64 * NQ + lane + 64 * i] = acc_b[i];
+    }
+  }
   __syncthreads();
-  f32x4 *pg = reinterpret_cast<f32x4 *>(a.partial + (int64_t)blockIdx.x * 2 * a.D);
-  f32x4 *pb = reinterpret_cast<f32x4 *>(a.partial + (int64_t)blockIdx.x * 2 * a.D + a.D);
-  for (int c = threadIdx.x; c < nv4; c += 256) {
-    pg[c] = acc_g[c];
-    pb[c] = acc_b[c];
+  if (grp == 0) {
+    f32x4 *pg = reinterpret_cast<f32x4 *>(a.partial + (int64_t)blockIdx.x * 2 * a.D);
+    f32x4 *pb = reinterpret_cast<f32x4 *>(a.partial + (int64_t)blockIdx.x * 2 * a.D + a.D);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int c = q * 64 * NQ + lane + 64 * i;
+      if (in_row(c)) {
+        pg[c] = acc_g[i] + xfer[0][c];
+        pb[c] = acc_b[i] + xfer[1][c];
+      }
+    }
   }
 }
 
@@ -314,6 +361,43 @@ __global__ __launch_bounds__(256) void col_sum_partial_kernel(const void *in, in
   part[(int64_t)blockIdx.y * cols + c] = acc;
 }
 
+// The same with 16-byte loads: each thread sums V = 16 / element-size
+// adjacent columns (needs 16-byte aligned rows and cols % V == 0).
+template <int DT>
+__global__ __launch_bounds__(256) void col_sum_partial_vec_kernel(const void *in, int64_t ld,
+                                                                  int rows, int cols, int chunk,
+                                                                  float *part) {
+  constexpr int V = DT == NOVA_HIP_DT_F32 ? 4 : 8;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * V;
+  if (c0 >= cols) return;
+  const int r0 = blockIdx.y * chunk;
+  const int r1 = min(rows, r0 + chunk);
+  float acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+  const char *base = static_cast<const char *>(in);
+  constexpr int esz = DT == NOVA_HIP_DT_F32 ? 4 : 2;
+  for (int r = r0; r < r1; ++r) {
+    const u32x4 w = *reinterpret_cast<const u32x4 *>(base + ((int64_t)r * ld + c0) * esz);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float x;
+      if constexpr (DT == NOVA_HIP_DT_F32) {
+        x = __uint_as_float(w[v]);
+      } else {
+        const uint16_t h = (uint16_t)(w[v >> 1] >> (16 * (v & 1)));
+        if constexpr (DT == NOVA_HIP_DT_BF16) x = __uint_as_float((uint32_t)h << 16);
+        else x = (float)__builtin_bit_cast(_Float16, h);
+      }
+      acc[v] = x + acc[v];
+    }
+  }
+  float *out = part + (int64_t)blockIdx.y * cols + c0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) out[v] = acc[v];
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
@@ -402,6 +486,12 @@ int32_t launch_sce_backward(const SceBackwardProblem &p, hipStream_t s) {
   a.C = (int)p.C;
   a.invN = (float)(1.0 / (double)p.rows);
   const bool vec = aligned16(p.softmax) && aligned16(p.grad) && p.ss % 4 == 0 && p.sg % 4 == 0;
+  const int64_t total4 = p.rows * (p.C / 4);
+  if (vec && p.C % 4 == 0 && p.ss == p.C && p.sg == p.C && total4 < 0x7fffffff - 256 * kU) {
+    const unsigned g = (unsigned)((total4 + 256 * kU - 1) / (256 * kU));
+    hipLaunchKernelGGL(sce_backward_flat_kernel, dim3(g), dim3(256), 0, s, a, (int)total4);
+    return check_hip(hipGetLastError(), "sce_backward launch");
+  }
   // Rows beyond 65535 go in several launches (grid y limit).
   for (int64_t r0 = 0; r0 < p.rows; r0 += 65535) {
     const int64_t nr = p.rows - r0 < 65535 ? p.rows - r0 : 65535;
@@ -431,11 +521,14 @@ int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_
   const bool vec = p.D % 4 == 0 && p.sgy % 4 == 0 && p.sx % 4 == 0 && (!p.dx || p.sdx % 4 == 0) &&
                    aligned16(p.gy) && aligned16(p.x) && aligned16(p.gamma) &&
                    (!p.dx || aligned16(p.dx));
-  // Persistent grid: 3 workgroups per CU (registers: gy and x rows), each
-  // one contiguous row block.
+  // Persistent grid: the vector kernel's 512-thread workgroups (two row
+  // groups of four waves) at 2 per CU, the general kernel's 256-thread ones
+  // at 3 per CU; each takes one contiguous row block.
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const int64_t want = (p.rows + 3) / 4;
-  const int grid = (int)(want < 3 * cus ? (want > 0 ? want : 1) : 3 * cus);
+  const bool use_vec = vec && p.D <= 8192;
+  const int64_t want = use_vec ? (p.rows + 1) / 2 : (p.rows + 3) / 4;
+  const int64_t cap = (int64_t)(use_vec ? 2 : 3) * cus;
+  const int grid = (int)(want < cap ? (want > 0 ? want : 1) : cap);
   const int ng = (grid + kGroup - 1) / kGroup;
   const size_t part_floats = (size_t)grid * 2 * p.D;
   const size_t ws_floats = part_floats + (size_t)(ng + 1) * 2 * p.D;
@@ -455,14 +548,16 @@ int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_
   a.rows = (int)p.rows;
   a.D = (int)p.D;
   a.invD = 1.0f / (float)p.D;
-  if (vec && p.D == 1024)
-    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<4, true>), dim3(grid), dim3(256), 0, s, a);
-  else if (vec && p.D <= 1024)
-    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<4, false>), dim3(grid), dim3(256), 0, s, a);
-  else if (vec && p.D == 4096)
-    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<16, true>), dim3(grid), dim3(256), 0, s, a);
-  else if (vec && p.D <= 4096)
-    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<16, false>), dim3(grid), dim3(256), 0, s, a);
+  if (use_vec && p.D == 1024)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<1, true>), dim3(grid), dim3(512), 0, s, a);
+  else if (use_vec && p.D <= 1024)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<1, false>), dim3(grid), dim3(512), 0, s, a);
+  else if (use_vec && p.D == 4096)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<4, true>), dim3(grid), dim3(512), 0, s, a);
+  else if (use_vec && p.D <= 4096)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<4, false>), dim3(grid), dim3(512), 0, s, a);
+  else if (use_vec)
+    hipLaunchKernelGGL((layer_norm_bwd_rows_kernel<8, false>), dim3(grid), dim3(512), 0, s, a);
   else
     hipLaunchKernelGGL(layer_norm_bwd_any_kernel, dim3(grid), dim3(256), 0, s, a);
   int32_t rc = check_hip(hipGetLastError(), "layer_norm_backward launch");
@@ -484,6 +579,23 @@ int32_t launch_col_sum(const ColSumProblem &p, hipStream_t s) {
   const size_t part_floats = (size_t)nch * p.cols;
   float *ws = static_cast<float *>(workspace(s, (part_floats + (size_t)(ng + 1) * p.cols) * 4));
   if (!ws) return NOVA_HIP_ENOMEM;
+  const int esz = p.in_dt == NOVA_HIP_DT_F32 ? 4 : 2;
+  const int V = 16 / esz;
+  if (aligned16(p.in) && (p.ld * esz) % 16 == 0 && p.cols % V == 0) {
+    const dim3 gv((unsigned)((p.cols / V + 255) / 256), (unsigned)nch);
+    if (p.in_dt == NOVA_HIP_DT_F32)
+      hipLaunchKernelGGL(col_sum_partial_vec_kernel<NOVA_HIP_DT_F32>, gv, dim3(256), 0, s, p.in,
+                         p.ld, (int)p.rows, (int)p.cols, (int)chunk, ws);
+    else if (p.in_dt == NOVA_HIP_DT_BF16)
+      hipLaunchKernelGGL(col_sum_partial_vec_kernel<NOVA_HIP_DT_BF16>, gv, dim3(256), 0, s, p.in,
+                         p.ld, (int)p.rows, (int)p.cols, (int)chunk, ws);
+    else
+      hipLaunchKernelGGL(col_sum_partial_vec_kernel<NOVA_HIP_DT_F16>, gv, dim3(256), 0, s, p.in,
+                         p.ld, (int)p.rows, (int)p.cols, (int)chunk, ws);
+    int32_t rc = check_hip(hipGetLastError(), "column sum launch");
+    if (rc) return rc;
+    return reduce_partials(ws, nch, 1, (int)p.cols, p.out, nullptr, p.out_dt, ws + part_floats, s);
+  }
   const dim3 g1((unsigned)((p.cols + 255) / 256), (unsigned)nch);
   if (p.in_dt == NOVA_HIP_DT_F32)
     hipLaunchKernelGGL(col_sum_partial_kernel<NOVA_HIP_DT_F32>, g1, dim3(256), 0, s, p.in, p.ld,
