@@ -257,42 +257,42 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Epilogue for full tiles when the MFMAs were issued with B as the first
 // operand, so acc[i][j] holds the 32x32 output tile transposed: lane l owns
 // output row (l % 32) and, for g = 0..3, the four consecutive columns
-// 8g + 4(l/32) + 0..3 in elements v = 4g .. 4g+3.  Every output is one 16-byte
-// (f32) or 8-byte (bf16/f16) store; no bounds checks (full tiles only).
-template <int TM, int TN, int ODT, int EPI>
-__device__ __forceinline__ void store_full_t(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
-                                             int bidx, int mw, int nw, int lane) {
-  constexpr bool kBias = (EPI == NOVA_HIP_EPI_BIAS || EPI == NOVA_HIP_EPI_BIAS_GELU);
-  constexpr bool kGelu = (EPI == NOVA_HIP_EPI_BIAS_GELU || EPI == NOVA_HIP_EPI_GELU);
+// 8g + 4(l/32) + 0..3 in elements v = 4g .. 4g+3.  Every four outputs are
+// one 16-byte (f32) or 8-byte (bf16/f16) store; no bounds checks (full tiles
+// only).  Specialised on the output dtype only: bias and GELU are uniform
+// branches, and the four bias values of a column group are loaded right
+// before the TM stores that use them, so no more than four registers hold
+// bias (hoisting all TN*16 of them made the kernel spill).
+template <int TM, int TN, int ODT>
+__device__ __forceinline__ void store_full_epi(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                               int bidx, int mw, int nw, int lane) {
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
   constexpr int kEsz = ODT == NOVA_HIP_DT_F32 ? 4 : 2;
   const int lr = lane & 31, lh = lane >> 5;
-  f32x4 bias[TN][4];
-  if constexpr (kBias) {
+  char *Cb = static_cast<char *>(a.C) + (int64_t)bidx * a.scb * kEsz;
+  char *row0 = Cb + ((int64_t)(mw + lr) * a.scm + nw + 4 * lh) * kEsz;
+  const int64_t row_step = (int64_t)32 * a.scm * kEsz;  // 32 output rows
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+  for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 4; ++g) {
+      f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+      if (has_bias) {
         const int n = nw + 32 * j + 8 * g + 4 * lh;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bias[j][g][e] = bias_at(a.bias, a.bias_dt, n + e);
+        for (int e = 0; e < 4; ++e) bv[e] = bias_at(a.bias, a.bias_dt, n + e);
       }
-  }
-  char *Cb = static_cast<char *>(a.C) + (int64_t)bidx * a.scb * kEsz;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    char *row = Cb + ((int64_t)(mw + 32 * i + lr) * a.scm + nw + 4 * lh) * kEsz;
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int i = 0; i < TM; ++i) {
         f32x4 x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                    acc[i][j][4 * g + 3]};
-        if constexpr (kBias) x = x + bias[j][g];
-        if constexpr (kGelu) {
+        if (has_bias) x = x + bv;
+        if (has_gelu) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) x[e] = gelu_tanh_fast(x[e]);
         }
-        char *dst = row + (32 * j + 8 * g) * kEsz;
+        char *dst = row0 + i * row_step + (32 * j + 8 * g) * kEsz;
         if constexpr (ODT == NOVA_HIP_DT_F32) {
           *reinterpret_cast<f32x4 *>(dst) = x;
         } else if constexpr (ODT == NOVA_HIP_DT_BF16) {
@@ -305,25 +305,7 @@ __device__ __forceinline__ void store_full_t(const f32x16 (&acc)[TM][TN], const 
                     to_f16(x[2]) | ((uint32_t)to_f16(x[3]) << 16)};
         }
       }
-  }
-}
-
-// Runtime (output dtype, epilogue) -> one compact specialisation.
-template <int TM, int TN>
-__device__ __forceinline__ void store_full(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
-                                           int bidx, int mw, int nw, int lane) {
-  switch (a.out_dt * 4 + a.epi) {
-#define NOVA_EPI_CASE(O, E) \
-  case O * 4 + E:           \
-    store_full_t<TM, TN, O, E>(acc, a, bidx, mw, nw, lane); \
-    break;
-    NOVA_EPI_CASE(0, 0) NOVA_EPI_CASE(0, 1) NOVA_EPI_CASE(0, 2) NOVA_EPI_CASE(0, 3)
-    NOVA_EPI_CASE(1, 0) NOVA_EPI_CASE(1, 1) NOVA_EPI_CASE(1, 2) NOVA_EPI_CASE(1, 3)
-    NOVA_EPI_CASE(2, 0) NOVA_EPI_CASE(2, 1) NOVA_EPI_CASE(2, 2) NOVA_EPI_CASE(2, 3)
-#undef NOVA_EPI_CASE
-    default:
-      break;
-  }
+    }
 }
 
 }  // namespace gemm
@@ -333,6 +315,13 @@ __device__ __forceinline__ void store_full(const f32x16 (&acc)[TM][TN], const Ge
 // register-staged kernel).
 bool gemm_dma_applicable(const gemm::GemmArgs &a, bool akc, bool bkc, bool vec);
 int32_t launch_gemm_dma(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc, hipStream_t s);
+// Per output dtype (gemm_dma_out_{f32,bf16,f16}.hip, compiled separately).
+int32_t launch_gemm_dma_f32out(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc,
+                               hipStream_t s);
+int32_t launch_gemm_dma_bf16out(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc,
+                                hipStream_t s);
+int32_t launch_gemm_dma_f16out(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc,
+                               hipStream_t s);
 // Small-K kernel (gemm_small.hip): whole K staged in LDS per output tile.
 bool gemm_small_applicable(const gemm::GemmArgs &a, bool akc, bool bkc);
 int32_t launch_gemm_small(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc, hipStream_t s);

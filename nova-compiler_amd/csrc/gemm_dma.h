@@ -1,0 +1,297 @@
+// MFMA GEMM for aligned problems made of whole 256x256 tiles (the large
+// configs: batch GEMM 8x4096^3, linear 4096x4096x11008).
+//
+// Operands travel global -> LDS with buffer_load ... lds (LDS DMA): no
+// staging registers.  K is consumed in steps of BK = 64 so that every
+// K-contiguous row segment a DMA instruction fetches is one whole 128-byte
+// line (with BK = 32 the L2 served twice the requests for the same bytes
+// and ran 93% busy at half the needed rate).  Two LDS stages of 64 KB: the
+// DMA of tile t+1 runs under the MFMAs of tile t.  Each stage holds
+//   * a K-contiguous operand as [256 rows][8 chunks of 8 k], 16-byte chunk
+//     index XOR-swizzled by row so the ds_read_b128 of 16 consecutive rows
+//     covers all banks;
+//   * an M/N-contiguous operand (row-major [K,N] B, or a transposed A) as
+//     [64 k][32 chunks of 8 rows], read with ds_read_b64_tr_b16, which
+//     transposes 16-bit data across each 16-lane group (lane i gets element
+//     i of four rows); an XOR by k keeps the rows read together on distinct
+//     banks.
+// A DMA instruction writes 64 lanes x 16 bytes contiguously, so the
+// swizzle is applied by choosing, per lane, which global chunk to fetch.
+//
+// Four wave64s in a 2x2 grid each own 128x128 of the output as 4x4 tiles of
+// v_mfma_f32_32x32x16 (256 accumulation registers), issued with B as the
+// first operand so each lane accumulates four consecutive output columns
+// and the epilogue writes them with one vector store.  Per K step (tile t,
+// four k16 steps): the fragments of k16-step s+1 are read while the MFMAs
+// of step s run; after step 2 the wave waits for its DMA of tile t+1, one
+// barrier, then the DMA of tile t+2 goes into the freed stage while tile
+// t+1's first fragments are read under the MFMAs of step 3.
+#pragma once
+
+#include "gemm_common.h"
+
+namespace nova_hip {
+namespace dma {
+
+using namespace gemm;
+
+constexpr int BM = 256, BN = 256;
+#ifndef NOVA_DMA_BK
+#define NOVA_DMA_BK 64
+#endif
+constexpr int BK = NOVA_DMA_BK;
+constexpr int kChunks = BK / 8;              // 16-byte chunks per K-contiguous row
+constexpr int kSlots = BM * BK / 8;          // 16-byte slots per operand per stage
+constexpr int kLoads = kSlots / kThreads;    // DMA instructions per thread per operand
+constexpr int kStages = 2;
+// The DMA of a tile is spread over this many k16 steps (see the main loop).
+#ifndef NOVA_DMA_SPREAD
+#define NOVA_DMA_SPREAD 2
+#endif
+constexpr int kSpread = NOVA_DMA_SPREAD;
+constexpr int kPerStep = (2 * kLoads + kSpread - 1) / kSpread;  // DMA loads per k16 step
+constexpr int TM = 4, TN = 4;  // 32x32 tiles per wave (128 x 128)
+static_assert(kStages * 2 * kSlots * 16 <= 160 * 1024, "LDS budget");
+static_assert(kPerStep <= TM * TN && TM + TN <= TM * TN &&
+                  kSpread <= BK / 16,
+              "one DMA load and one fragment read per MFMA at most");
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// vmcnt(n) with expcnt and lgkmcnt left free; lgkmcnt(0) with the others
+// free (gfx9 encodings).
+#define NOVA_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
+#define NOVA_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xC07F)
+
+// Swizzles, conflict-free whether the LDS serves 8 or 16 lanes of a
+// ds_read_b128 per cycle (16 or 32 lanes of a ds_read_b64_tr_b16):
+//   K-contiguous: chunk c of row r at c ^ f(r)
+//   M/N-contiguous: 16-byte chunk c of k-row k at c ^ (2(k&3) ^ 4(k&3))
+__device__ __forceinline__ int kc_swz(int row) {
+  if constexpr (kChunks == 8) return (row ^ (row >> 3)) & 7;
+  else return ((row >> 1) ^ (row >> 2)) & 3;
+}
+__device__ __forceinline__ int kc_slot(int row, int c) { return row * kChunks + (c ^ kc_swz(row)); }
+__device__ __forceinline__ int mn_swz(int k) { return ((k & 3) << 1) ^ ((k & 3) << 2); }
+__device__ __forceinline__ int mn_slot(int k, int c16) { return k * 32 + (c16 ^ mn_swz(k)); }
+
+struct DmaOperand {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[kLoads];  // this lane's byte offset for each of its DMA loads, k0 = 0
+  uint32_t k_step;       // bytes to advance one K tile
+};
+
+// Per-lane source offsets: wave w's load i fills slots [(i*4 + w) * 64, +64).
+// Slot s holds the chunk kc_slot / mn_slot place there (the XOR swizzle is
+// its own inverse).
+template <bool KC>
+__device__ __forceinline__ void dma_setup(DmaOperand &o, int64_t s_outer, int row0, int wave,
+                                          int lane) {
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int s = (i * 4 + wave) * 64 + lane;
+    int64_t e;
+    if constexpr (KC) {
+      const int row = s / kChunks, c = (s % kChunks) ^ kc_swz(s / kChunks);
+      e = (int64_t)(row0 + row) * s_outer + c * 8;
+    } else {
+      const int k = s >> 5, c16 = (s & 31) ^ mn_swz(s >> 5);
+      e = (int64_t)k * s_outer + row0 + c16 * 8;
+    }
+    o.off[i] = (uint32_t)(e * 2);
+  }
+  o.k_step = KC ? (uint32_t)(BK * 2) : (uint32_t)(BK * s_outer * 2);
+}
+
+// DMA load q of K tile kt: q < kLoads are A's loads into sa, the rest B's
+// into sb (kt past the end: the offset falls outside the buffer range and
+// nothing is read).
+__device__ __forceinline__ void dma_load(const DmaOperand &oa, const DmaOperand &ob, u32x4 *sa,
+                                         u32x4 *sb, int q, int kt, int nk, int wave) {
+  const bool live = kt < nk;
+  if (q < kLoads)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(oa.rsrc, (lds_void *)(sa + (q * 4 + wave) * 64), 16,
+                                             live ? oa.off[q] + (uint32_t)kt * oa.k_step : kOOB, 0,
+                                             0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        ob.rsrc, (lds_void *)(sb + ((q - kLoads) * 4 + wave) * 64), 16,
+        live ? ob.off[q - kLoads] + (uint32_t)kt * ob.k_step : kOOB, 0, 0, 0);
+}
+
+// LDS reads as inline assembly.  Written as intrinsics or plain loads, the
+// compiler assumes they may read what any in-flight LDS DMA writes and
+// drains the DMA queue (vmcnt) before them; it cannot tell the two ring
+// stages apart.  As assembly they are invisible to that analysis, and the
+// kernel places the lgkmcnt waits for them itself.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const lds_void *)p;
+}
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ u32x2v lds_read_tr(uint32_t addr) {
+  u32x2v v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Fragment of a 32-row block for k16-step kk (issued, not yet landed).
+template <bool KC>
+__device__ __forceinline__ u32x4 read_frag(const u32x4 *stage, int row_base, int kk, int lane) {
+  if constexpr (KC) {
+    const int row = row_base + (lane & 31);
+    return lds_read_b128(lds_addr(stage + kc_slot(row, kk * 2 + (lane >> 5))));
+  } else {
+    const int g = lane >> 4, p = lane & 15;
+    const int n = row_base + 16 * (g & 1) + 4 * (p & 3);
+    const int kb = kk * 16 + 8 * (g >> 1) + (p >> 2);
+    const uint16_t *base = reinterpret_cast<const uint16_t *>(stage);
+    const int e0 = mn_slot(kb, n >> 3) * 8 + (n & 7);
+    const int e1 = mn_slot(kb + 4, n >> 3) * 8 + (n & 7);
+    const u32x2v lo = lds_read_tr(lds_addr(base + e0));
+    const u32x2v hi = lds_read_tr(lds_addr(base + e1));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
+}
+
+template <int DT, bool AKC, bool BKC, int ODT>
+__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
+  __shared__ u32x4 ring_a[kStages][kSlots];
+  __shared__ u32x4 ring_b[kStages][kSlots];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int bidx, tm, tn;
+  round_tile_of(blockIdx.x, a, bidx, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  DmaOperand oa, ob;
+  oa.rsrc = make_rsrc(a.A + (int64_t)bidx * a.sab, a.a_bytes);
+  ob.rsrc = make_rsrc(a.B + (int64_t)bidx * a.sbb, a.b_bytes);
+  dma_setup<AKC>(oa, a.sa_outer, m0, wave, lane);
+  dma_setup<BKC>(ob, a.sb_outer, n0, wave, lane);
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int nk = a.K / BK;
+  const int am = wm * 128, bn = wn * 128;
+  constexpr int kSteps = BK / 16;
+  constexpr int kFrags = TM + TN;
+
+  u32x4 fa[2][TM], fb[2][TN];
+
+  // (Every lambda here must inline: a call would force acc into memory.)
+  auto read_one = [&](int f, int buf, const u32x4 *A, const u32x4 *B, int kk)
+                      __attribute__((always_inline)) {
+    if (f < TM) fa[buf][f] = read_frag<AKC>(A, am + f * 32, kk, lane);
+    else fb[buf][f - TM] = read_frag<BKC>(B, bn + (f - TM) * 32, kk, lane);
+  };
+  auto mfma_one = [&](int m, int buf) __attribute__((always_inline)) {
+    const int i = m / TN, j = m % TN;
+    acc[i][j] = mfma_32x32x16<DT>(fb[buf][j], fa[buf][i], acc[i][j]);
+  };
+
+  // The DMA of tile t+2 goes into tile t's stage, which is free from tile
+  // t's barrier on.  Its 2*kLoads loads are spread over kSpread k16 steps:
+  // portion 0 in the last step of tile t (after the barrier), portion p in
+  // step p-1 of tile t+1.  All must land before tile t+1's barrier, which
+  // waits for them (vmcnt(0)) ahead of the first read of tile t+2.
+  auto dma_portion = [&](int p, u32x4 *sa, u32x4 *sb, int kt, int m)
+                         __attribute__((always_inline)) {
+    if (m < kPerStep && p * kPerStep + m < 2 * kLoads)
+      dma_load(oa, ob, sa, sb, p * kPerStep + m, kt, nk, wave);
+  };
+
+  // Prologue: tile 0 and portion 0 of tile 1 in flight, tile 0 landed, its
+  // first fragments read.
+#pragma unroll
+  for (int q = 0; q < 2 * kLoads; ++q) dma_load(oa, ob, ring_a[0], ring_b[0], q, 0, nk, wave);
+#pragma unroll
+  for (int m = 0; m < kPerStep; ++m) dma_portion(0, ring_a[1], ring_b[1], 1, m);
+  NOVA_WAIT_VMCNT(kPerStep);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int f = 0; f < kFrags; ++f) read_one(f, 0, ring_a[0], ring_b[0], 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Every instruction group below is fenced with sched_barrier(0), so the
+  // order written is the order issued: MFMA m of a k16 step, then the
+  // fragment read m of the next step, then DMA load m of the step's portion.
+  int cur = 0;
+  for (int t = 0; t < nk; ++t) {
+    u32x4 *A = ring_a[cur], *B = ring_b[cur];
+    const int nxt = cur ^ 1;
+#pragma unroll
+    for (int s = 0; s < kSteps - 1; ++s) {
+      NOVA_WAIT_LGKMCNT0();  // fragments of step s
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < TM * TN; ++m) {
+        mfma_one(m, s & 1);
+        if (m < kFrags) read_one(m, (s + 1) & 1, A, B, s + 1);
+        if (s + 1 < kSpread) dma_portion(s + 1, ring_a[nxt], ring_b[nxt], t + 1, m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // This wave's fragments of the last step and its DMA of tile t+1 have
+    // landed; after the barrier everyone's have, and tile t's stage is free.
+    NOVA_WAIT_LGKMCNT0();
+    NOVA_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // Last step: tile t+1's first fragments and portion 0 of tile t+2's DMA.
+#pragma unroll
+    for (int m = 0; m < TM * TN; ++m) {
+      mfma_one(m, (kSteps - 1) & 1);
+      if (m < kFrags) read_one(m, 0, ring_a[nxt], ring_b[nxt], 0);
+      dma_portion(0, A, B, t + 2, m);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    cur = nxt;
+  }
+  // No DMA may still target this workgroup's LDS when it retires, and the
+  // (unused) fragment reads past the last tile must have landed.
+  NOVA_WAIT_VMCNT(0);
+  NOVA_WAIT_LGKMCNT0();
+  __builtin_amdgcn_sched_barrier(0);
+
+  store_full_epi<TM, TN, ODT>(acc, a, bidx, m0 + am, n0 + bn, lane);
+}
+
+template <int DT, bool AKC, bool BKC, int ODT>
+int32_t launch(const GemmArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, AKC, BKC, ODT>),
+                     dim3((unsigned)(a.batch * a.tiles_m * a.tiles_n)), dim3(kThreads), 0, s, a);
+  return check_hip(hipGetLastError(), "gemm_dma launch");
+}
+
+template <int ODT>
+int32_t launch_out(const GemmArgs &a, int in_dt, bool akc, bool bkc, hipStream_t s) {
+  if (in_dt == NOVA_HIP_DT_BF16) {
+    if (akc && bkc) return launch<NOVA_HIP_DT_BF16, true, true, ODT>(a, s);
+    if (akc) return launch<NOVA_HIP_DT_BF16, true, false, ODT>(a, s);
+    if (bkc) return launch<NOVA_HIP_DT_BF16, false, true, ODT>(a, s);
+    return launch<NOVA_HIP_DT_BF16, false, false, ODT>(a, s);
+  }
+  if (akc && bkc) return launch<NOVA_HIP_DT_F16, true, true, ODT>(a, s);
+  if (akc) return launch<NOVA_HIP_DT_F16, true, false, ODT>(a, s);
+  if (bkc) return launch<NOVA_HIP_DT_F16, false, true, ODT>(a, s);
+  return launch<NOVA_HIP_DT_F16, false, false, ODT>(a, s);
+}
+
+}  // namespace dma
+}  // namespace nova_hip
