@@ -53,7 +53,7 @@ def parse():
                     help="skip the CPU oracle timing (cpu_baseline becomes null)")
     ap.add_argument("--only", default="",
                     help="comma list of configs to run (c2,c3,c4,ln,sce,sce_bwd,sce_fwd_bwd,ln_bwd,"
-                         "c3_bwd; copy = HBM copy calibration)")
+                         "c3_bwd,c2_vendor; copy = HBM copy calibration)")
     return ap.parse_args()
 
 
@@ -289,6 +289,28 @@ def bench_c3_bwd(args, torch, nh, S):
     return {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS}
 
 
+def bench_c2_vendor(args, torch, S):
+    """The vendor library on config 2 for comparison, not part of this
+    build: torch.bmm (hipBLASLt on ROCm) with bf16 inputs and f32 output,
+    the same inputs and timing as bench_c2."""
+    inp = S.config_inputs("c2")
+    A = to_dev(inp["A"], S.BF16, torch)
+    B = to_dev(inp["B"], S.BF16, torch)
+    del inp
+    C = torch.empty(8, 4096, 4096, device="cuda", dtype=torch.float32)
+
+    def fn(_):
+        torch.bmm(A, B, out_dtype=torch.float32, out=C)
+
+    try:
+        ms = time_launches(fn, args.steps, args.warmup, torch)
+    except (TypeError, RuntimeError) as e:  # torch without out_dtype support
+        return {"error": str(e)[:200]}
+    tf = C2_FLOP / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+            "library": "torch.bmm(out_dtype=float32) -> hipBLASLt"}
+
+
 def bench_copy(args, torch):
     """A plain device copy of 256 MiB (torch's copy kernel): the practical
     read+write HBM ceiling the reductions are compared with, and the known
@@ -347,7 +369,8 @@ def main():
     torch.cuda.set_device(0)
     nh.lib()
     only = (set(args.only.split(",")) if args.only else
-            {"c2", "c3", "c4", "ln", "sce", "sce_bwd", "sce_fwd_bwd", "ln_bwd", "c3_bwd"})
+            {"c2", "c3", "c4", "ln", "sce", "sce_bwd", "sce_fwd_bwd", "ln_bwd", "c3_bwd",
+             "c2_vendor"})
     cfg = {}
 
     def stage(name, f):
@@ -380,6 +403,8 @@ def main():
             "ln_bwd", lambda: bench_ln_bwd(args, torch, nh, S))
     if "c3_bwd" in only:
         cfg["c3_linear_backward_bf16_f32"] = stage("c3_bwd", lambda: bench_c3_bwd(args, torch, nh, S))
+    if "c2_vendor" in only:
+        cfg["c2_vendor_hipblaslt_reference"] = stage("c2_vendor", lambda: bench_c2_vendor(args, torch, S))
     if "copy" in only:  # calibration only; not part of the default run
         cfg["hbm_copy_256MiB"] = stage("copy", lambda: bench_copy(args, torch))
 
