@@ -254,60 +254,6 @@ __device__ __forceinline__ void store_outputs(const f32x16 (&acc)[TM][TN], const
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Epilogue for full tiles when the MFMAs were issued with B as the first
-// operand, so acc[i][j] holds the 32x32 output tile transposed: lane l owns
-// output row (l % 32) and, for g = 0..3, the four consecutive columns
-// 8g + 4(l/32) + 0..3 in elements v = 4g .. 4g+3.  Every four outputs are
-// one 16-byte (f32) or 8-byte (bf16/f16) store; no bounds checks (full tiles
-// only).  Specialised on the output dtype only: bias and GELU are uniform
-// branches, and the four bias values of a column group are loaded right
-// before the TM stores that use them, so no more than four registers hold
-// bias (hoisting all TN*16 of them made the kernel spill).
-template <int TM, int TN, int ODT>
-__device__ __forceinline__ void store_full_epi(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
-                                               int bidx, int mw, int nw, int lane) {
-  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
-  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
-  constexpr int kEsz = ODT == NOVA_HIP_DT_F32 ? 4 : 2;
-  const int lr = lane & 31, lh = lane >> 5;
-  char *Cb = static_cast<char *>(a.C) + (int64_t)bidx * a.scb * kEsz;
-  char *row0 = Cb + ((int64_t)(mw + lr) * a.scm + nw + 4 * lh) * kEsz;
-  const int64_t row_step = (int64_t)32 * a.scm * kEsz;  // 32 output rows
-#pragma unroll
-  for (int j = 0; j < TN; ++j)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-      if (has_bias) {
-        const int n = nw + 32 * j + 8 * g + 4 * lh;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] = bias_at(a.bias, a.bias_dt, n + e);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        f32x4 x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                   acc[i][j][4 * g + 3]};
-        if (has_bias) x = x + bv;
-        if (has_gelu) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = gelu_tanh_fast(x[e]);
-        }
-        char *dst = row0 + i * row_step + (32 * j + 8 * g) * kEsz;
-        if constexpr (ODT == NOVA_HIP_DT_F32) {
-          *reinterpret_cast<f32x4 *>(dst) = x;
-        } else if constexpr (ODT == NOVA_HIP_DT_BF16) {
-          *reinterpret_cast<u32x2 *>(dst) =
-              u32x2{to_bf16(x[0]) | ((uint32_t)to_bf16(x[1]) << 16),
-                    to_bf16(x[2]) | ((uint32_t)to_bf16(x[3]) << 16)};
-        } else {
-          *reinterpret_cast<u32x2 *>(dst) =
-              u32x2{to_f16(x[0]) | ((uint32_t)to_f16(x[1]) << 16),
-                    to_f16(x[2]) | ((uint32_t)to_f16(x[3]) << 16)};
-        }
-      }
-    }
-}
-
 }  // namespace gemm
 
 // Launchers (host).  launch_gemm_dma returns NOVA_HIP_EDTYPE when the

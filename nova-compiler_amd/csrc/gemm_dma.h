@@ -158,6 +158,87 @@ __device__ __forceinline__ u32x4 read_frag(const u32x4 *stage, int row_base, int
   }
 }
 
+// Epilogue of a wave's 128x128 output tile, staged through kStageBytes of
+// LDS so that every global store instruction writes whole 128-byte lines.
+// Stored straight from the accumulators (lane l holding 16 or 8 bytes of
+// one row, 32 rows per instruction) the lines were written in 32-byte
+// slices, and while the DMA stream cycled the L2 some partly written lines
+// were evicted and written back more than once (20-35% more HBM writes than
+// the output).  Here the accumulators go to LDS in output layout (bias and
+// GELU applied on the way), and are read back as whole row segments: f32 in
+// two rounds of 64 rows x 512 B, bf16/f16 in one round of 128 rows x 256 B.
+// 16-byte chunk c of LDS row R sits at chunk c ^ (R mod #chunks per row),
+// which keeps both the column-wise writes and the row-wise reads free of
+// bank conflicts.
+constexpr int kStageBytes = 32768;
+static_assert(4 * kStageBytes <= kStages * 2 * kSlots * 16, "staging fits the ring");
+
+template <int ODT>
+__device__ __forceinline__ void store_staged(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
+                                             int bidx, int mw, int nw, int lane, char *stg) {
+  static_assert(TM == 4 && TN == 4, "staging assumes a 128x128 wave tile");
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
+  const int lr = lane & 31, lh = lane >> 5;
+  constexpr bool kF32 = ODT == NOVA_HIP_DT_F32;
+  constexpr int kRounds = kF32 ? 2 : 1;      // 64 or 128 rows per round
+  constexpr int kRowBytes = kF32 ? 512 : 256;
+  constexpr int kChunks = kRowBytes / 16;    // 16-byte chunks per LDS row
+  constexpr int kEsz = kF32 ? 4 : 2;
+  char *Cb = static_cast<char *>(a.C) + (int64_t)bidx * a.scb * kEsz;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        if (has_bias) {
+          const int n = nw + 32 * j + 8 * g + 4 * lh;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[e] = bias_at(a.bias, a.bias_dt, n + e);
+        }
+#pragma unroll
+        for (int ii = 0; ii < TM / kRounds; ++ii) {
+          const int i = r * (TM / kRounds) + ii;
+          f32x4 x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                     acc[i][j][4 * g + 3]};
+          if (has_bias) x = x + bv;
+          if (has_gelu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = gelu_tanh_fast(x[e]);
+          }
+          const int R = 32 * ii + lr;  // row within the round
+          if constexpr (kF32) {
+            const int c = 8 * j + 2 * g + lh;
+            *reinterpret_cast<f32x4 *>(stg + R * kRowBytes + ((c ^ (R & (kChunks - 1))) << 4)) = x;
+          } else {
+            const int c = 4 * j + g;
+            const u32x2 w = ODT == NOVA_HIP_DT_BF16
+                                ? u32x2{to_bf16(x[0]) | ((uint32_t)to_bf16(x[1]) << 16),
+                                        to_bf16(x[2]) | ((uint32_t)to_bf16(x[3]) << 16)}
+                                : u32x2{to_f16(x[0]) | ((uint32_t)to_f16(x[1]) << 16),
+                                        to_f16(x[2]) | ((uint32_t)to_f16(x[3]) << 16)};
+            *reinterpret_cast<u32x2 *>(stg + R * kRowBytes + ((c ^ (R & (kChunks - 1))) << 4) +
+                                       8 * lh) = w;
+          }
+        }
+      }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes done
+    constexpr int kRowsPerInst = 1024 / kRowBytes;  // 64 lanes x 16 bytes
+    constexpr int kRoundRows = 128 / kRounds;
+#pragma unroll
+    for (int t = 0; t < kRoundRows / kRowsPerInst; ++t) {
+      const int R = kRowsPerInst * t + lane / kChunks, c = lane % kChunks;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + R * kRowBytes +
+                                                       ((c ^ (R & (kChunks - 1))) << 4));
+      char *dst = Cb + ((int64_t)(mw + kRoundRows * r + R) * a.scm + nw) * kEsz + 16 * c;
+      *reinterpret_cast<u32x4 *>(dst) = v;
+    }
+    if (r + 1 < kRounds) __builtin_amdgcn_s_waitcnt(0xC07F);  // reads done before the next round
+  }
+}
+
 template <int DT, bool AKC, bool BKC, int ODT>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
   __shared__ u32x4 ring_a[kStages][kSlots];
@@ -269,7 +350,12 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
   NOVA_WAIT_LGKMCNT0();
   __builtin_amdgcn_sched_barrier(0);
 
-  store_full_epi<TM, TN, ODT>(acc, a, bidx, m0 + am, n0 + bn, lane);
+  // Epilogue through LDS (the ring is free once every wave is past its last
+  // fragment read).
+  __syncthreads();
+  char *stg = (wave < 2 ? reinterpret_cast<char *>(ring_a) : reinterpret_cast<char *>(ring_b)) +
+              (wave & 1) * kStageBytes;
+  store_staged<ODT>(acc, a, bidx, m0 + am, n0 + bn, lane, stg);
 }
 
 template <int DT, bool AKC, bool BKC, int ODT>
