@@ -1,0 +1,1229 @@
+// libnova_run: MLIR-free planner and executor for Nova programs in the op
+// surface of this path (C ABI in include/nova_run.h).
+//
+// Three stages:
+//   parse   -- a small reader for the textual IR nova-opt consumes: func.func
+//              signatures, one op per statement (lines joined while brackets
+//              are open), nova / linalg / tensor / arith / bufferization ops
+//              of the subset, tensor and memref types with static shapes.
+//              Result types of nova ops are inferred as the reference's
+//              inferReturnTypes do (NovaOps.cpp:1116-1285 matmul, 2032-2053
+//              layer_norm, 2075-2103 linear, 1648-1677 sce).
+//   plan    -- each value gets a physical view (buffer, shape, strides,
+//              stored dtype).  nova.transpose of the last two dims is a view;
+//              a widening nova.cast (bf16/f16 -> f32, exact) keeps the stored
+//              dtype, so the GEMM that consumes it reads the narrow operand
+//              directly (the config-2/3 forms nova.cast -> nova.matmul /
+//              nova.linear); a nova.gelu and a narrowing nova.cast on a GEMM
+//              result with no other use fold into the GEMM epilogue
+//              (FuseMatmulBias.cpp:95-199 puts the bias there already).  Every
+//              remaining op maps to one libnova_hip entry point.
+//   execute -- device buffers for every planned buffer, host->device copies
+//              of the arguments, the launches on the calling thread's stream,
+//              one synchronisation, device->host copies of the results.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <memory>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/nova_hip.h"
+#include "../../include/nova_run.h"
+
+namespace {
+
+thread_local char t_err[1024] = {0};
+
+int32_t fail(int32_t code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(t_err, sizeof(t_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_I32 = 3, DT_I64 = 4 };
+const char *dt_name(int dt) {
+  static const char *n[] = {"f32", "bf16", "f16", "i32", "i64"};
+  return dt >= 0 && dt <= 4 ? n[dt] : "?";
+}
+int dt_size(int dt) { return dt == DT_F32 || dt == DT_I32 ? 4 : dt == DT_I64 ? 8 : 2; }
+
+struct Type {
+  std::vector<int64_t> shape;
+  int dt = -1;
+  bool memref = false;
+  int64_t numel() const {
+    int64_t n = 1;
+    for (int64_t d : shape) n *= d;
+    return n;
+  }
+};
+
+struct Op {
+  std::string name;
+  std::vector<std::string> results;
+  std::vector<std::string> operands;
+  std::vector<Type> operand_types;
+  std::vector<Type> result_types;
+  std::map<std::string, std::string> attrs;
+  std::string literal;  // arith.constant value
+  int line = 0;
+};
+
+struct Func {
+  std::string name;
+  std::vector<std::string> arg_names;
+  std::vector<Type> arg_types;
+  std::vector<Op> ops;
+  std::vector<std::string> rets;
+  std::vector<Type> ret_types;
+};
+
+// ---- text helpers ----------------------------------------------------------
+std::string trim(const std::string &s) {
+  size_t a = 0, b = s.size();
+  while (a < b && isspace((unsigned char)s[a])) ++a;
+  while (b > a && isspace((unsigned char)s[b - 1])) --b;
+  return s.substr(a, b - a);
+}
+
+// Split at top-level occurrences of `sep` (outside (), <>, [], {}).
+std::vector<std::string> split_top(const std::string &s, char sep) {
+  std::vector<std::string> out;
+  int depth = 0;
+  size_t start = 0;
+  for (size_t i = 0; i < s.size(); ++i) {
+    const char c = s[i];
+    if (c == '(' || c == '<' || c == '[' || c == '{') ++depth;
+    else if (c == ')' || c == '>' || c == ']' || c == '}') --depth;
+    else if (c == sep && depth == 0) {
+      out.push_back(trim(s.substr(start, i - start)));
+      start = i + 1;
+    }
+  }
+  out.push_back(trim(s.substr(start)));
+  if (out.size() == 1 && out[0].empty()) out.clear();
+  return out;
+}
+
+// Index of the first top-level `c`, or npos.
+size_t find_top(const std::string &s, char c, size_t from = 0) {
+  int depth = 0;
+  for (size_t i = from; i < s.size(); ++i) {
+    const char x = s[i];
+    if (x == c && depth == 0) return i;
+    if (x == '(' || x == '<' || x == '[' || x == '{') ++depth;
+    else if (x == ')' || x == '>' || x == ']' || x == '}') --depth;
+  }
+  return std::string::npos;
+}
+
+// Matching close bracket for the open one at s[i].
+size_t match_close(const std::string &s, size_t i) {
+  const char open = s[i];
+  const char close = open == '(' ? ')' : open == '{' ? '}' : open == '[' ? ']' : '>';
+  int depth = 0;
+  for (size_t j = i; j < s.size(); ++j) {
+    if (s[j] == open) ++depth;
+    else if (s[j] == close && --depth == 0) return j;
+  }
+  return std::string::npos;
+}
+
+bool parse_type(const std::string &s_in, Type &t) {
+  const std::string s = trim(s_in);
+  size_t lt = s.find('<');
+  if (lt == std::string::npos) return false;
+  const std::string kind = trim(s.substr(0, lt));
+  if (kind != "tensor" && kind != "memref") return false;
+  t.memref = kind == "memref";
+  const size_t gt = match_close(s, lt);
+  if (gt == std::string::npos) return false;
+  std::string body = s.substr(lt + 1, gt - lt - 1);
+  // memref<...xf32, 1>: drop a memory space / layout after the first comma
+  const size_t comma = find_top(body, ',');
+  if (comma != std::string::npos) body = body.substr(0, comma);
+  body = trim(body);
+  t.shape.clear();
+  size_t pos = 0;
+  while (true) {
+    const size_t x = body.find('x', pos);
+    const std::string tok = body.substr(pos, x == std::string::npos ? std::string::npos : x - pos);
+    if (!tok.empty() && isdigit((unsigned char)tok[0]) && x != std::string::npos) {
+      t.shape.push_back(strtoll(tok.c_str(), nullptr, 10));
+      pos = x + 1;
+      continue;
+    }
+    const std::string el = trim(body.substr(pos));
+    if (el == "f32") t.dt = DT_F32;
+    else if (el == "bf16") t.dt = DT_BF16;
+    else if (el == "f16") t.dt = DT_F16;
+    else if (el == "i32") t.dt = DT_I32;
+    else if (el == "i64") t.dt = DT_I64;
+    else return false;
+    return true;
+  }
+}
+
+// Strip `//` comments.
+std::string strip_comments(const std::string &text) {
+  std::string out;
+  size_t i = 0;
+  while (i < text.size()) {
+    const size_t nl = text.find('\n', i);
+    std::string line = text.substr(i, nl == std::string::npos ? std::string::npos : nl - i);
+    const size_t c = line.find("//");
+    if (c != std::string::npos) line = line.substr(0, c);
+    out += line;
+    out += '\n';
+    if (nl == std::string::npos) break;
+    i = nl + 1;
+  }
+  return out;
+}
+
+int line_of(const std::string &text, size_t pos) {
+  int n = 1;
+  for (size_t i = 0; i < pos && i < text.size(); ++i) n += text[i] == '\n';
+  return n;
+}
+
+// ---- op parsing --------------------------------------------------------------
+// Operand names (%x) in a comma list, skipping keyword pairs and attr dicts.
+std::vector<std::string> operand_names(const std::string &s) {
+  std::vector<std::string> out;
+  for (const std::string &part : split_top(s, ',')) {
+    std::string p = trim(part);
+    if (!p.empty() && p[0] == '%') {
+      size_t e = 1;
+      while (e < p.size() && (isalnum((unsigned char)p[e]) || p[e] == '_' || p[e] == '#')) ++e;
+      out.push_back(p.substr(0, e));
+    }
+  }
+  return out;
+}
+
+void parse_attr_dict(const std::string &s, std::map<std::string, std::string> &attrs) {
+  const size_t lb = s.find('{');
+  if (lb == std::string::npos) return;
+  const size_t rb = match_close(s, lb);
+  if (rb == std::string::npos) return;
+  for (const std::string &kv : split_top(s.substr(lb + 1, rb - lb - 1), ',')) {
+    const size_t eq = kv.find('=');
+    if (eq == std::string::npos) continue;
+    std::string v = trim(kv.substr(eq + 1));
+    const size_t colon = find_top(v, ':');
+    if (colon != std::string::npos) v = trim(v.substr(0, colon));
+    attrs[trim(kv.substr(0, eq))] = v;
+  }
+}
+
+// `ins(%a, %b : t1, t2)` -> names and types.
+bool parse_ins_outs(const std::string &s, const char *kw, std::vector<std::string> &names,
+                    std::vector<Type> &types) {
+  const size_t k = s.find(kw);
+  if (k == std::string::npos) return false;
+  const size_t lp = s.find('(', k);
+  const size_t rp = lp == std::string::npos ? lp : match_close(s, lp);
+  if (rp == std::string::npos) return false;
+  const std::string in = s.substr(lp + 1, rp - lp - 1);
+  const size_t colon = find_top(in, ':');
+  if (colon == std::string::npos) return false;
+  names = operand_names(in.substr(0, colon));
+  for (const std::string &ts : split_top(in.substr(colon + 1), ',')) {
+    Type t;
+    if (parse_type(ts, t)) types.push_back(t);
+    else if (trim(ts) == "f32" || trim(ts) == "bf16" || trim(ts) == "f16") {
+      t.dt = trim(ts) == "f32" ? DT_F32 : trim(ts) == "bf16" ? DT_BF16 : DT_F16;
+      types.push_back(t);  // scalar (rank 0)
+    } else {
+      return false;
+    }
+  }
+  return names.size() == types.size();
+}
+
+int32_t parse_op(const std::string &stmt, int line, Op &op) {
+  op.line = line;
+  std::string rest = stmt;
+  const size_t eq = find_top(stmt, '=');
+  if (eq != std::string::npos && stmt[0] == '%') {
+    for (const std::string &r : split_top(stmt.substr(0, eq), ',')) {
+      const size_t colon = r.find(':');
+      if (colon != std::string::npos) {  // %r:3
+        const std::string base = trim(r.substr(0, colon));
+        const int n = atoi(r.c_str() + colon + 1);
+        for (int i = 0; i < n; ++i) op.results.push_back(base + "#" + std::to_string(i));
+      } else {
+        op.results.push_back(trim(r));
+      }
+    }
+    rest = trim(stmt.substr(eq + 1));
+  }
+  size_t sp = 0;
+  while (sp < rest.size() && !isspace((unsigned char)rest[sp]) && rest[sp] != '(') ++sp;
+  op.name = rest.substr(0, sp);
+  const std::string body = trim(rest.substr(sp));
+
+  if (op.name == "linalg.matmul" || op.name == "linalg.batch_matmul" || op.name == "linalg.fill") {
+    std::vector<std::string> in, out;
+    std::vector<Type> tin, tout;
+    if (!parse_ins_outs(body, "ins", in, tin) || !parse_ins_outs(body, "outs", out, tout))
+      return fail(NOVA_HIP_EINVAL, "line %d: cannot read ins/outs of %s", line, op.name.c_str());
+    op.operands = in;
+    op.operand_types = tin;
+    op.operands.insert(op.operands.end(), out.begin(), out.end());
+    op.operand_types.insert(op.operand_types.end(), tout.begin(), tout.end());
+    op.result_types = tout;
+    return NOVA_HIP_SUCCESS;
+  }
+  if (op.name == "tensor.empty") {
+    Type t;
+    const size_t colon = find_top(body, ':');
+    if (colon == std::string::npos || !parse_type(body.substr(colon + 1), t))
+      return fail(NOVA_HIP_EINVAL, "line %d: cannot read tensor.empty type", line);
+    op.result_types.push_back(t);
+    return NOVA_HIP_SUCCESS;
+  }
+  if (op.name == "arith.constant") {
+    const size_t colon = find_top(body, ':');
+    op.literal = trim(body.substr(0, colon));
+    return NOVA_HIP_SUCCESS;
+  }
+  if (op.name == "bufferization.to_tensor") {
+    // %arg restrict : memref<...> to tensor<...>
+    const size_t colon = find_top(body, ':');
+    op.operands = operand_names(body.substr(0, colon));
+    const std::string ts = body.substr(colon + 1);
+    const size_t to = ts.rfind(" to ");
+    Type t;
+    if (to == std::string::npos || !parse_type(ts.substr(to + 4), t))
+      return fail(NOVA_HIP_EINVAL, "line %d: cannot read bufferization.to_tensor", line);
+    op.result_types.push_back(t);
+    return NOVA_HIP_SUCCESS;
+  }
+  if (op.name == "bufferization.materialize_in_destination") {
+    // %v in writable %arg : (tensor, memref) -> ()
+    const size_t colon = find_top(body, ':');
+    std::string head = body.substr(0, colon);
+    const size_t in = head.find(" in ");
+    if (in == std::string::npos)
+      return fail(NOVA_HIP_EINVAL, "line %d: cannot read materialize_in_destination", line);
+    op.operands = operand_names(head.substr(0, in));
+    std::string dst = trim(head.substr(in + 4));
+    if (dst.compare(0, 8, "writable") == 0) dst = trim(dst.substr(8));
+    const std::vector<std::string> d = operand_names(dst);
+    op.operands.insert(op.operands.end(), d.begin(), d.end());
+    return NOVA_HIP_SUCCESS;
+  }
+  if (op.name.compare(0, 5, "nova.") == 0) {
+    const size_t colon = find_top(body, ':');
+    if (colon == std::string::npos)
+      return fail(NOVA_HIP_EINVAL, "line %d: %s has no type list", line, op.name.c_str());
+    std::string head = body.substr(0, colon), tail = body.substr(colon + 1);
+    parse_attr_dict(head, op.attrs);
+    // keyword attributes of nova.transpose: `axes1 = -1 axes2 = -2`
+    // (written before any attr-dict)
+    for (const char *kw : {"axes1", "axes2"}) {
+      const size_t lb0 = head.find('{');
+      const size_t k = head.find(kw);
+      if (k == std::string::npos || (lb0 != std::string::npos && k > lb0)) continue;
+      const size_t eqk = head.find('=', k);
+      if (eqk == std::string::npos) continue;
+      op.attrs[kw] = std::to_string(strtol(head.c_str() + eqk + 1, nullptr, 10));
+    }
+    const size_t lb = head.find('{');
+    op.operands = operand_names(lb == std::string::npos ? head : head.substr(0, lb));
+    const size_t arrow = find_top(tail, '-');
+    std::string res_t;
+    if (arrow != std::string::npos && arrow + 1 < tail.size() && tail[arrow + 1] == '>') {
+      res_t = tail.substr(arrow + 2);
+      tail = tail.substr(0, arrow);
+    }
+    for (const std::string &ts : split_top(tail, ',')) {
+      Type t;
+      if (!parse_type(ts, t))
+        return fail(NOVA_HIP_EINVAL, "line %d: unsupported type '%s' (static tensor shapes of f32/bf16/f16/i32/i64 only)",
+                    line, ts.c_str());
+      op.operand_types.push_back(t);
+    }
+    if (!res_t.empty()) {
+      Type t;
+      if (!parse_type(res_t, t)) return fail(NOVA_HIP_EINVAL, "line %d: bad result type", line);
+      op.result_types.push_back(t);
+    }
+    if (op.operand_types.size() != op.operands.size())
+      return fail(NOVA_HIP_EINVAL, "line %d: %s lists %zu operands and %zu types", line,
+                  op.name.c_str(), op.operands.size(), op.operand_types.size());
+    return NOVA_HIP_SUCCESS;
+  }
+  return fail(NOVA_HIP_EINVAL, "line %d: op '%s' is not part of this path's op surface", line,
+              op.name.c_str());
+}
+
+// ---- result type inference (the reference's inferReturnTypes) -------------------
+int32_t infer(Op &op) {
+  auto &T = op.operand_types;
+  auto need = [&](size_t n) {
+    return T.size() == n ? NOVA_HIP_SUCCESS
+                         : fail(NOVA_HIP_EINVAL, "line %d: %s takes %zu operands", op.line,
+                                op.name.c_str(), n);
+  };
+  std::vector<Type> &R = op.result_types;
+  if (!R.empty() && op.name != "nova.cast") return NOVA_HIP_SUCCESS;
+  int32_t rc;
+  if (op.name == "nova.matmul") {
+    if ((rc = need(2))) return rc;
+    const Type &a = T[0], &b = T[1];
+    if (a.shape.size() < 2 || b.shape.size() < 2)
+      return fail(NOVA_HIP_ESHAPE, "line %d: nova.matmul needs rank >= 2", op.line);
+    Type r;
+    r.shape = a.shape.size() >= b.shape.size() ? a.shape : b.shape;
+    r.shape[r.shape.size() - 2] = a.shape[a.shape.size() - 2];
+    r.shape[r.shape.size() - 1] = b.shape.back();
+    // NovaOps.cpp:1198: bf16 x bf16 and f16 x f16 give f16; f32 gives f32.
+    r.dt = a.dt == DT_F32 ? DT_F32 : DT_F16;
+    R.push_back(r);
+  } else if (op.name == "nova.linear") {
+    if ((rc = need(3))) return rc;
+    Type r = T[0];
+    r.shape.back() = T[1].shape.back();
+    R.push_back(r);
+  } else if (op.name == "nova.gelu") {
+    if ((rc = need(1))) return rc;
+    R.push_back(T[0]);
+  } else if (op.name == "nova.cast") {
+    if ((rc = need(1))) return rc;
+    if (R.size() != 1) return fail(NOVA_HIP_EINVAL, "line %d: nova.cast needs `-> type`", op.line);
+  } else if (op.name == "nova.transpose") {
+    if ((rc = need(1))) return rc;
+    Type r = T[0];
+    const int n = (int)r.shape.size();
+    int a1 = op.attrs.count("axes1") ? atoi(op.attrs["axes1"].c_str()) : -1;
+    int a2 = op.attrs.count("axes2") ? atoi(op.attrs["axes2"].c_str()) : -2;
+    if (a1 < 0) a1 += n;
+    if (a2 < 0) a2 += n;
+    if (n < 2 || a1 < 0 || a2 < 0 || a1 >= n || a2 >= n)
+      return fail(NOVA_HIP_ESHAPE, "line %d: bad transpose axes", op.line);
+    std::swap(r.shape[a1], r.shape[a2]);
+    op.attrs["axes1"] = std::to_string(a1);
+    op.attrs["axes2"] = std::to_string(a2);
+    R.push_back(r);
+  } else if (op.name == "nova.layer_norm") {
+    if ((rc = need(3))) return rc;
+    Type s = T[0];
+    s.shape.pop_back();
+    R = {T[0], s, s};
+  } else if (op.name == "nova.sce") {
+    if ((rc = need(2))) return rc;
+    Type loss;
+    loss.shape = {1};
+    loss.dt = T[0].dt;
+    R = {T[0], loss};
+  } else if (op.name == "nova.sce_backward") {
+    if ((rc = need(2))) return rc;
+    R = {T[0]};
+  } else if (op.name == "nova.layer_norm_backward") {
+    if ((rc = need(5))) return rc;
+    R = {T[1], T[2], T[2]};
+  } else if (op.name == "nova.linear_backward") {
+    if ((rc = need(3))) return rc;
+    Type gb = T[2];
+    gb.shape = {T[2].shape.back()};
+    R = {T[1], T[2], gb};
+  } else if (op.name == "nova.matmul_backward") {
+    if ((rc = need(3))) return rc;
+    R = {T[1], T[2]};
+  } else if (op.name.compare(0, 5, "nova.") == 0) {
+    return fail(NOVA_HIP_EINVAL, "line %d: op '%s' is not part of this path's op surface",
+                op.line, op.name.c_str());
+  }
+  return NOVA_HIP_SUCCESS;
+}
+
+// A single-result op written `%x = nova.sce` names the loss (result 1), as
+// in the reference's own ltest/_sce.mlir.
+void bind_results(Op &op) {
+  if (op.name == "nova.sce" && op.results.size() == 1) op.results = {"", op.results[0]};
+}
+
+int32_t parse_func(const std::string &text, size_t at, size_t &end_out, Func &f) {
+  const size_t name_at = text.find('@', at);
+  const size_t lp = text.find('(', name_at);
+  if (name_at == std::string::npos || lp == std::string::npos)
+    return fail(NOVA_HIP_EINVAL, "line %d: malformed func.func", line_of(text, at));
+  f.name = trim(text.substr(name_at + 1, lp - name_at - 1));
+  const size_t rp = match_close(text, lp);
+  if (rp == std::string::npos) return fail(NOVA_HIP_EINVAL, "unbalanced func signature");
+  for (const std::string &a : split_top(text.substr(lp + 1, rp - lp - 1), ',')) {
+    const size_t colon = a.find(':');
+    if (colon == std::string::npos) return fail(NOVA_HIP_EINVAL, "bad argument '%s'", a.c_str());
+    Type t;
+    std::string ts = a.substr(colon + 1);
+    const size_t brace = find_top(ts, '{');
+    if (brace != std::string::npos) ts = ts.substr(0, brace);
+    if (!parse_type(ts, t))
+      return fail(NOVA_HIP_EINVAL, "line %d: unsupported argument type '%s'", line_of(text, lp),
+                  trim(ts).c_str());
+    f.arg_names.push_back(trim(a.substr(0, colon)));
+    f.arg_types.push_back(t);
+  }
+  const size_t body_lb = text.find('{', rp);
+  // `attributes {...}` before the body
+  size_t lb = body_lb;
+  const size_t attr = text.find("attributes", rp);
+  if (attr != std::string::npos && attr < body_lb) lb = text.find('{', match_close(text, body_lb) + 1);
+  const size_t rb = match_close(text, lb);
+  if (lb == std::string::npos || rb == std::string::npos)
+    return fail(NOVA_HIP_EINVAL, "line %d: func body not closed", line_of(text, at));
+  end_out = rb + 1;
+  // statements: lines joined while brackets are open
+  const std::string body = text.substr(lb + 1, rb - lb - 1);
+  size_t i = 0;
+  std::string stmt;
+  int depth = 0, stmt_line = 0;
+  while (i <= body.size()) {
+    const size_t nl = body.find('\n', i);
+    const std::string ln = body.substr(i, nl == std::string::npos ? std::string::npos : nl - i);
+    if (stmt.empty()) stmt_line = line_of(text, lb + 1 + i);
+    for (char c : ln) depth += (c == '(' || c == '[' || c == '{') - (c == ')' || c == ']' || c == '}');
+    stmt += " " + ln;
+    // A statement also continues on a next line that starts with `outs`,
+    // `->` or `:` (linalg ops written over several lines).
+    bool cont = false;
+    if (depth <= 0 && nl != std::string::npos) {
+      size_t nx = nl + 1;
+      while (nx < body.size() && (body[nx] == ' ' || body[nx] == '\t')) ++nx;
+      cont = body.compare(nx, 4, "outs") == 0 || body.compare(nx, 2, "->") == 0 ||
+             body.compare(nx, 1, ":") == 0;
+    }
+    if (depth <= 0 && !cont) {
+      const std::string s = trim(stmt);
+      stmt.clear();
+      depth = 0;
+      if (!s.empty()) {
+        if (s.compare(0, 6, "return") == 0) {
+          std::string r = trim(s.substr(6));
+          const size_t colon = find_top(r, ':');
+          f.rets = operand_names(colon == std::string::npos ? r : r.substr(0, colon));
+        } else {
+          Op op;
+          int32_t rc = parse_op(s, stmt_line, op);
+          if (rc) return rc;
+          bind_results(op);
+          if ((rc = infer(op))) return rc;
+          f.ops.push_back(op);
+        }
+      }
+    }
+    if (nl == std::string::npos) break;
+    i = nl + 1;
+  }
+  return NOVA_HIP_SUCCESS;
+}
+
+// ---- planning ----------------------------------------------------------------
+struct View {
+  int buf = -1;
+  std::vector<int64_t> shape, strides;  // elements
+  int dt = -1;                          // stored dtype
+  int logical = -1;                     // dtype the program sees
+  bool zero = false;                    // known all-zero (linalg.fill 0)
+  int producer = -1;                    // step that writes the buffer, if a GEMM
+};
+
+struct Buffer {
+  int64_t bytes = 0;
+  int arg = -1;  // host argument index it is copied from, or -1
+};
+
+struct Step {
+  std::string kind;  // gemm, layer_norm, sce, sce_bwd, ln_bwd, lin_bwd, mm_bwd, zero, copy
+  std::vector<View> in, out;
+  int epi = NOVA_HIP_EPI_NONE;
+  int out_dt = DT_F32;
+  std::string text;
+};
+
+std::vector<int64_t> dense_strides(const std::vector<int64_t> &shape) {
+  std::vector<int64_t> st(shape.size(), 1);
+  for (int i = (int)shape.size() - 2; i >= 0; --i) st[i] = st[i + 1] * shape[i + 1];
+  return st;
+}
+
+bool is_dense(const View &v) { return v.strides == dense_strides(v.shape); }
+
+struct Plan {
+  std::vector<Buffer> bufs;
+  std::vector<Step> steps;
+  std::vector<View> results;
+  std::vector<int> out_args;  // writable memref arguments: arg index per materialize step
+};
+
+std::string view_str(const View &v) {
+  std::string s = "b" + std::to_string(v.buf) + "[";
+  for (size_t i = 0; i < v.shape.size(); ++i) s += (i ? "," : "") + std::to_string(v.shape[i]);
+  s += "]";
+  s += dt_name(v.dt);
+  if (!is_dense(v)) {
+    s += " strides(";
+    for (size_t i = 0; i < v.strides.size(); ++i)
+      s += (i ? "," : "") + std::to_string(v.strides[i]);
+    s += ")";
+  }
+  return s;
+}
+
+struct Planner {
+  const Func &f;
+  Plan plan;
+  std::map<std::string, View> env;
+  std::map<std::string, int> uses;
+  std::map<std::string, std::string> consts;
+
+  explicit Planner(const Func &fn) : f(fn) {}
+
+  int new_buf(const Type &t, int arg = -1) {
+    Buffer b;
+    b.bytes = t.numel() * dt_size(t.dt);
+    b.arg = arg;
+    plan.bufs.push_back(b);
+    return (int)plan.bufs.size() - 1;
+  }
+  View fresh(const Type &t) {
+    View v;
+    v.buf = new_buf(t);
+    v.shape = t.shape;
+    v.strides = dense_strides(t.shape);
+    v.dt = v.logical = t.dt;
+    return v;
+  }
+  int32_t get(const Op &op, size_t i, View &v) {
+    auto it = env.find(op.operands[i]);
+    if (it == env.end())
+      return fail(NOVA_HIP_EINVAL, "line %d: %s uses undefined value %s", op.line, op.name.c_str(),
+                  op.operands[i].c_str());
+    v = it->second;
+    return NOVA_HIP_SUCCESS;
+  }
+  int32_t need_f32(const Op &op, const View &v, const char *what) {
+    if (v.dt != DT_F32)
+      return fail(NOVA_HIP_EDTYPE,
+                  "line %d: %s of %s must be stored f32 (a cast from %s is folded only into GEMM "
+                  "operands)",
+                  op.line, what, op.name.c_str(), dt_name(v.dt));
+    return NOVA_HIP_SUCCESS;
+  }
+  // The single consumer of `name` if it has exactly one use, else null.
+  const Op *sole_user(const std::string &name, size_t from) {
+    if (uses[name] != 1) return nullptr;
+    for (size_t k = from; k < f.ops.size(); ++k)
+      for (const std::string &o : f.ops[k].operands)
+        if (o == name) return &f.ops[k];
+    return nullptr;
+  }
+
+  // A GEMM-family step writing `out` (reusing its buffer when it has one of
+  // the output dtype, as a linalg init does); then folds of a following
+  // gelu / narrowing cast.
+  int32_t emit_gemm(const Op &op, size_t idx, View a, View b, const View *bias, View out,
+                    std::set<const Op *> &folded) {
+    if (a.dt != b.dt)
+      return fail(NOVA_HIP_EDTYPE, "line %d: %s operands are stored as %s and %s", op.line,
+                  op.name.c_str(), dt_name(a.dt), dt_name(b.dt));
+    if (a.dt > DT_F16)
+      return fail(NOVA_HIP_EDTYPE, "line %d: %s on %s is not on this path", op.line,
+                  op.name.c_str(), dt_name(a.dt));
+    if (a.dt == DT_F32 && out.dt != DT_F32)
+      return fail(NOVA_HIP_EDTYPE, "line %d: f32 operands give f32 results only", op.line);
+    Step s;
+    s.kind = "gemm";
+    s.in = {a, b};
+    if (bias) s.in.push_back(*bias);
+    s.epi = bias ? NOVA_HIP_EPI_BIAS : NOVA_HIP_EPI_NONE;
+    s.out_dt = out.dt;
+    std::string name = op.results[0];
+    std::string fused = op.name;
+    const Op *u = sole_user(name, idx + 1);
+    if (u && u->name == "nova.gelu") {
+      s.epi = bias ? NOVA_HIP_EPI_BIAS_GELU : NOVA_HIP_EPI_GELU;
+      folded.insert(u);
+      fused += " + nova.gelu";
+      env[u->results[0]] = out;  // placeholder, fixed below
+      name = u->results[0];
+      u = sole_user(name, idx + 1);
+    }
+    if (u && u->name == "nova.cast" && u->result_types[0].dt != DT_F32 && out.dt == DT_F32 &&
+        u->result_types[0].dt <= DT_F16) {
+      s.out_dt = u->result_types[0].dt;
+      folded.insert(u);
+      fused += " + nova.cast";
+      name = u->results[0];
+    }
+    if (out.buf < 0 || out.dt != s.out_dt) out = fresh(Type{out.shape, s.out_dt, false});
+    out.zero = false;
+    out.producer = (int)plan.steps.size();
+    s.out = {out};
+    char buf[512];
+    snprintf(buf, sizeof(buf), "%s -> _mlir_ciface_nova_hip_gemm(%s, %s%s%s) -> %s epilogue=%s",
+             fused.c_str(), view_str(a).c_str(), view_str(b).c_str(), bias ? ", bias " : "",
+             bias ? view_str(*bias).c_str() : "", view_str(out).c_str(),
+             s.epi == NOVA_HIP_EPI_NONE ? "none" : s.epi == NOVA_HIP_EPI_BIAS ? "bias"
+             : s.epi == NOVA_HIP_EPI_BIAS_GELU ? "bias+gelu" : "gelu");
+    s.text = buf;
+    plan.steps.push_back(s);
+    env[op.results[0]] = out;
+    env[name] = out;
+    return NOVA_HIP_SUCCESS;
+  }
+
+  int32_t run() {
+    for (size_t i = 0; i < f.arg_names.size(); ++i) {
+      View v;
+      v.buf = new_buf(f.arg_types[i], (int)i);
+      v.shape = f.arg_types[i].shape;
+      v.strides = dense_strides(v.shape);
+      v.dt = v.logical = f.arg_types[i].dt;
+      env[f.arg_names[i]] = v;
+    }
+    for (const Op &op : f.ops)
+      for (const std::string &o : op.operands) uses[o]++;
+    for (const std::string &r : f.rets) uses[r]++;
+    std::set<const Op *> folded;
+    int32_t rc;
+    for (size_t k = 0; k < f.ops.size(); ++k) {
+      const Op &op = f.ops[k];
+      if (folded.count(&op)) continue;
+      const std::string &n = op.name;
+      if (n == "arith.constant") {
+        consts[op.results[0]] = op.literal;
+      } else if (n == "tensor.empty") {
+        env[op.results[0]] = fresh(op.result_types[0]);
+      } else if (n == "bufferization.to_tensor") {
+        View v;
+        if ((rc = get(op, 0, v))) return rc;
+        env[op.results[0]] = v;
+      } else if (n == "linalg.fill") {
+        View dst;
+        if ((rc = get(op, 1, dst))) return rc;
+        const std::string c = consts.count(op.operands[0]) ? consts[op.operands[0]] : "";
+        if (c.empty() || strtod(c.c_str(), nullptr) != 0.0)
+          return fail(NOVA_HIP_EINVAL, "line %d: linalg.fill with a value other than 0 is not on this path",
+                      op.line);
+        dst.zero = true;
+        env[op.results[0]] = dst;
+        // The fill only matters if its result is read by something other
+        // than a matmul's outs (which the GEMM overwrites).
+        bool only_outs = true;
+        for (size_t j = k + 1; j < f.ops.size(); ++j)
+          for (size_t o = 0; o < f.ops[j].operands.size(); ++o)
+            if (f.ops[j].operands[o] == op.results[0] &&
+                !((f.ops[j].name == "linalg.matmul" || f.ops[j].name == "linalg.batch_matmul") &&
+                  o == 2))
+              only_outs = false;
+        for (const std::string &r : f.rets) only_outs = only_outs && r != op.results[0];
+        if (!only_outs) {
+          Step s;
+          s.kind = "zero";
+          s.out = {dst};
+          s.text = "linalg.fill 0 -> hipMemsetAsync(" + view_str(dst) + ")";
+          plan.steps.push_back(s);
+        }
+      } else if (n == "linalg.matmul" || n == "linalg.batch_matmul") {
+        View a, b, c;
+        if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = get(op, 2, c))) return rc;
+        if (!c.zero)
+          return fail(NOVA_HIP_EINVAL,
+                      "line %d: %s accumulating into a non-zero tensor is not on this path", op.line,
+                      n.c_str());
+        if (op.result_types[0].dt != DT_F32 && a.dt != op.result_types[0].dt)
+          return fail(NOVA_HIP_EDTYPE, "line %d: %s with %s outs is not on this path", op.line,
+                      n.c_str(), dt_name(op.result_types[0].dt));
+        if ((rc = emit_gemm(op, k, a, b, nullptr, c, folded))) return rc;
+      } else if (n == "nova.matmul") {
+        View a, b;
+        if ((rc = get(op, 0, a)) || (rc = get(op, 1, b))) return rc;
+        View out;
+        out.shape = op.result_types[0].shape;
+        out.dt = op.result_types[0].dt;
+        if ((rc = emit_gemm(op, k, a, b, nullptr, out, folded))) return rc;
+      } else if (n == "nova.linear") {
+        View x, w, bias;
+        if ((rc = get(op, 0, x)) || (rc = get(op, 1, w)) || (rc = get(op, 2, bias))) return rc;
+        View out;
+        out.shape = op.result_types[0].shape;
+        out.dt = op.result_types[0].dt;
+        if ((rc = emit_gemm(op, k, x, w, &bias, out, folded))) return rc;
+      } else if (n == "nova.gelu") {
+        return fail(NOVA_HIP_EINVAL,
+                    "line %d: nova.gelu outside a GEMM epilogue is not on this path (it folds only "
+                    "into the nova.linear / matmul it follows)",
+                    op.line);
+      } else if (n == "nova.transpose") {
+        View v;
+        if ((rc = get(op, 0, v))) return rc;
+        const int a1 = atoi(op.attrs.at("axes1").c_str()), a2 = atoi(op.attrs.at("axes2").c_str());
+        std::swap(v.shape[a1], v.shape[a2]);
+        std::swap(v.strides[a1], v.strides[a2]);
+        v.producer = -1;
+        env[op.results[0]] = v;
+        plan.steps.push_back(Step{"view", {}, {}, 0, 0,
+                                  "nova.transpose -> view " + view_str(v)});
+      } else if (n == "nova.cast") {
+        View v;
+        if ((rc = get(op, 0, v))) return rc;
+        const int to = op.result_types[0].dt;
+        if (to == v.logical) {
+          env[op.results[0]] = v;
+        } else if (to == DT_F32 && (v.logical == DT_BF16 || v.logical == DT_F16)) {
+          v.logical = DT_F32;  // exact widening: consumers read the stored narrow data
+          env[op.results[0]] = v;
+          plan.steps.push_back(Step{"view", {}, {}, 0, 0,
+                                    std::string("nova.cast ") + dt_name(v.dt) +
+                                        " -> f32 folded: consumers read " + view_str(v)});
+        } else {
+          return fail(NOVA_HIP_EINVAL,
+                      "line %d: nova.cast %s -> %s is not foldable here (narrowing casts fold "
+                      "only into the GEMM whose sole use they are)",
+                      op.line, dt_name(v.logical), dt_name(to));
+        }
+      } else if (n == "nova.layer_norm") {
+        View x, g, b;
+        if ((rc = get(op, 0, x)) || (rc = get(op, 1, g)) || (rc = get(op, 2, b))) return rc;
+        if ((rc = need_f32(op, x, "input")) || (rc = need_f32(op, g, "gamma")) ||
+            (rc = need_f32(op, b, "beta")))
+          return rc;
+        Step s;
+        s.kind = "layer_norm";
+        s.in = {x, g, b};
+        s.out = {fresh(op.result_types[0]), fresh(op.result_types[1]), fresh(op.result_types[2])};
+        s.text = "nova.layer_norm -> _mlir_ciface_nova_hip_layer_norm_f32(" + view_str(x) +
+                 ") -> " + view_str(s.out[0]) + ", " + view_str(s.out[1]) + ", " +
+                 view_str(s.out[2]);
+        for (int r = 0; r < 3 && r < (int)op.results.size(); ++r) env[op.results[r]] = s.out[r];
+        plan.steps.push_back(s);
+      } else if (n == "nova.sce") {
+        View x, t;
+        if ((rc = get(op, 0, x)) || (rc = get(op, 1, t))) return rc;
+        if ((rc = need_f32(op, x, "logits"))) return rc;
+        if (t.dt != DT_I32) return fail(NOVA_HIP_EDTYPE, "line %d: nova.sce targets must be i32", op.line);
+        Step s;
+        s.kind = "sce";
+        s.in = {x, t};
+        const bool want_sm = !op.results[0].empty() && uses[op.results[0]] > 0;
+        View sm;
+        if (want_sm) sm = fresh(op.result_types[0]);
+        s.out = {sm, fresh(op.result_types[1])};
+        s.text = "nova.sce -> _mlir_ciface_nova_hip_sce_f32(" + view_str(x) + ", " + view_str(t) +
+                 ") -> " + (want_sm ? view_str(sm) : std::string("(softmax unused)")) + ", " +
+                 view_str(s.out[1]);
+        if (want_sm) env[op.results[0]] = sm;
+        env[op.results[1]] = s.out[1];
+        plan.steps.push_back(s);
+      } else if (n == "nova.sce_backward") {
+        View sm, t;
+        if ((rc = get(op, 0, sm)) || (rc = get(op, 1, t))) return rc;
+        if ((rc = need_f32(op, sm, "softmax"))) return rc;
+        if (t.dt != DT_I32)
+          return fail(NOVA_HIP_EDTYPE, "line %d: nova.sce_backward targets must be i32", op.line);
+        if (op.attrs.count("dim")) {
+          const int d = atoi(op.attrs.at("dim").c_str());
+          if (d != -1 && d != (int)sm.shape.size() - 1)
+            return fail(NOVA_HIP_EINVAL, "line %d: nova.sce_backward over dim %d (class dim last only)",
+                        op.line, d);
+        }
+        Step s;
+        s.kind = "sce_bwd";
+        s.in = {sm, t};
+        s.out = {fresh(op.result_types[0])};
+        s.text = "nova.sce_backward -> _mlir_ciface_nova_hip_sce_backward_f32(" + view_str(sm) +
+                 ") -> " + view_str(s.out[0]);
+        env[op.results[0]] = s.out[0];
+        plan.steps.push_back(s);
+      } else if (n == "nova.layer_norm_backward") {
+        View gy, x, g, S, r;
+        if ((rc = get(op, 0, gy)) || (rc = get(op, 1, x)) || (rc = get(op, 2, g)) ||
+            (rc = get(op, 3, S)) || (rc = get(op, 4, r)))
+          return rc;
+        for (const View *v : {&gy, &x, &g, &S, &r})
+          if ((rc = need_f32(op, *v, "operand"))) return rc;
+        Step s;
+        s.kind = "ln_bwd";
+        s.in = {gy, x, g, S, r};
+        s.out = {fresh(op.result_types[0]), fresh(op.result_types[1]), fresh(op.result_types[2])};
+        s.text = "nova.layer_norm_backward -> _mlir_ciface_nova_hip_layer_norm_backward_f32(" +
+                 view_str(gy) + ", " + view_str(x) + ") -> " + view_str(s.out[0]) + ", " +
+                 view_str(s.out[1]) + ", " + view_str(s.out[2]);
+        for (int i = 0; i < 3 && i < (int)op.results.size(); ++i) env[op.results[i]] = s.out[i];
+        plan.steps.push_back(s);
+      } else if (n == "nova.linear_backward" || n == "nova.matmul_backward") {
+        View go, x, w;
+        if ((rc = get(op, 0, go)) || (rc = get(op, 1, x)) || (rc = get(op, 2, w))) return rc;
+        if (go.dt != x.dt || x.dt != w.dt)
+          return fail(NOVA_HIP_EDTYPE, "line %d: %s operands must share a stored dtype", op.line,
+                      n.c_str());
+        const bool lin = n == "nova.linear_backward";
+        Step s;
+        s.kind = lin ? "lin_bwd" : "mm_bwd";
+        s.in = {go, x, w};
+        for (size_t r = 0; r < op.result_types.size(); ++r) s.out.push_back(fresh(op.result_types[r]));
+        s.out_dt = op.result_types[0].dt;
+        s.text = n + " -> _mlir_ciface_nova_hip_" + (lin ? "linear" : "matmul") + "_backward(" +
+                 view_str(go) + ", " + view_str(x) + ", " + view_str(w) + ") -> ";
+        for (size_t r = 0; r < s.out.size(); ++r) s.text += (r ? ", " : "") + view_str(s.out[r]);
+        for (size_t r = 0; r < op.results.size() && r < s.out.size(); ++r) env[op.results[r]] = s.out[r];
+        plan.steps.push_back(s);
+      } else if (n == "bufferization.materialize_in_destination") {
+        View src, dst;
+        if ((rc = get(op, 0, src)) || (rc = get(op, 1, dst))) return rc;
+        if (src.shape != dst.shape || !is_dense(src) || src.dt != dst.dt)
+          return fail(NOVA_HIP_ESHAPE, "line %d: materialize_in_destination of a %s value into %s",
+                      op.line, view_str(src).c_str(), view_str(dst).c_str());
+        Step s;
+        s.kind = "copy";
+        s.in = {src};
+        s.out = {dst};
+        s.text = "materialize_in_destination -> hipMemcpyAsync(" + view_str(dst) + " <- " +
+                 view_str(src) + ")";
+        plan.steps.push_back(s);
+        plan.out_args.push_back(plan.bufs[dst.buf].arg);
+      } else {
+        return fail(NOVA_HIP_EINVAL, "line %d: op '%s' is not part of this path's op surface",
+                    op.line, n.c_str());
+      }
+    }
+    for (const std::string &r : f.rets) {
+      auto it = env.find(r);
+      if (it == env.end()) return fail(NOVA_HIP_EINVAL, "return of undefined value %s", r.c_str());
+      if (!is_dense(it->second) || it->second.dt != it->second.logical)
+        return fail(NOVA_HIP_EINVAL,
+                    "returned value %s is a view (transpose / folded cast) that is never "
+                    "materialised on this path",
+                    r.c_str());
+      plan.results.push_back(it->second);
+    }
+    return NOVA_HIP_SUCCESS;
+  }
+};
+
+// ---- execution -----------------------------------------------------------------
+template <int R>
+struct Desc {
+  void *allocated, *aligned;
+  int64_t offset, sizes[R], strides[R];
+};
+
+template <int R>
+Desc<R> desc(const View &v, const std::vector<void *> &ptr) {
+  Desc<R> d;
+  d.allocated = d.aligned = ptr[v.buf];
+  d.offset = 0;
+  const int n = (int)v.shape.size();
+  for (int i = 0; i < R; ++i) {
+    const int j = n - R + i;
+    d.sizes[i] = j >= 0 ? v.shape[j] : 1;
+    d.strides[i] = j >= 0 ? v.strides[j] : 0;
+  }
+  // leading dims folded into the first kept one (dense leading dims only)
+  for (int j = 0; j < n - R; ++j) d.sizes[0] *= v.shape[j];
+  return d;
+}
+
+int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) {
+  if (s.kind == "view") return NOVA_HIP_SUCCESS;
+  if (s.kind == "zero") {
+    int64_t n = 1;
+    for (int64_t d : s.out[0].shape) n *= d;
+    return hipMemsetAsync(ptr[s.out[0].buf], 0, n * dt_size(s.out[0].dt), st) == hipSuccess
+               ? NOVA_HIP_SUCCESS
+               : fail(NOVA_HIP_EDEVICE, "memset failed");
+  }
+  if (s.kind == "copy") {
+    int64_t n = 1;
+    for (int64_t d : s.in[0].shape) n *= d;
+    return hipMemcpyAsync(ptr[s.out[0].buf], ptr[s.in[0].buf], n * dt_size(s.in[0].dt),
+                          hipMemcpyDeviceToDevice, st) == hipSuccess
+               ? NOVA_HIP_SUCCESS
+               : fail(NOVA_HIP_EDEVICE, "device copy failed");
+  }
+  if (s.kind == "gemm") {
+    const View &a = s.in[0], &b = s.in[1], &c = s.out[0];
+    Desc<3> A = desc<3>(a, ptr), B = desc<3>(b, ptr), C = desc<3>(c, ptr);
+    // rank-2 operands of a batched product broadcast over the batch
+    if (a.shape.size() == 2) A.strides[0] = 0;
+    if (b.shape.size() == 2) B.strides[0] = 0;
+    if (a.shape.size() == 2 && c.shape.size() == 3) A.sizes[0] = 1;
+    if (b.shape.size() == 2 && c.shape.size() == 3) B.sizes[0] = 1;
+    Desc<1> bias;
+    const Desc<1> *pb = nullptr;
+    int bias_dt = 0;
+    if (s.in.size() > 2) {
+      bias = desc<1>(s.in[2], ptr);
+      pb = &bias;
+      bias_dt = s.in[2].dt;
+    }
+    if (a.dt != b.dt) return fail(NOVA_HIP_EDTYPE, "GEMM operands stored as %s and %s", dt_name(a.dt), dt_name(b.dt));
+    return _mlir_ciface_nova_hip_gemm(reinterpret_cast<const NovaMemRef3D *>(&A),
+                                      reinterpret_cast<const NovaMemRef3D *>(&B),
+                                      reinterpret_cast<NovaMemRef3D *>(&C),
+                                      reinterpret_cast<const NovaMemRef1D *>(pb),
+                                      NOVA_HIP_GEMM_FLAGS(a.dt, s.out_dt, s.epi, bias_dt));
+  }
+  if (s.kind == "layer_norm") {
+    Desc<2> x = desc<2>(s.in[0], ptr), y = desc<2>(s.out[0], ptr);
+    Desc<1> g = desc<1>(s.in[1], ptr), b = desc<1>(s.in[2], ptr);
+    Desc<1> S = desc<1>(s.out[1], ptr), r = desc<1>(s.out[2], ptr);
+    return _mlir_ciface_nova_hip_layer_norm_f32(
+        reinterpret_cast<const NovaMemRef2D *>(&x), reinterpret_cast<const NovaMemRef1D *>(&g),
+        reinterpret_cast<const NovaMemRef1D *>(&b), reinterpret_cast<NovaMemRef2D *>(&y),
+        reinterpret_cast<NovaMemRef1D *>(&S), reinterpret_cast<NovaMemRef1D *>(&r), 1e-5f);
+  }
+  if (s.kind == "sce") {
+    Desc<2> x = desc<2>(s.in[0], ptr);
+    Desc<1> t = desc<1>(s.in[1], ptr), loss = desc<1>(s.out[1], ptr);
+    Desc<2> sm;
+    const bool has_sm = s.out[0].buf >= 0;
+    if (has_sm) sm = desc<2>(s.out[0], ptr);
+    return _mlir_ciface_nova_hip_sce_f32(reinterpret_cast<const NovaMemRef2D *>(&x),
+                                         reinterpret_cast<const NovaMemRef1D *>(&t),
+                                         reinterpret_cast<NovaMemRef1D *>(&loss),
+                                         has_sm ? reinterpret_cast<NovaMemRef2D *>(&sm) : nullptr);
+  }
+  if (s.kind == "sce_bwd") {
+    Desc<2> sm = desc<2>(s.in[0], ptr), g = desc<2>(s.out[0], ptr);
+    Desc<1> t = desc<1>(s.in[1], ptr);
+    return _mlir_ciface_nova_hip_sce_backward_f32(reinterpret_cast<const NovaMemRef2D *>(&sm),
+                                                  reinterpret_cast<const NovaMemRef1D *>(&t),
+                                                  reinterpret_cast<NovaMemRef2D *>(&g));
+  }
+  if (s.kind == "ln_bwd") {
+    Desc<2> gy = desc<2>(s.in[0], ptr), x = desc<2>(s.in[1], ptr), dx = desc<2>(s.out[0], ptr);
+    Desc<1> g = desc<1>(s.in[2], ptr), dg = desc<1>(s.out[1], ptr), db = desc<1>(s.out[2], ptr);
+    // stats may carry a trailing unit dim ([R, 1]): fold to [R]
+    View S = s.in[3], r = s.in[4];
+    if (S.shape.size() >= 2 && S.shape.back() == 1) { S.shape.pop_back(); S.strides.pop_back(); }
+    if (r.shape.size() >= 2 && r.shape.back() == 1) { r.shape.pop_back(); r.strides.pop_back(); }
+    Desc<1> dS = desc<1>(S, ptr), dr = desc<1>(r, ptr);
+    dS.strides[0] = dr.strides[0] = 1;
+    return _mlir_ciface_nova_hip_layer_norm_backward_f32(
+        reinterpret_cast<const NovaMemRef2D *>(&gy), reinterpret_cast<const NovaMemRef2D *>(&x),
+        reinterpret_cast<const NovaMemRef1D *>(&g), reinterpret_cast<const NovaMemRef1D *>(&dS),
+        reinterpret_cast<const NovaMemRef1D *>(&dr), reinterpret_cast<NovaMemRef2D *>(&dx),
+        reinterpret_cast<NovaMemRef1D *>(&dg), reinterpret_cast<NovaMemRef1D *>(&db));
+  }
+  if (s.kind == "lin_bwd" || s.kind == "mm_bwd") {
+    Desc<2> go = desc<2>(s.in[0], ptr), x = desc<2>(s.in[1], ptr), w = desc<2>(s.in[2], ptr);
+    Desc<2> o0 = desc<2>(s.out[0], ptr), o1 = desc<2>(s.out[1], ptr);
+    const int32_t flags = NOVA_HIP_GEMM_FLAGS(s.in[1].dt, s.out_dt, 0, 0);
+    if (s.kind == "mm_bwd")
+      return _mlir_ciface_nova_hip_matmul_backward(
+          reinterpret_cast<const NovaMemRef2D *>(&go), reinterpret_cast<const NovaMemRef2D *>(&x),
+          reinterpret_cast<const NovaMemRef2D *>(&w), reinterpret_cast<NovaMemRef2D *>(&o0),
+          reinterpret_cast<NovaMemRef2D *>(&o1), flags);
+    Desc<1> o2 = desc<1>(s.out[2], ptr);
+    return _mlir_ciface_nova_hip_linear_backward(
+        reinterpret_cast<const NovaMemRef2D *>(&go), reinterpret_cast<const NovaMemRef2D *>(&x),
+        reinterpret_cast<const NovaMemRef2D *>(&w), reinterpret_cast<NovaMemRef2D *>(&o0),
+        reinterpret_cast<NovaMemRef2D *>(&o1), reinterpret_cast<NovaMemRef1D *>(&o2), flags);
+  }
+  return fail(NOVA_HIP_EINVAL, "internal: unknown step %s", s.kind.c_str());
+}
+
+}  // namespace
+
+struct NovaRunProgram {
+  std::vector<Func> funcs;
+  const Func *find(const char *name) const {
+    for (const Func &f : funcs)
+      if (name && f.name == name) return &f;
+    return funcs.size() == 1 && !name ? &funcs[0] : nullptr;
+  }
+};
+
+namespace {
+int32_t plan_of(const NovaRunProgram *p, const char *func, Plan &out, const Func **fo) {
+  t_err[0] = 0;
+  if (!p) return fail(NOVA_HIP_EINVAL, "null program");
+  const Func *f = p->find(func);
+  if (!f) return fail(NOVA_HIP_EINVAL, "no function @%s", func ? func : "(null)");
+  Planner pl(*f);
+  int32_t rc = pl.run();
+  if (rc) return rc;
+  out = pl.plan;
+  if (fo) *fo = f;
+  return NOVA_HIP_SUCCESS;
+}
+
+void fill_info(const Type &t, int32_t *dtype, int32_t *rank, int64_t *shape) {
+  if (dtype) *dtype = t.dt;
+  if (rank) *rank = (int32_t)t.shape.size();
+  if (shape)
+    for (size_t i = 0; i < t.shape.size() && i < 8; ++i) shape[i] = t.shape[i];
+}
+}  // namespace
+
+extern "C" {
+
+NovaRunProgram *nova_run_parse(const char *text_in) {
+  t_err[0] = 0;
+  if (!text_in) {
+    fail(NOVA_HIP_EINVAL, "null text");
+    return nullptr;
+  }
+  const std::string text = strip_comments(text_in);
+  std::unique_ptr<NovaRunProgram> p(new NovaRunProgram);
+  size_t at = 0;
+  while ((at = text.find("func.func", at)) != std::string::npos) {
+    Func f;
+    size_t end = 0;
+    if (parse_func(text, at, end, f)) return nullptr;
+    for (const Type &t : f.arg_types)
+      if (t.dt < 0) {
+        fail(NOVA_HIP_EINVAL, "@%s: unsupported argument type", f.name.c_str());
+        return nullptr;
+      }
+    p->funcs.push_back(f);
+    at = end;
+  }
+  if (p->funcs.empty()) {
+    fail(NOVA_HIP_EINVAL, "no func.func in the module");
+    return nullptr;
+  }
+  // result types: from the values returned
+  for (Func &f : p->funcs) {
+    Planner pl(f);
+    if (pl.run()) continue;  // reported again by plan / execute
+    for (const View &v : pl.plan.results) f.ret_types.push_back(Type{v.shape, v.dt, false});
+  }
+  return p.release();
+}
+
+void nova_run_free(NovaRunProgram *p) { delete p; }
+
+const char *nova_run_last_error(void) { return t_err; }
+
+int32_t nova_run_num_funcs(const NovaRunProgram *p) { return p ? (int32_t)p->funcs.size() : 0; }
+
+const char *nova_run_func_name(const NovaRunProgram *p, int32_t i) {
+  return p && i >= 0 && i < (int32_t)p->funcs.size() ? p->funcs[i].name.c_str() : nullptr;
+}
+
+int32_t nova_run_num_args(const NovaRunProgram *p, const char *func) {
+  const Func *f = p ? p->find(func) : nullptr;
+  return f ? (int32_t)f->arg_types.size() : -1;
+}
+
+int32_t nova_run_num_results(const NovaRunProgram *p, const char *func) {
+  Plan pl;
+  if (plan_of(p, func, pl, nullptr)) return -1;
+  return (int32_t)pl.results.size();
+}
+
+int32_t nova_run_arg_info(const NovaRunProgram *p, const char *func, int32_t i, int32_t *dtype,
+                          int32_t *rank, int64_t *shape) {
+  const Func *f = p ? p->find(func) : nullptr;
+  if (!f || i < 0 || i >= (int32_t)f->arg_types.size()) return fail(NOVA_HIP_EINVAL, "no argument %d", i);
+  fill_info(f->arg_types[i], dtype, rank, shape);
+  return NOVA_HIP_SUCCESS;
+}
+
+int32_t nova_run_result_info(const NovaRunProgram *p, const char *func, int32_t i,
+                             int32_t *dtype, int32_t *rank, int64_t *shape) {
+  Plan pl;
+  int32_t rc = plan_of(p, func, pl, nullptr);
+  if (rc) return rc;
+  if (i < 0 || i >= (int32_t)pl.results.size()) return fail(NOVA_HIP_EINVAL, "no result %d", i);
+  const View &v = pl.results[i];
+  fill_info(Type{v.shape, v.dt, false}, dtype, rank, shape);
+  return NOVA_HIP_SUCCESS;
+}
+
+int32_t nova_run_plan(const NovaRunProgram *p, const char *func, char *buf, size_t len) {
+  Plan pl;
+  const Func *f = nullptr;
+  int32_t rc = plan_of(p, func, pl, &f);
+  if (rc) return rc;
+  std::string s = "func @" + f->name + ":\n";
+  for (const Step &st : pl.steps) s += "  " + st.text + "\n";
+  s += "  return";
+  for (size_t i = 0; i < pl.results.size(); ++i) s += (i ? ", " : " ") + view_str(pl.results[i]);
+  s += "\n";
+  if (buf && len) {
+    strncpy(buf, s.c_str(), len - 1);
+    buf[len - 1] = 0;
+  }
+  return NOVA_HIP_SUCCESS;
+}
+
+int32_t nova_run_execute(const NovaRunProgram *p, const char *func, const void *const *host_args,
+                         void *const *host_results) {
+  Plan pl;
+  const Func *f = nullptr;
+  int32_t rc = plan_of(p, func, pl, &f);
+  if (rc) return rc;
+  if ((!host_args && !f->arg_types.empty()) || (!host_results && !pl.results.empty()))
+    return fail(NOVA_HIP_EINVAL, "null argument or result array");
+  hipStream_t st = static_cast<hipStream_t>(nova_hip_get_stream());
+  std::vector<void *> ptr(pl.bufs.size(), nullptr);
+  // Only buffers a step or a result touches get device memory.
+  std::vector<bool> used(pl.bufs.size(), false);
+  for (const Step &s : pl.steps) {
+    for (const View &v : s.in) if (v.buf >= 0) used[v.buf] = true;
+    for (const View &v : s.out) if (v.buf >= 0) used[v.buf] = true;
+  }
+  for (const View &v : pl.results) used[v.buf] = true;
+  auto cleanup = [&]() {
+    for (void *q : ptr)
+      if (q) (void)hipFree(q);
+  };
+  for (size_t b = 0; b < pl.bufs.size(); ++b) {
+    if (pl.bufs[b].bytes == 0 || !used[b]) continue;
+    if (hipMalloc(&ptr[b], (size_t)pl.bufs[b].bytes) != hipSuccess) {
+      cleanup();
+      return fail(NOVA_HIP_ENOMEM, "hipMalloc of %lld bytes failed", (long long)pl.bufs[b].bytes);
+    }
+    if (pl.bufs[b].arg >= 0 &&
+        hipMemcpyAsync(ptr[b], host_args[pl.bufs[b].arg], (size_t)pl.bufs[b].bytes,
+                       hipMemcpyHostToDevice, st) != hipSuccess) {
+      cleanup();
+      return fail(NOVA_HIP_EDEVICE, "copy of argument %d failed", pl.bufs[b].arg);
+    }
+  }
+  for (const Step &s : pl.steps) {
+    if ((rc = run_step(s, ptr, st))) {
+      const std::string why = nova_hip_last_error();
+      (void)hipStreamSynchronize(st);
+      cleanup();
+      if (why.size()) fail(rc, "%s: %s", s.text.c_str(), why.c_str());
+      return rc;
+    }
+  }
+  for (size_t i = 0; i < pl.results.size(); ++i) {
+    const View &v = pl.results[i];
+    if (hipMemcpyAsync(host_results[i], ptr[v.buf], (size_t)pl.bufs[v.buf].bytes,
+                       hipMemcpyDeviceToHost, st) != hipSuccess) {
+      cleanup();
+      return fail(NOVA_HIP_EDEVICE, "copy of result %zu failed", i);
+    }
+  }
+  for (int a : pl.out_args) {  // writable memref arguments hold outputs
+    for (size_t b = 0; b < pl.bufs.size(); ++b)
+      if (pl.bufs[b].arg == a &&
+          hipMemcpyAsync(const_cast<void *>(host_args[a]), ptr[b], (size_t)pl.bufs[b].bytes,
+                         hipMemcpyDeviceToHost, st) != hipSuccess) {
+        cleanup();
+        return fail(NOVA_HIP_EDEVICE, "copy back of argument %d failed", a);
+      }
+  }
+  const hipError_t e = hipStreamSynchronize(st);
+  cleanup();
+  return e == hipSuccess ? NOVA_HIP_SUCCESS : fail(NOVA_HIP_EDEVICE, "%s", hipGetErrorString(e));
+}
+
+}  // extern "C"

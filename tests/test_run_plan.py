@@ -1,0 +1,110 @@
+"""The MLIR-free planner (libnova_run) on CPU: programs written in the op
+surface parse, get the launch plan the lowering would emit (folds of
+widening casts and transposes into GEMM operands, of GELU and narrowing
+casts into the epilogue, zero fills elided), infer the reference's result
+types, and ops outside this path are refused by name."""
+import os
+
+import pytest
+
+import nova_run
+from conftest import GOLDEN
+
+MLIR = os.path.join(GOLDEN, "mlir")
+
+
+def prog(name):
+    with open(os.path.join(MLIR, name)) as f:
+        return nova_run.Program(f.read())
+
+
+def test_linear_gelu_folds_into_one_gemm():
+    p = prog("linear_gelu_bf16.mlir")
+    plan = p.plan("linear_gelu")
+    launches = [l for l in plan.splitlines() if "_mlir_ciface_" in l]
+    assert len(launches) == 1
+    assert "nova.linear + nova.gelu + nova.cast -> _mlir_ciface_nova_hip_gemm" in launches[0]
+    assert "epilogue=bias+gelu" in launches[0]
+    assert "strides(1,160)" in launches[0]          # the transposed weight is a view
+    assert "bf16" in launches[0].split("->")[-1]    # bf16 output
+    assert p.args("linear_gelu") == [(1, (96, 160)), (1, (200, 160)), (1, (200,))]
+    assert p.results("linear_gelu") == [(1, (96, 200))]
+
+
+def test_batch_matmul_forms():
+    p = prog("batch_matmul_bf16.mlir")
+    for f in ("bmm", "bmm_nova"):
+        plan = p.plan(f)
+        assert plan.count("_mlir_ciface_nova_hip_gemm") == 1
+        assert "hipMemsetAsync" not in plan         # the zero fill only feeds the GEMM's outs
+        assert p.results(f) == [(0, (4, 128, 160))]
+
+
+def test_reductions_and_backward_plans():
+    p = prog("reductions.mlir")
+    assert p.results("ln") == [(0, (64, 1024)), (0, (64,)), (0, (64,))]
+    assert "_mlir_ciface_nova_hip_layer_norm_backward_f32" in p.plan("ln_train")
+    plan = p.plan("sce_train")
+    assert "_mlir_ciface_nova_hip_sce_f32" in plan and "_mlir_ciface_nova_hip_sce_backward_f32" in plan
+    assert p.results("sce_train") == [(0, (1,)), (0, (32, 5000))]
+    b = prog("backward.mlir")
+    assert b.results("lin_bwd") == [(0, (40, 36)), (0, (36, 24)), (0, (24,))]
+    assert b.results("mm_bwd") == [(1, (64, 128)), (1, (128, 96))]
+
+
+def test_memref_entry_writes_output_argument():
+    p = prog("memref_main.mlir")
+    plan = p.plan("main")
+    assert "materialize_in_destination" in plan
+    assert p.results("main") == []
+    assert len(p.args("main")) == 4
+
+
+def test_nova_matmul_bf16_infers_f16_result():
+    """NovaOps.cpp:1198: bf16 x bf16 nova.matmul gives f16."""
+    p = nova_run.Program("""func.func @m(%a: tensor<8x16xbf16>, %b: tensor<16x4xbf16>) -> tensor<8x4xf16> {
+      %r = nova.matmul %a, %b : tensor<8x16xbf16>, tensor<16x4xbf16>
+      return %r : tensor<8x4xf16>
+    }""")
+    assert p.results("m") == [(2, (8, 4))]
+
+
+def test_ops_outside_the_path_are_refused():
+    with pytest.raises(nova_run.NovaRunError, match="nova.relu"):
+        prog("not_on_path.mlir")
+    p = nova_run.Program("""func.func @g(%x: tensor<4x8xf32>) -> tensor<4x8xf32> {
+      %g = nova.gelu %x : tensor<4x8xf32>
+      return %g : tensor<4x8xf32>
+    }""")
+    with pytest.raises(nova_run.NovaRunError, match="outside a GEMM epilogue"):
+        p.plan("g")
+    p = nova_run.Program("""func.func @c(%x: tensor<4x8xf32>) -> tensor<4x8xbf16> {
+      %c = nova.cast %x : tensor<4x8xf32> -> tensor<4x8xbf16>
+      return %c : tensor<4x8xbf16>
+    }""")
+    with pytest.raises(nova_run.NovaRunError, match="not foldable"):
+        p.plan("c")
+    with pytest.raises(nova_run.NovaRunError, match="no function"):
+        p.plan("missing")
+
+
+def test_bad_syntax_and_types_are_reported_with_lines():
+    with pytest.raises(nova_run.NovaRunError, match="line 2"):
+        nova_run.Program("""func.func @f(%x: tensor<4x8xf32>) -> tensor<4x8xf32> {
+          %r = nova.linear %x, %x : tensor<4x8xf32>
+          return %r : tensor<4x8xf32>
+        }""")
+    with pytest.raises(nova_run.NovaRunError, match="unsupported"):
+        nova_run.Program("func.func @f(%x: tensor<?x8xf32>) { return }")
+
+
+def test_library_exports_every_declared_symbol():
+    import re
+    from conftest import REPO
+    text = open(os.path.join(REPO, "include", "nova_run.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = sorted(set(re.findall(r"\b(nova_run_\w+)\s*\(", text)))
+    assert len(names) >= 10
+    L = nova_run.lib()
+    for n in names:
+        assert hasattr(L, n), n
