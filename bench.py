@@ -435,7 +435,7 @@ def main():
                 "A,B uniform[-1,1] seed 1",
         "config": {"workload": "c2: linalg.batch_matmul bf16 x bf16 -> f32 accumulate/output, "
                                "batch=8, M=N=K=4096",
-                   "kernel": "gemm_dma_kernel: 256x256x64 tiles, 2-stage LDS-DMA ring, v_mfma_f32_32x32x16_bf16",
+                   "kernel": "gemm_pers_kernel: persistent, one workgroup per CU, 256x256x64 tiles, 2-stage LDS-DMA ring, v_mfma_f32_32x32x16_bf16",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": head["frac_mfma"], "traffic": traffic},

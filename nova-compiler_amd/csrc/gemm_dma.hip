@@ -1,7 +1,8 @@
-// Host side of the LDS-DMA GEMM (kernel in gemm_dma.h): which problems it
-// takes, the round size of its tile order, and dispatch to the per-output-
-// dtype translation units gemm_dma_out_{f32,bf16,f16}.hip, each of which
-// instantiates the kernel for its output dtype (compiled in parallel).
+// Host side of the LDS-DMA GEMM (kernels in gemm_dma.h and gemm_pers.h):
+// which problems it takes, the round size of its tile order, and dispatch
+// to the per-output-dtype translation units gemm_dma_out_{f32,bf16,f16}.hip,
+// each of which instantiates the kernels for its output dtype (compiled in
+// parallel).
 #include "gemm_common.h"
 
 namespace nova_hip {
@@ -25,8 +26,9 @@ int32_t launch_gemm_dma(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool bk
   gemm::GemmArgs a = a_in;
   a.tiles_m = a.M / kBM;
   a.tiles_n = a.N / kBN;
-  // The kernel's 128 KB of LDS allows one workgroup per CU: a round is one
-  // workgroup per CU of the current device (8 XCDs, so a multiple of 8).
+  // The kernels' 128 KB (160 KB persistent) of LDS allow one workgroup per
+  // CU: a round is one workgroup per CU of the current device (8 XCDs, so a
+  // multiple of 8); the persistent kernel launches one round.
   const int cus = device_cu_count();
   a.round = (cus > 0 && cus % 8 == 0) ? cus : 0;
   if (a.out_dt == NOVA_HIP_DT_F32) return launch_gemm_dma_f32out(a, in_dt, akc, bkc, s);

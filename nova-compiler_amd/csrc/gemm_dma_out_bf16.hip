@@ -1,11 +1,13 @@
-// Instantiates the LDS-DMA GEMM kernel (gemm_dma.h) for bf16 output: both
+// Instantiates the LDS-DMA GEMM kernels (gemm_dma.h, and its persistent form
+// gemm_pers.h for problems without an epilogue op) for bf16 output: both
 // input dtypes and the four operand layouts.
-#include "gemm_dma.h"
+#include "gemm_pers.h"
 
 namespace nova_hip {
 
 int32_t launch_gemm_dma_bf16out(const gemm::GemmArgs &a, int in_dt, bool akc, bool bkc,
                                hipStream_t s) {
+  if (pers::applicable(a)) return pers::launch_out<NOVA_HIP_DT_BF16>(a, in_dt, akc, bkc, s);
   return dma::launch_out<NOVA_HIP_DT_BF16>(a, in_dt, akc, bkc, s);
 }
 

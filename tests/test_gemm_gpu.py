@@ -80,11 +80,12 @@ def test_gemm_mfma_lane_layout_exact(cuda):
 @pytest.mark.parametrize("dt", [S.BF16, S.F16])
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
 def test_gemm_dma_path_exact(cuda, dt, layout):
-    """Whole 256x256 tiles, K % 128 == 0 and >= 128 tiles select the LDS-DMA
-    kernel (transposing LDS reads for M/N-contiguous operands).  Integer
-    grids make the result exact, so any lane / swizzle slip is caught."""
+    """Whole 256x256 tiles, K % 64 == 0 and 128..255 tiles select the
+    one-tile-per-workgroup LDS-DMA kernel (transposing LDS reads for
+    M/N-contiguous operands).  Integer grids make the result exact, so any
+    lane / swizzle slip is caught."""
     g = np.random.default_rng(19)
-    batch, M, N, K = 32, 512, 256, 384
+    batch, M, N, K = 32, 512, 512, 384
     af = g.integers(-4, 5, (batch, M, K)).astype(np.float32)
     bf = g.integers(-4, 5, (batch, K, N)).astype(np.float32)
     a, b = S.round_to(af, dt), S.round_to(bf, dt)
@@ -93,6 +94,50 @@ def test_gemm_dma_path_exact(cuda, dt, layout):
     B = view_as(b, layout[1], cuda, dt)
     got = nh.gemm(A, B).cpu().numpy()
     assert np.array_equal(got, want), (layout, float(np.abs(got - want).max()))
+
+
+@pytest.mark.parametrize("dt,layout,shape", [
+    (S.BF16, "NN", (17, 1024, 1024, 128)),   # 272 tiles: 16 workgroups take two
+    (S.BF16, "NT", (9, 1536, 1280, 192)),    # 270 tiles, three K steps
+    (S.BF16, "TN", (17, 1024, 1024, 128)),
+    (S.BF16, "TT", (9, 1536, 1280, 192)),
+    (S.F16, "NN", (3, 2816, 2304, 320)),     # 297 tiles, five K steps
+    (S.F16, "TT", (17, 1024, 1024, 128)),
+])
+def test_gemm_persistent_path_exact(cuda, dt, layout, shape):
+    """A full round of 256x256 tiles or more (one workgroup per CU), K % 64
+    == 0, K >= 128 and no epilogue op select the persistent LDS-DMA kernel:
+    each workgroup computes several tiles and prefetches the next tile's
+    first K steps during an epilogue.  A last, partial round leaves some
+    workgroups one tile fewer.  Integer grids make the result exact."""
+    g = np.random.default_rng(23)
+    batch, M, N, K = shape
+    af = g.integers(-4, 5, (batch, M, K)).astype(np.float32)
+    bf = g.integers(-4, 5, (batch, K, N)).astype(np.float32)
+    a, b = S.round_to(af, dt), S.round_to(bf, dt)
+    want = np.matmul(af.astype(np.float64), bf.astype(np.float64)).astype(np.float32)
+    A = view_as(a, layout[0], cuda, dt)
+    B = view_as(b, layout[1], cuda, dt)
+    got = nh.gemm(A, B).cpu().numpy()
+    assert np.array_equal(got, want), (layout, shape, float(np.abs(got - want).max()))
+
+
+@pytest.mark.parametrize("out", ["bf16", "f16"])
+def test_gemm_persistent_path_16bit_out(cuda, out):
+    """The persistent kernel's 16-bit epilogue: integer sums up to 2048 are
+    exact in bf16 only up to 256, so compare against the RNE rounding of the
+    exact f32 result."""
+    import torch
+    g = np.random.default_rng(29)
+    batch, M, N, K = 17, 1024, 1024, 128
+    af = g.integers(-4, 5, (batch, M, K)).astype(np.float32)
+    bf = g.integers(-4, 5, (batch, K, N)).astype(np.float32)
+    a, b = S.round_to(af, S.BF16), S.round_to(bf, S.BF16)
+    exact = np.matmul(af.astype(np.float64), bf.astype(np.float64)).astype(np.float32)
+    odt = torch.bfloat16 if out == "bf16" else torch.float16
+    got = nh.gemm(to_dev(a, S.BF16, cuda), to_dev(b, S.BF16, cuda), out_dtype=odt)
+    want = torch.from_numpy(exact).to(odt)
+    assert torch.equal(got.cpu(), want), out
 
 
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN"])
