@@ -10,6 +10,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "nova_hip_internal.h"
 
 namespace nova_hip {
@@ -181,13 +183,12 @@ __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
   const int per_wg = (a.rows + gridDim.x - 1) / gridDim.x;
   const int row0 = min(a.rows, (int)blockIdx.x * per_wg);
   const int row_end = min(a.rows, row0 + per_wg);
-  int it = 0;
-  for (int rb = row0; rb < row_end; rb += 2, ++it) {
-    const int row = rb + grp;
+  // Loads of row r (zeros past the block's end): gy, x, mean, rstd.
+  auto load_row = [&](int row, f32x4 (&g)[NQ], f32x4 (&xv)[NQ], float &mean, float &rs)
+                      __attribute__((always_inline)) {
     const bool live = row < row_end;
     const f32x4 *gr = reinterpret_cast<const f32x4 *>(a.gy + (int64_t)(live ? row : row0) * a.sgy);
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)(live ? row : row0) * a.sx);
-    f32x4 g[NQ], xv[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int c = q * 64 * NQ + lane + 64 * i;
@@ -195,8 +196,33 @@ __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
       g[i] = ok ? __builtin_nontemporal_load(gr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
       xv[i] = ok ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    const float mean = live ? a.mean_sum[row] * a.invD : 0.0f;
-    const float rs = live ? a.rstd[row] : 0.0f;
+    mean = live ? a.mean_sum[row] * a.invD : 0.0f;
+    rs = live ? a.rstd[row] : 0.0f;
+  };
+  // With NQ <= 4 the row pairs two iterations ahead are loaded while the
+  // current one is reduced and written (three register slots; the loop is
+  // unrolled by three so that slots are compile-time registers).  The
+  // barrier waits for LDS only, not for these loads.
+  constexpr bool kAhead = NQ <= 4;
+  constexpr int kSlots = kAhead ? 3 : 1;
+  f32x4 G[kSlots][NQ], X[kSlots][NQ];
+  float Mn[kSlots], Rs[kSlots];
+  if constexpr (kAhead) {
+    load_row(row0 + grp, G[0], X[0], Mn[0], Rs[0]);
+    load_row(row0 + 2 + grp, G[1], X[1], Mn[1], Rs[1]);
+  }
+  int it = 0;
+  // One row pair: row rb + grp, its data in slot S.
+  auto pair = [&](auto slot, int rb) __attribute__((always_inline)) {
+    constexpr int S = decltype(slot)::value;
+    const int row = rb + grp;
+    const bool live = row < row_end;
+    if constexpr (kAhead) load_row(rb + 4 + grp, G[(S + 2) % 3], X[(S + 2) % 3], Mn[(S + 2) % 3],
+                                   Rs[(S + 2) % 3]);
+    else load_row(row, G[0], X[0], Mn[0], Rs[0]);
+    const f32x4 *g = G[S];
+    const f32x4 *xv = X[S];
+    const float mean = Mn[S], rs = Rs[S];
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < NQ; ++i)
@@ -242,6 +268,17 @@ __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
         if (a.dx && in_row(c)) __builtin_nontemporal_store(o, dr + c);
       }
     }
+    ++it;
+  };
+  if constexpr (kAhead) {
+    // Uniform trip count; pairs past row_end do nothing but the barrier.
+    for (int rb = row0; rb < row_end; rb += 6) {
+      pair(std::integral_constant<int, 0>{}, rb);
+      pair(std::integral_constant<int, 1>{}, rb + 2);
+      pair(std::integral_constant<int, 2>{}, rb + 4);
+    }
+  } else {
+    for (int rb = row0; rb < row_end; rb += 2) pair(std::integral_constant<int, 0>{}, rb);
   }
   // Group 1's column sums join group 0's (group 0 held the earlier row of
   // every pair), then group 0 writes the workgroup's partial.
@@ -521,13 +558,16 @@ int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_
   const bool vec = p.D % 4 == 0 && p.sgy % 4 == 0 && p.sx % 4 == 0 && (!p.dx || p.sdx % 4 == 0) &&
                    aligned16(p.gy) && aligned16(p.x) && aligned16(p.gamma) &&
                    (!p.dx || aligned16(p.dx));
-  // Persistent grid: the vector kernel's 512-thread workgroups (two row
-  // groups of four waves) at 2 per CU, the general kernel's 256-thread ones
-  // at 3 per CU; each takes one contiguous row block.
+  // Persistent grid, as many workgroups as fit the CUs at once, each taking
+  // one contiguous row block: the vector kernel's 512-thread workgroups (two
+  // row groups of four waves) at 2 per CU for D <= 1024 and 1 per CU above
+  // (their registers, with the next row pair in flight, leave room for one),
+  // the general kernel's 256-thread ones at 3 per CU.
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const bool use_vec = vec && p.D <= 8192;
   const int64_t want = use_vec ? (p.rows + 1) / 2 : (p.rows + 3) / 4;
-  const int64_t cap = (int64_t)(use_vec ? 2 : 3) * cus;
+  const int per_cu = !use_vec ? 3 : (p.D <= 1024 ? 2 : 1);
+  const int64_t cap = (int64_t)per_cu * cus;
   const int grid = (int)(want < cap ? (want > 0 ? want : 1) : cap);
   const int ng = (grid + kGroup - 1) / kGroup;
   const size_t part_floats = (size_t)grid * 2 * p.D;
