@@ -77,32 +77,38 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return (0.5f * x) * (1.0f + t);
 }
 
-// GELU with tanh from the hardware exponential and reciprocal,
-// tanh(s) = 1 - 2 / (1 + e^(2s)) (exact limits +-1 at overflow / underflow
-// of e^(2s)); the polynomial part keeps the reference's f32 operation order
-// (NovaToLinalgGeneric.cpp:1310-1331).  Absolute error of tanh ~1e-7, far
-// inside the bf16 output rounding.
+// The same GELU (NovaToLinalgGeneric.cpp:1310-1331) for the GEMM epilogues,
+// in the equivalent sigmoid form 0.5 x (1 + tanh s) = x / (1 + e^(-2s)),
+// s = sqrt(2/pi) (x + 0.044715 x^3): -2s log2(e) = x (k1 + k2 x^2), then
+// the hardware exp2 and reciprocal.  Five VALU operations and two
+// transcendentals instead of twelve and two (the epilogue is where config 3
+// spends its GELU time); limits: x / inf = -0 for x << 0, x for x >> 0.
+// Against the f64 formula: abs error <= 5.2e-7, rel error <= 9e-7 where
+// |gelu| > 1e-3 (x in [-12, 12]); bf16 rounding is 3.9e-3.
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
-#pragma clang fp contract(off)
-  const float x2 = x * x;
-  const float x3 = x2 * x;
-  const float cubic = 4.471500e-02f * x3;
-  const float inner = x + cubic;
-  const float scaled = 0.7978845608028654f * inner;
-  const float e = __builtin_amdgcn_exp2f(scaled * 2.8853900817779268f);  // e^(2s)
-  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
-  return (0.5f * x) * (1.0f + t);
+  constexpr float k1 = -2.3022082f;   // -2 sqrt(2/pi) log2(e)
+  constexpr float k2 = -0.10294324f;  // k1 * 0.044715
+  const float u = x * __builtin_fmaf(k2, x * x, k1);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u));
 }
 
+// f32 -> bf16 / f16, round to nearest even (NaN stays NaN), on gfx950's
+// conversion instructions (v_cvt_pk_bf16_f32, v_cvt_pk_f16_f32): branch-free,
+// and two values per instruction in the packed forms (a in the low half).
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint16_t to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
-
 __device__ __forceinline__ uint16_t to_f16(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, bf16x2v));
+}
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, f16x2v));
 }
 
 // Map a linear tile index to (batch, tile_m, tile_n), wave-uniform: within
@@ -142,14 +148,21 @@ __device__ __forceinline__ void tile_of(int id, const GemmArgs &a, int &b, int &
 // tiles [x*round/8, (x+1)*round/8): all eight XCDs work on neighbouring
 // tiles of the same band sweep, so an operand panel one XCD fetches from HBM
 // is found in the MALL by the XCDs that share it, and each XCD's 32 tiles
-// form a 4 x 8 block whose panels its L2 shares.  The last, partial round
-// keeps the identity order.
+// form a 4 x 8 block whose panels its L2 shares.  A last, partial round of
+// rem tiles gets the same treatment when rem is a multiple of 8 (XCD x takes
+// [x*rem/8, (x+1)*rem/8) of it); otherwise it keeps the identity order.
 __device__ __forceinline__ void round_tile_of(int id, const GemmArgs &a, int &b, int &tm, int &tn) {
   const int total = a.batch * a.tiles_m * a.tiles_n;
   const int round = a.round;
-  if (round > 0 && id < total / round * round) {
-    const int r = id / round, q = id - r * round;
-    id = r * round + (q & 7) * (round >> 3) + (q >> 3);
+  if (round > 0) {
+    const int full = total / round * round;
+    if (id < full) {
+      const int r = id / round, q = id - r * round;
+      id = r * round + (q & 7) * (round >> 3) + (q >> 3);
+    } else if (((total - full) & 7) == 0) {
+      const int q = id - full;
+      id = full + (q & 7) * ((total - full) >> 3) + (q >> 3);
+    }
   }
   band_tile(id, a, b, tm, tn);
 }

@@ -173,9 +173,17 @@ __device__ __forceinline__ u32x4 read_frag(const u32x4 *stage, int row_base, int
 constexpr int kStageBytes = 32768;
 static_assert(4 * kStageBytes <= kStages * 2 * kSlots * 16, "staging fits the ring");
 
+// The bias of the workgroup's 256 columns is staged to LDS as f32 at kernel
+// start (bias_s, nw0 = its first column) and read here with 16-byte LDS
+// loads, and the 16-bit conversions are the branch-free hardware ones: with
+// a per-element global bias load (behind a switch over the bias dtype) and a
+// NaN branch per converted value the compiler split the epilogue into ~1600
+// basic blocks whose loads each waited out a memory latency (config 3 spent
+// ~90 us of ~400 there).
 template <int ODT>
 __device__ __forceinline__ void store_staged(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
-                                             int bidx, int mw, int nw, int lane, char *stg) {
+                                             int bidx, int mw, int nw, int lane, char *stg,
+                                             const float *bias_s, int nw0) {
   static_assert(TM == 4 && TN == 4, "staging assumes a 128x128 wave tile");
   const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
   const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
@@ -193,11 +201,8 @@ __device__ __forceinline__ void store_staged(const f32x16 (&acc)[TM][TN], const 
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-        if (has_bias) {
-          const int n = nw + 32 * j + 8 * g + 4 * lh;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bv[e] = bias_at(a.bias, a.bias_dt, n + e);
-        }
+        if (has_bias)
+          bv = *reinterpret_cast<const f32x4 *>(bias_s + (nw - nw0) + 32 * j + 8 * g + 4 * lh);
 #pragma unroll
         for (int ii = 0; ii < TM / kRounds; ++ii) {
           const int i = r * (TM / kRounds) + ii;
@@ -215,10 +220,8 @@ __device__ __forceinline__ void store_staged(const f32x16 (&acc)[TM][TN], const 
           } else {
             const int c = 4 * j + g;
             const u32x2 w = ODT == NOVA_HIP_DT_BF16
-                                ? u32x2{to_bf16(x[0]) | ((uint32_t)to_bf16(x[1]) << 16),
-                                        to_bf16(x[2]) | ((uint32_t)to_bf16(x[3]) << 16)}
-                                : u32x2{to_f16(x[0]) | ((uint32_t)to_f16(x[1]) << 16),
-                                        to_f16(x[2]) | ((uint32_t)to_f16(x[3]) << 16)};
+                                ? u32x2{pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])}
+                                : u32x2{pack_f16(x[0], x[1]), pack_f16(x[2], x[3])};
             *reinterpret_cast<u32x2 *>(stg + R * kRowBytes + ((c ^ (R & (kChunks - 1))) << 4) +
                                        8 * lh) = w;
           }
@@ -243,6 +246,7 @@ template <int DT, bool AKC, bool BKC, int ODT>
 __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
   __shared__ u32x4 ring_a[kStages][kSlots];
   __shared__ u32x4 ring_b[kStages][kSlots];
+  __shared__ __attribute__((aligned(16))) float bias_s[BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -252,6 +256,9 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
   int bidx, tm, tn;
   round_tile_of(blockIdx.x, a, bidx, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  // The tile's bias as f32 (read by the epilogue after its barrier).
+  if ((a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU) && tid < BN)
+    bias_s[tid] = bias_at(a.bias, a.bias_dt, n0 + tid);
 
   DmaOperand oa, ob;
   oa.rsrc = make_rsrc(a.A + (int64_t)bidx * a.sab, a.a_bytes);
@@ -355,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs a) {
   __syncthreads();
   char *stg = (wave < 2 ? reinterpret_cast<char *>(ring_a) : reinterpret_cast<char *>(ring_b)) +
               (wave & 1) * kStageBytes;
-  store_staged<ODT>(acc, a, bidx, m0 + am, n0 + bn, lane, stg);
+  store_staged<ODT>(acc, a, bidx, m0 + am, n0 + bn, lane, stg, bias_s, n0);
 }
 
 template <int DT, bool AKC, bool BKC, int ODT>

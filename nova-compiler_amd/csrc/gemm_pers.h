@@ -86,17 +86,22 @@ __device__ __forceinline__ void dma_issue(const GemmArgs &a, const uint32_t (&la
 template <int ODT>
 constexpr int kEpiStores = ODT == NOVA_HIP_DT_F32 ? 64 : 32;
 
-// Epilogue of a wave's 128x128 output tile through its own 8 KB of LDS, in
-// rounds of 32 rows x 256 bytes (f32: 64 columns, 16-bit: 128 columns), so
-// that every global store instruction writes four rows x 256 B, i.e. whole
-// 128-byte lines.  16-byte chunk c of staging row R sits at c ^ (R & 15),
-// conflict-free for the column-wise writes and the row-wise reads.  The
-// staging accesses are plain C++ on an array of its own: the compiler then
-// writes the accumulation registers to LDS directly, and as the array is
-// not the DMA ring it places no DMA wait before them.
+// Epilogue of a wave's 128x128 output tile through its own 4 KB of LDS, in
+// rounds of 32 rows x 128 bytes (f32: one 32-column block, 16-bit: two), so
+// that every global store instruction writes eight rows x 128 B, i.e. whole
+// 128-byte lines.  16-byte chunk c of staging row R sits at c ^ (R & 7),
+// conflict-free for the column-wise writes and the row-wise reads.  Bias
+// (f32, staged in LDS for the tile's 256 columns) and GELU are applied on
+// the way.  The staging accesses are plain C++ on arrays of their own: the
+// compiler then stores the accumulation registers to LDS directly where no
+// arithmetic intervenes, and as they are not the DMA ring it places no DMA
+// wait before them.
 template <int ODT>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
-                                           int bidx, int mw, int nw, int lane, char *stg) {
+                                           int bidx, int mw, int nw, int lane, char *stg,
+                                           const float *bias_w) {
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
   // Lane-derived addresses are recomputed per tile: an opaque copy of the
   // lane id keeps the compiler from hoisting them out of the tile loop,
   // where they would stay live across the K loop.
@@ -105,44 +110,47 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], const Ge
   const int lr = ln & 31, lh = ln >> 5;
   constexpr bool kF32 = ODT == NOVA_HIP_DT_F32;
   constexpr int kEsz = kF32 ? 4 : 2;
-  constexpr int kJH = kF32 ? 2 : 1;  // rounds per 32-row block
-  constexpr int kJ = TN / kJH;       // 32-column blocks per round
+  constexpr int kJ = kF32 ? 1 : 2;   // 32-column blocks per round
+  constexpr int kJR = TN / kJ;       // rounds per 32-row block
   char *Cb = static_cast<char *>(a.C) + (int64_t)bidx * a.scb * kEsz;
 #pragma unroll
-  for (int jh = 0; jh < kJH; ++jh) {
+  for (int jr = 0; jr < kJR; ++jr) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int jj = 0; jj < kJ; ++jj)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int j = jh * kJ + jj;
-          const f32x4 x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                           acc[i][j][4 * g + 3]};
+          const int j = jr * kJ + jj;
+          f32x4 x = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                     acc[i][j][4 * g + 3]};
+          if (has_bias) x = x + *reinterpret_cast<const f32x4 *>(bias_w + 32 * j + 8 * g + 4 * lh);
+          if (has_gelu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = gelu_tanh_fast(x[e]);
+          }
           const int R = lr;
           if constexpr (kF32) {
-            const int c = 8 * jj + 2 * g + lh;
-            *reinterpret_cast<f32x4 *>(stg + R * 256 + ((c ^ (R & 15)) << 4)) = x;
+            const int c = 2 * g + lh;
+            *reinterpret_cast<f32x4 *>(stg + R * 128 + ((c ^ (R & 7)) << 4)) = x;
           } else {
             const int c = 4 * jj + g;
             const u32x2 w = ODT == NOVA_HIP_DT_BF16
-                                ? u32x2{to_bf16(x[0]) | ((uint32_t)to_bf16(x[1]) << 16),
-                                        to_bf16(x[2]) | ((uint32_t)to_bf16(x[3]) << 16)}
-                                : u32x2{to_f16(x[0]) | ((uint32_t)to_f16(x[1]) << 16),
-                                        to_f16(x[2]) | ((uint32_t)to_f16(x[3]) << 16)};
-            *reinterpret_cast<u32x2 *>(stg + R * 256 + ((c ^ (R & 15)) << 4) + 8 * lh) = w;
+                                ? u32x2{pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])}
+                                : u32x2{pack_f16(x[0], x[1]), pack_f16(x[2], x[3])};
+            *reinterpret_cast<u32x2 *>(stg + R * 128 + ((c ^ (R & 7)) << 4) + 8 * lh) = w;
           }
         }
-      u32x4 v[8];
+      u32x4 v[4];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int R = 4 * t + (ln >> 4), c = ln & 15;
-        v[t] = *reinterpret_cast<const u32x4 *>(stg + R * 256 + ((c ^ (R & 15)) << 4));
+      for (int t = 0; t < 4; ++t) {
+        const int R = 8 * t + (ln >> 3), c = ln & 7;
+        v[t] = *reinterpret_cast<const u32x4 *>(stg + R * 128 + ((c ^ (R & 7)) << 4));
       }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int R = 4 * t + (ln >> 4), c = ln & 15;
-        char *dst = Cb + ((int64_t)(mw + 32 * i + R) * a.scm + nw + 64 * jh) * kEsz + 16 * c;
+      for (int t = 0; t < 4; ++t) {
+        const int R = 8 * t + (ln >> 3), c = ln & 7;
+        char *dst = Cb + ((int64_t)(mw + 32 * i + R) * a.scm + nw + 32 * kJ * jr) * kEsz + 16 * c;
         *reinterpret_cast<u32x4 *>(dst) = v[t];
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -150,13 +158,21 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[TM][TN], const Ge
   }
 }
 
-// Launch: gridDim.x <= number of tiles, a.K / BK >= 2, a.epi == NONE.
+// Launch: gridDim.x <= number of tiles, a.K / BK >= 2.
 template <int DT, bool AKC, bool BKC, int ODT>
 __global__ __launch_bounds__(kThreads) void gemm_pers_kernel(GemmArgs a) {
   __shared__ u32x4 ring_a[kStages][kSlots];
   __shared__ u32x4 ring_b[kStages][kSlots];
-  __shared__ u32x4 stage_out[4][512];  // 8 KB per wave
-  static_assert(sizeof(ring_a) + sizeof(ring_b) + sizeof(stage_out) <= 160 * 1024, "LDS");
+  __shared__ u32x4 stage_out[4][256];  // 4 KB per wave
+  // The bias of the tile's 256 columns as f32, double-buffered by tile
+  // parity: a tile's bias is written at its start while the previous tile's
+  // epilogue may still read the other buffer.
+  __shared__ __attribute__((aligned(16))) float bias_s[2][BN];
+  static_assert(sizeof(ring_a) + sizeof(ring_b) + sizeof(stage_out) + sizeof(bias_s) <=
+                    160 * 1024,
+                "LDS");
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  static_assert(kThreads == BN, "one bias column per thread");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -283,6 +299,8 @@ __global__ __launch_bounds__(kThreads) void gemm_pers_kernel(GemmArgs a) {
 
   char *stg = reinterpret_cast<char *>(stage_out[wave]);
   for (int ti = 0; ti < ntiles; ++ti) {
+    // This tile's bias, read by its epilogue (after the K loop's barriers).
+    if (has_bias) bias_s[ti & 1][tid] = bias_at(a.bias, a.bias_dt, tc.n0 + tid);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -292,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void gemm_pers_kernel(GemmArgs a) {
     kstep(std::integral_constant<int, 0>{}, 0, ti);
     for (int kt = 1; kt < nk - 1; ++kt) kstep(std::integral_constant<int, 1>{}, kt, ti);
     kstep(std::integral_constant<int, 2>{}, nk - 1, ti);
-    store_tile<ODT>(acc, a, tc.bidx, tc.m0 + am, tc.n0 + bn, lane, stg);
+    store_tile<ODT>(acc, a, tc.bidx, tc.m0 + am, tc.n0 + bn, lane, stg, bias_s[ti & 1] + bn);
     tc = tn;
     tn_live = ti + 2 < ntiles;
     if (tn_live) tn = tile_at(a, ti + 2);
@@ -315,10 +333,10 @@ int32_t launch(const GemmArgs &a, hipStream_t s) {
   return check_hip(hipGetLastError(), "gemm_pers launch");
 }
 
-// The persistent kernel's problems: no epilogue op, two K steps or more, a
-// round size (one workgroup per CU) and at least one full round of tiles.
+// The persistent kernel's problems: two K steps or more, a round size (one
+// workgroup per CU) and at least one full round of tiles.
 inline bool applicable(const GemmArgs &a) {
-  return a.epi == NOVA_HIP_EPI_NONE && a.K / BK >= 2 && a.round > 0 &&
+  return a.K / BK >= 2 && a.round > 0 &&
          (int64_t)a.batch * a.tiles_m * a.tiles_n >= a.round;
 }
 

@@ -269,6 +269,55 @@ def test_c3_linear_bias_gelu_full_size(cuda):
     assert_close_lp(got, want, "c3")
 
 
+@pytest.mark.parametrize("N", [2048, 4352])
+@pytest.mark.parametrize("epi", [nh.EPI_GELU, nh.EPI_BIAS_GELU, nh.EPI_BIAS])
+def test_dma_epilogue_f32_out(cuda, epi, N):
+    """The LDS-DMA kernels' epilogue (bias staged in LDS as f32, GELU in its
+    sigmoid form on the hardware exp2 / reciprocal) with f32 output, held to
+    the f32 bar against the oracle's libm tanh evaluation.  N = 2048 gives 128
+    whole 256x256 tiles (the one-tile-per-workgroup kernel), N = 4352 gives
+    272 (the persistent kernel: 16 workgroups take two tiles, and each tile's
+    bias goes to the LDS buffer of its parity)."""
+    import torch
+    M, K = 4096, 192
+    x = S.normal((M, K), 31, dtype=S.BF16)
+    w = S.normal((N, K), 31, 0.0, 0.08, dtype=S.BF16, offset=M * K)
+    bias = S.normal((N,), 31, 0.0, 0.5, dtype=S.F32, offset=M * K + N * K)
+    X = to_dev(x, S.BF16, cuda)
+    Wt = to_dev(w, S.BF16, cuda).t()
+    has_bias = epi in (nh.EPI_BIAS, nh.EPI_BIAS_GELU)
+    Bs = torch.from_numpy(bias).to(cuda) if has_bias else None
+    got = nh.gemm(X, Wt, bias=Bs, epilogue=epi).cpu().numpy()
+    idx = sample_idx(1, M, N, 65536, 32)
+    want = ref.gemm_sampled(x, w.T, idx, adt=S.BF16, bdt=S.BF16,
+                            bias=bias if has_bias else None, biasdt=S.F32 if has_bias else None,
+                            epilogue=epi)
+    assert_close_f32(got[idx[:, 1], idx[:, 2]], want, f"dma epilogue {epi} N={N}")
+
+
+@pytest.mark.parametrize("epi", [nh.EPI_BIAS_GELU, nh.EPI_NONE])
+def test_persistent_epilogue_bf16_out(cuda, epi):
+    """The persistent kernel with bf16 output (config 3's epilogue form):
+    272 tiles, bias in bf16, against the oracle rounded to bf16."""
+    import torch
+    M, N, K = 4096, 4352, 256
+    x = S.normal((M, K), 33, dtype=S.BF16)
+    w = S.normal((N, K), 33, 0.0, 0.06, dtype=S.BF16, offset=M * K)
+    bias = S.normal((N,), 33, 0.0, 0.5, dtype=S.BF16, offset=M * K + N * K)
+    has_bias = epi != nh.EPI_NONE
+    X = to_dev(x, S.BF16, cuda)
+    Wt = to_dev(w, S.BF16, cuda).t()
+    Bs = to_dev(bias, S.BF16, cuda) if has_bias else None
+    got = nh.gemm(X, Wt, bias=Bs, epilogue=epi, out_dtype=torch.bfloat16)
+    idx = sample_idx(1, M, N, 65536, 34)
+    it = torch.from_numpy(idx).to(cuda)
+    g = got[it[:, 1], it[:, 2]].float().cpu().numpy()
+    want = ref.gemm_sampled(x, w.T, idx, adt=S.BF16, bdt=S.BF16,
+                            bias=bias if has_bias else None, biasdt=S.BF16 if has_bias else None,
+                            epilogue=epi, cdt=S.BF16)
+    assert_close_lp(g, want, f"persistent bf16 epilogue {epi}")
+
+
 @pytest.mark.parametrize("cfg", ["c4a", "c4b"])
 def test_c4_fp16_unaligned_full(cuda, cfg):
     """Config 4: fp16 batch GEMM with non-tile-aligned shapes (edge tiles)."""
