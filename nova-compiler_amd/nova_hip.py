@@ -150,8 +150,11 @@ def check(rc: int) -> None:
         raise NovaHipError(rc, lib().nova_hip_last_error().decode())
 
 
-def ref(d) -> Optional[ctypes.c_void_p]:
-    return None if d is None else ctypes.cast(ctypes.pointer(d), ctypes.c_void_p)
+def ref(d):
+    """Pointer argument to descriptor d (None passes NULL).  ctypes.byref is
+    accepted for the c_void_p parameters and costs ~0.1 us against ~3 us
+    for cast(pointer(d)); it keeps d alive for the call."""
+    return None if d is None else ctypes.byref(d)
 
 
 # --------------------------------------------------------------------------
