@@ -482,7 +482,17 @@ __global__ __launch_bounds__(256) void col_group_kernel(const float *part, int n
   const int g = blockIdx.y;
   const int p0 = g * kGroup, p1 = min(np, p0 + kGroup);
   float acc = 0.0f;
-  for (int p = p0; p < p1; ++p) acc = acc + part[(int64_t)p * width + idx];
+  if (p1 - p0 == kGroup) {
+    // A full group: all loads in flight at once, then the sum in partial
+    // order (a load-add loop waited out one memory latency per partial).
+    float v[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) v[u] = part[(int64_t)(p0 + u) * width + idx];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) acc = acc + v[u];
+  } else {
+    for (int p = p0; p < p1; ++p) acc = acc + part[(int64_t)p * width + idx];
+  }
   out[(int64_t)g * width + idx] = acc;
 }
 

@@ -295,27 +295,30 @@ def test_dma_epilogue_f32_out(cuda, epi, N):
     assert_close_f32(got[idx[:, 1], idx[:, 2]], want, f"dma epilogue {epi} N={N}")
 
 
-@pytest.mark.parametrize("epi", [nh.EPI_BIAS_GELU, nh.EPI_NONE])
-def test_persistent_epilogue_bf16_out(cuda, epi):
-    """The persistent kernel with bf16 output (config 3's epilogue form):
-    272 tiles, bias in bf16, against the oracle rounded to bf16."""
+@pytest.mark.parametrize("epi,odt", [(nh.EPI_BIAS_GELU, "bf16"), (nh.EPI_NONE, "bf16"),
+                                     (nh.EPI_BIAS_GELU, "f16"), (nh.EPI_GELU, "f16")])
+def test_persistent_epilogue_bf16_out(cuda, epi, odt):
+    """The persistent kernel with 16-bit output (config 3's epilogue form for
+    bf16): 272 tiles, bias in bf16, against the oracle rounded to the output
+    dtype."""
     import torch
+    cdt, tdt = (S.BF16, torch.bfloat16) if odt == "bf16" else (S.F16, torch.float16)
     M, N, K = 4096, 4352, 256
     x = S.normal((M, K), 33, dtype=S.BF16)
     w = S.normal((N, K), 33, 0.0, 0.06, dtype=S.BF16, offset=M * K)
     bias = S.normal((N,), 33, 0.0, 0.5, dtype=S.BF16, offset=M * K + N * K)
-    has_bias = epi != nh.EPI_NONE
+    has_bias = epi in (nh.EPI_BIAS, nh.EPI_BIAS_GELU)
     X = to_dev(x, S.BF16, cuda)
     Wt = to_dev(w, S.BF16, cuda).t()
     Bs = to_dev(bias, S.BF16, cuda) if has_bias else None
-    got = nh.gemm(X, Wt, bias=Bs, epilogue=epi, out_dtype=torch.bfloat16)
+    got = nh.gemm(X, Wt, bias=Bs, epilogue=epi, out_dtype=tdt)
     idx = sample_idx(1, M, N, 65536, 34)
     it = torch.from_numpy(idx).to(cuda)
     g = got[it[:, 1], it[:, 2]].float().cpu().numpy()
     want = ref.gemm_sampled(x, w.T, idx, adt=S.BF16, bdt=S.BF16,
                             bias=bias if has_bias else None, biasdt=S.BF16 if has_bias else None,
-                            epilogue=epi, cdt=S.BF16)
-    assert_close_lp(g, want, f"persistent bf16 epilogue {epi}")
+                            epilogue=epi, cdt=cdt)
+    assert_close_lp(g, want, f"persistent {odt} epilogue {epi}")
 
 
 @pytest.mark.parametrize("cfg", ["c4a", "c4b"])
