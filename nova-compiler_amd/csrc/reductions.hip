@@ -387,8 +387,19 @@ __global__ __launch_bounds__(64) void sce_mean_kernel(const float *row_loss, int
   const int per = (rows + 63) / 64;
   const int start = threadIdx.x * per;
   const int end = min(start + per, rows);
+  // The chunk's loads go out 32 at a time and are summed in order (a
+  // load-add loop waited out one memory latency per row: ~9 us at 4096
+  // rows).
+  constexpr int kBatch = 32;
   float p = 0.0f;
-  for (int i = start; i < end; ++i) p = p + row_loss[i];
+  for (int b0 = start; b0 < end; b0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) v[u] = b0 + u < end ? row_loss[b0 + u] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (b0 + u < end) p = p + v[u];
+  }
   part[threadIdx.x] = p;
   __syncthreads();
   if (threadIdx.x == 0) {
