@@ -375,6 +375,8 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_any_kernel(LnBwdArgs a) {
 // (x, y) sums rows [y*chunk, (y+1)*chunk) of columns [256x, 256x+256) in row
 // order, one column per thread, into part[y][cols] (f32).
 // ---------------------------------------------------------------------------
+constexpr int kColBatch = 16;  // rows in flight per thread in the column sums
+
 template <int DT>
 __global__ __launch_bounds__(256) void col_sum_partial_kernel(const void *in, int64_t ld, int rows,
                                                               int cols, int chunk, float *part) {
@@ -382,19 +384,28 @@ __global__ __launch_bounds__(256) void col_sum_partial_kernel(const void *in, in
   if (c >= cols) return;
   const int r0 = blockIdx.y * chunk;
   const int r1 = min(rows, r0 + chunk);
-  float acc = 0.0f;
-  for (int r = r0; r < r1; ++r) {
+  auto load = [&](int r) __attribute__((always_inline)) -> float {
     const int64_t i = (int64_t)r * ld + c;
-    float v;
     if constexpr (DT == NOVA_HIP_DT_F32) {
-      v = static_cast<const float *>(in)[i];
+      return static_cast<const float *>(in)[i];
     } else {
       const uint16_t h = static_cast<const uint16_t *>(in)[i];
-      if constexpr (DT == NOVA_HIP_DT_BF16) v = __uint_as_float((uint32_t)h << 16);
-      else v = (float)__builtin_bit_cast(_Float16, h);
+      if constexpr (DT == NOVA_HIP_DT_BF16) return __uint_as_float((uint32_t)h << 16);
+      else return (float)__builtin_bit_cast(_Float16, h);
     }
-    acc = v + acc;
+  };
+  // Rows go out kColBatch at a time and are added in row order (a load-add
+  // loop waited out one memory latency per row).
+  float acc = 0.0f;
+  int r = r0;
+  for (; r + kColBatch <= r1; r += kColBatch) {
+    float v[kColBatch];
+#pragma unroll
+    for (int u = 0; u < kColBatch; ++u) v[u] = load(r + u);
+#pragma unroll
+    for (int u = 0; u < kColBatch; ++u) acc = v[u] + acc;
   }
+  for (; r < r1; ++r) acc = load(r) + acc;
   part[(int64_t)blockIdx.y * cols + c] = acc;
 }
 
@@ -415,8 +426,7 @@ __global__ __launch_bounds__(256) void col_sum_partial_vec_kernel(const void *in
   for (int v = 0; v < V; ++v) acc[v] = 0.0f;
   const char *base = static_cast<const char *>(in);
   constexpr int esz = DT == NOVA_HIP_DT_F32 ? 4 : 2;
-  for (int r = r0; r < r1; ++r) {
-    const u32x4 w = *reinterpret_cast<const u32x4 *>(base + ((int64_t)r * ld + c0) * esz);
+  auto add_row = [&](const u32x4 &w) __attribute__((always_inline)) {
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       float x;
@@ -429,7 +439,21 @@ __global__ __launch_bounds__(256) void col_sum_partial_vec_kernel(const void *in
       }
       acc[v] = x + acc[v];
     }
+  };
+  auto row_ptr = [&](int r) __attribute__((always_inline)) {
+    return reinterpret_cast<const u32x4 *>(base + ((int64_t)r * ld + c0) * esz);
+  };
+  // Rows go out kColBatch at a time and are added in row order (a load-add
+  // loop waited out one memory latency per row).
+  int r = r0;
+  for (; r + kColBatch <= r1; r += kColBatch) {
+    u32x4 w[kColBatch];
+#pragma unroll
+    for (int u = 0; u < kColBatch; ++u) w[u] = *row_ptr(r + u);
+#pragma unroll
+    for (int u = 0; u < kColBatch; ++u) add_row(w[u]);
   }
+  for (; r < r1; ++r) add_row(*row_ptr(r));
   float *out = part + (int64_t)blockIdx.y * cols + c0;
 #pragma unroll
   for (int v = 0; v < V; ++v) out[v] = acc[v];
