@@ -2,10 +2,9 @@
 // backward and the column sums of nova.linear_backward's bias gradient.  All
 // are HBM-bound streams (no MFMA): rows are read with coalesced 16-byte
 // loads, row reductions run inside one wave64 with cross-lane shuffles, and
-// column reductions over rows are deterministic -- each workgroup sums its
-// own contiguous block of rows in row order into per-workgroup partials,
-// which a second pass adds up in workgroup order -- so two runs give the
-// same bits.
+// column reductions over rows are deterministic -- each workgroup sums a
+// fixed set of rows in a fixed order into per-workgroup partials, which a
+// second pass adds up in workgroup order -- so two runs give the same bits.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -137,9 +136,9 @@ __global__ __launch_bounds__(256) void sce_backward_flat_kernel(SceBwdArgs a, in
 //   s1 = sum gg, s2 = sum gg * xh                        (row reductions)
 //   dx = ((gg - s1*invD) - xh * (s2*invD)) * rstd        (reference op order)
 //   dgamma[d] = sum_r gy * xh, dbeta[d] = sum_r gy       (column reductions)
-// Each workgroup takes one contiguous block of rows and writes its column
-// sums as one partial [2][D] to [grid][2][D]; reduce_partials adds the
-// partials in workgroup order.
+// Each workgroup takes a fixed set of rows and writes its column sums as
+// one partial [2][D] to [grid][2][D]; reduce_partials adds the partials in
+// workgroup order.
 // ---------------------------------------------------------------------------
 struct LnBwdArgs {
   const float *gy;
@@ -159,9 +158,10 @@ struct LnBwdArgs {
 // accumulators for the same columns, so the column sums need no LDS
 // traffic and no turn-taking; the row reductions s1, s2 combine the four
 // waves' partials through LDS in wave order (one barrier per row).  A
-// 512-thread workgroup runs two such groups on alternate rows of its
-// contiguous row block; at the end group 1's column sums are added to group
-// 0's through LDS, and the workgroup writes one partial [2][D].
+// 512-thread workgroup runs two such groups on the two rows of each of its
+// row pairs (pairs b, b + grid, b + 2 * grid, ... for workgroup b); at the
+// end group 1's column sums are added to group 0's through LDS, and the
+// workgroup writes one partial [2][D].
 template <int NQ, bool FULL>
 __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
 #pragma clang fp contract(off)
@@ -175,31 +175,38 @@ __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
   f32x4 gm[NQ], acc_g[NQ], acc_b[NQ];
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
-    const int c = q * 64 * NQ + lane + 64 * i;
-    gm[i] = in_row(c) ? gam4[c] : f32x4{0.f, 0.f, 0.f, 0.f};
     acc_g[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     acc_b[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const int per_wg = (a.rows + gridDim.x - 1) / gridDim.x;
-  const int row0 = min(a.rows, (int)blockIdx.x * per_wg);
-  const int row_end = min(a.rows, row0 + per_wg);
-  // Loads of row r (zeros past the block's end): gy, x, mean, rstd.
-  auto load_row = [&](int row, f32x4 (&g)[NQ], f32x4 (&xv)[NQ], float &mean, float &rs)
+  // Row pairs interleaved over the grid (workgroup b takes pairs b,
+  // b + grid, ...): the rows in work at any time form one window that
+  // sweeps the matrix in order.
+  const int step = 2 * gridDim.x;
+  const int row0 = 2 * blockIdx.x;
+  const int row_end = a.rows;
+  // Loads of row r: gy, x, the saved mean sum and rstd.  A row past the
+  // matrix's end reads its last row and a chunk past the row's end
+  // reads its last chunk (valid memory; the values are masked or discarded
+  // where they are used), so that no load sits under a branch: a load issued
+  // on one path only makes every later wait assume nothing else is in flight
+  // and drain the loads of the rows ahead.  The caller guarantees
+  // row0 < row_end and D >= 4.
+  auto load_row = [&](int row, f32x4 (&g)[NQ], f32x4 (&xv)[NQ], float &msum, float &rs)
                       __attribute__((always_inline)) {
-    const bool live = row < row_end;
-    const f32x4 *gr = reinterpret_cast<const f32x4 *>(a.gy + (int64_t)(live ? row : row0) * a.sgy);
-    const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)(live ? row : row0) * a.sx);
+    const int rc = min(row, row_end - 1);
+    const f32x4 *gr = reinterpret_cast<const f32x4 *>(a.gy + (int64_t)rc * a.sgy);
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)rc * a.sx);
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int c = q * 64 * NQ + lane + 64 * i;
-      const bool ok = live && in_row(c);
-      g[i] = ok ? __builtin_nontemporal_load(gr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
-      xv[i] = ok ? __builtin_nontemporal_load(xr + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const int cc = FULL ? c : min(c, nv4 - 1);
+      g[i] = __builtin_nontemporal_load(gr + cc);
+      xv[i] = __builtin_nontemporal_load(xr + cc);
     }
-    mean = live ? a.mean_sum[row] * a.invD : 0.0f;
-    rs = live ? a.rstd[row] : 0.0f;
+    msum = a.mean_sum[rc];
+    rs = a.rstd[rc];
   };
-  // With NQ <= 4 the row pairs two iterations ahead are loaded while the
+  // With NQ <= 4 the row pairs two steps ahead are loaded while the
   // current one is reduced and written (three register slots; the loop is
   // unrolled by three so that slots are compile-time registers).  The
   // barrier waits for LDS only, not for these loads.
@@ -207,28 +214,31 @@ __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
   constexpr int kSlots = kAhead ? 3 : 1;
   f32x4 G[kSlots][NQ], X[kSlots][NQ];
   float Mn[kSlots], Rs[kSlots];
-  if constexpr (kAhead) {
-    load_row(row0 + grp, G[0], X[0], Mn[0], Rs[0]);
-    load_row(row0 + 2 + grp, G[1], X[1], Mn[1], Rs[1]);
-  }
   int it = 0;
   // One row pair: row rb + grp, its data in slot S.
   auto pair = [&](auto slot, int rb) __attribute__((always_inline)) {
     constexpr int S = decltype(slot)::value;
     const int row = rb + grp;
     const bool live = row < row_end;
-    if constexpr (kAhead) load_row(rb + 4 + grp, G[(S + 2) % 3], X[(S + 2) % 3], Mn[(S + 2) % 3],
-                                   Rs[(S + 2) % 3]);
+    if constexpr (kAhead) load_row(rb + 2 * step + grp, G[(S + 2) % 3], X[(S + 2) % 3],
+                                   Mn[(S + 2) % 3], Rs[(S + 2) % 3]);
     else load_row(row, G[0], X[0], Mn[0], Rs[0]);
-    const f32x4 *g = G[S];
-    const f32x4 *xv = X[S];
-    const float mean = Mn[S], rs = Rs[S];
+    // Chunks past the row's end count as zeros.
+    f32x4 g[NQ], xv[NQ], gmv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const bool in = in_row(q * 64 * NQ + lane + 64 * i);
+      g[i] = in ? G[S][i] : f32x4{0.f, 0.f, 0.f, 0.f};
+      xv[i] = in ? X[S][i] : f32x4{0.f, 0.f, 0.f, 0.f};
+      gmv[i] = in ? gm[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float mean = Mn[S] * a.invD, rs = Rs[S];
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < NQ; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float gg = g[i][e] * gm[i][e];
+        const float gg = g[i][e] * gmv[i][e];
         const float xh = (xv[i][e] - mean) * rs;
         s1 = s1 + gg;
         s2 = s2 + gg * xh;
@@ -257,7 +267,7 @@ __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
         f32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float gg = g[i][e] * gm[i][e];
+          const float gg = g[i][e] * gmv[i][e];
           const float xh = (xv[i][e] - mean) * rs;
           const float t1 = gg - ms1;
           const float t2 = xh * ms2;
@@ -270,15 +280,33 @@ __global__ __launch_bounds__(512) void layer_norm_bwd_rows_kernel(LnBwdArgs a) {
     }
     ++it;
   };
-  if constexpr (kAhead) {
-    // Uniform trip count; pairs past row_end do nothing but the barrier.
-    for (int rb = row0; rb < row_end; rb += 6) {
-      pair(std::integral_constant<int, 0>{}, rb);
-      pair(std::integral_constant<int, 1>{}, rb + 2);
-      pair(std::integral_constant<int, 2>{}, rb + 4);
+  // One guard around the first loads and the loop: a path that enters the
+  // loop without the first loads would leave gamma's loads as the only ones
+  // in flight on it, and the loop's waits would be set for that path.
+  if (row0 < row_end) {
+    // Gamma first, ahead of the rows' loads, so that its wait is covered by
+    // the first row's.
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int c = q * 64 * NQ + lane + 64 * i;
+      gm[i] = gam4[FULL ? c : min(c, nv4 - 1)];
     }
-  } else {
-    for (int rb = row0; rb < row_end; rb += 2) pair(std::integral_constant<int, 0>{}, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kAhead) {
+      // In order, as the loop issues them: the loop's waits count on it.
+      load_row(row0 + grp, G[0], X[0], Mn[0], Rs[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      load_row(row0 + step + grp, G[1], X[1], Mn[1], Rs[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      // Uniform trip count; pairs past row_end do nothing but the barrier.
+      for (int rb = row0; rb < row_end; rb += 3 * step) {
+        pair(std::integral_constant<int, 0>{}, rb);
+        pair(std::integral_constant<int, 1>{}, rb + step);
+        pair(std::integral_constant<int, 2>{}, rb + 2 * step);
+      }
+    } else {
+      for (int rb = row0; rb < row_end; rb += step) pair(std::integral_constant<int, 0>{}, rb);
+    }
   }
   // Group 1's column sums join group 0's (group 0 held the earlier row of
   // every pair), then group 0 writes the workgroup's partial.
@@ -466,6 +494,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// out[c] = v in dtype odt (nothing when out is null).
+__device__ __forceinline__ void store_col(void *out, int c, float v, int odt) {
+  if (!out) return;
+  if (odt == NOVA_HIP_DT_F32) static_cast<float *>(out)[c] = v;
+  else if (odt == NOVA_HIP_DT_BF16) static_cast<uint16_t *>(out)[c] = f32_to_bf16(v);
+  else static_cast<uint16_t *>(out)[c] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
 // Stage 2 (shared by the LayerNorm and bias gradients): out_k[c] =
 // sum_p part[p][k][c] over the np partials in order, for the nk outputs k
 // of each partial (stride np_stride elements between partials), stored in
@@ -488,11 +524,7 @@ __global__ __launch_bounds__(256) void col_reduce_kernel(const float *part, int 
     for (int u = 0; u < 8; ++u) acc = acc + v[u];
   }
   for (; i < np; ++i) acc = acc + p[(int64_t)i * p_stride];
-  void *out = k == 0 ? out0 : out1;
-  if (!out) return;
-  if (odt == NOVA_HIP_DT_F32) static_cast<float *>(out)[c] = acc;
-  else if (odt == NOVA_HIP_DT_BF16) static_cast<uint16_t *>(out)[c] = f32_to_bf16(acc);
-  else static_cast<uint16_t *>(out)[c] = __builtin_bit_cast(uint16_t, (_Float16)acc);
+  store_col(k == 0 ? out0 : out1, c, acc, odt);
 }
 
 // Two-level reduction of np partials when np is large: groups of kGroup
@@ -520,6 +552,45 @@ __global__ __launch_bounds__(256) void col_group_kernel(const float *part, int n
   out[(int64_t)g * width + idx] = acc;
 }
 
+// One launch for np <= kTreeGroups * kGroup partials: a workgroup's 256
+// threads are kTreeCols columns x kTreeGroups groups; thread (g, c) sums
+// partials [g * kGroup, (g + 1) * kGroup) of column c in order, all loads in
+// flight at once, and the group sums are added in group order through LDS.
+// That is the order of col_group_kernel followed by col_reduce_kernel, so
+// the sums are the same bits, with one launch and one memory latency less.
+constexpr int kTreeGroups = 8;
+constexpr int kTreeCols = 256 / kTreeGroups;
+
+__global__ __launch_bounds__(256) void col_tree_kernel(const float *part, int np, int nk,
+                                                       int cols, void *out0, void *out1,
+                                                       int odt) {
+  __shared__ float red[kTreeGroups][kTreeCols];
+  const int width = nk * cols;
+  const int cl = threadIdx.x % kTreeCols, g = threadIdx.x / kTreeCols;
+  const int idx = blockIdx.x * kTreeCols + cl;
+  const int p0 = g * kGroup, p1 = min(np, p0 + kGroup);
+  float acc = 0.0f;
+  if (idx < width) {
+    if (p1 - p0 == kGroup) {
+      float v[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) v[u] = part[(int64_t)(p0 + u) * width + idx];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) acc = acc + v[u];
+    } else {
+      for (int p = p0; p < p1; ++p) acc = acc + part[(int64_t)p * width + idx];
+    }
+  }
+  red[g][cl] = acc;
+  __syncthreads();
+  if (g != 0 || idx >= width) return;
+  const int ng = (np + kGroup - 1) / kGroup;
+  float t = 0.0f;
+  for (int j = 0; j < ng; ++j) t = t + red[j][cl];
+  const int k = idx / cols, c = idx - k * cols;
+  store_col(k == 0 ? out0 : out1, c, t, odt);
+}
+
 // Final column reduction of np partials, each `width` = nk * cols floats
 // ([np][nk][cols]); uses ws2 (np / kGroup + 1) * width floats when np is
 // large.
@@ -527,6 +598,11 @@ int32_t reduce_partials(const float *part, int np, int nk, int cols, void *out0,
                         int odt, float *ws2, hipStream_t s) {
   const int width = nk * cols;
   const unsigned blocks = (unsigned)((width + 255) / 256);
+  if (np > 2 * kGroup && np <= kTreeGroups * kGroup) {
+    hipLaunchKernelGGL(col_tree_kernel, dim3((unsigned)((width + kTreeCols - 1) / kTreeCols)),
+                       dim3(256), 0, s, part, np, nk, cols, out0, out1, odt);
+    return check_hip(hipGetLastError(), "column reduce launch");
+  }
   if (np > 2 * kGroup) {
     const int ng = (np + kGroup - 1) / kGroup;
     hipLaunchKernelGGL(col_group_kernel, dim3(blocks, (unsigned)ng), dim3(256), 0, s, part, np,
@@ -586,19 +662,26 @@ int32_t launch_sce_backward(const SceBackwardProblem &p, hipStream_t s) {
 
 int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_t s) {
   // The column accumulators of a workgroup live in LDS: rows up to 8192.
-  if (p.rows > 0x7fffffff - 4 || p.D > kAnyMaxD)
+  // Row indices run up to three grid strides past the last row (the row
+  // kernel's lookahead): rows stay below 2^31 - 2^20.
+  if (p.rows > 0x7fffffff - (1 << 20))
+    return fail(NOVA_HIP_ERANGE, "layer_norm_backward: %lld rows exceed 2^31 - 2^20",
+                (long long)p.rows);
+  if (p.D > kAnyMaxD)
     return fail(NOVA_HIP_ERANGE, "layer_norm_backward: D = %lld exceeds %d", (long long)p.D,
                 kAnyMaxD);
   const bool vec = p.D % 4 == 0 && p.sgy % 4 == 0 && p.sx % 4 == 0 && (!p.dx || p.sdx % 4 == 0) &&
                    aligned16(p.gy) && aligned16(p.x) && aligned16(p.gamma) &&
                    (!p.dx || aligned16(p.dx));
   // Persistent grid, as many workgroups as fit the CUs at once, each taking
-  // one contiguous row block: the vector kernel's 512-thread workgroups (two
+  // a fixed set of rows (every grid-th row pair in the vector kernel, one
+  // contiguous block in the general one): the vector kernel's 512-thread
+  // workgroups (two
   // row groups of four waves) at 2 per CU for D <= 1024 and 1 per CU above
   // (their registers, with the next row pair in flight, leave room for one),
   // the general kernel's 256-thread ones at 3 per CU.
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const bool use_vec = vec && p.D <= 8192;
+  const bool use_vec = vec && p.D >= 4 && p.D <= 8192;
   const int64_t want = use_vec ? (p.rows + 1) / 2 : (p.rows + 3) / 4;
   const int per_cu = !use_vec ? 3 : (p.D <= 1024 ? 2 : 1);
   const int64_t cap = (int64_t)per_cu * cus;

@@ -127,7 +127,8 @@ def check_ln_bwd(gy, x, g, Sm, rs, cuda, what):
 
 
 @pytest.mark.parametrize("R,D", [(1, 4), (3, 3), (5, 64), (7, 1000), (33, 1024), (9, 4096),
-                                 (4, 5000), (2, 8192), (130, 257), (1001, 1024)])
+                                 (4, 5000), (2, 8192), (130, 257), (1001, 1024),
+                                 (301, 4096), (600, 2048)])
 def test_layer_norm_backward_shapes(cuda, R, D):
     check_ln_bwd(*ln_bwd_inputs(R, D, 51), cuda, f"ln_bwd {R}x{D}")
 
@@ -200,7 +201,8 @@ def test_linear_backward_f32_bit_exact(cuda, M, K, N):
     assert_close_f32(gb.cpu().numpy(), gb_ref, "f32 grad_bias")
 
 
-@pytest.mark.parametrize("M,K,N", [(7, 5, 3), (96, 160, 200), (256, 512, 256), (300, 200, 520)])
+@pytest.mark.parametrize("M,K,N", [(7, 5, 3), (96, 160, 200), (256, 512, 256), (300, 200, 520),
+                                   (6400, 64, 96)])
 def test_linear_backward_bf16(cuda, M, K, N):
     dt = S.BF16
     x = S.normal((M, K), 62, dtype=dt)
