@@ -478,6 +478,9 @@ __global__ __launch_bounds__(256) void col_sum_partial_vec_kernel(const void *in
     u32x4 w[kColBatch];
 #pragma unroll
     for (int u = 0; u < kColBatch; ++u) w[u] = *row_ptr(r + u);
+    // All loads before the first add (for f16 the scheduler otherwise
+    // moved half of them down, each with its own wait).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kColBatch; ++u) add_row(w[u]);
   }
