@@ -66,8 +66,16 @@ def to_dev(a, dt, torch):
     return t.view(torch.bfloat16 if dt == S.BF16 else torch.float16)
 
 
+# Per-launch distribution of the last time_launches call (see there).
+_LAUNCH_STATS = {}
+
+
 def time_launches(fn, steps, warmup, torch):
-    """Average ms per call over `steps` calls after `warmup` calls."""
+    """Average ms per call over `steps` back-to-back calls after `warmup`
+    calls (the returned figure).  A second pass of `steps` calls, each
+    between two events, gives the median and p10 / p90 of single launches
+    in _LAUNCH_STATS; those events add a little to each launch, so the
+    average is taken from the first pass only."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -78,7 +86,21 @@ def time_launches(fn, steps, warmup, torch):
         fn(i)
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    avg = start.elapsed_time(end) / steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
+        fn(i)
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    t = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+
+    def q(f):
+        return t[min(len(t) - 1, int(round(f * (len(t) - 1))))]
+
+    _LAUNCH_STATS.clear()
+    _LAUNCH_STATS.update({"p10": q(0.1), "p50": q(0.5), "p90": q(0.9), "n": steps})
+    return avg
 
 
 def bench_c2(args, torch, nh, S):
@@ -351,7 +373,19 @@ def cpu_baseline(S):
                       f"({flop:.3g} FLOP in {spent:.1f} s, single thread, "
                       f"oracle/nova_cpu_ref.c i-j-k loop order); extrapolated linearly",
             "full_config_seconds_extrapolated": C2_FLOP / (tf * 1e12),
-            "host_cpus": os.cpu_count()}
+            "host_cpus": os.cpu_count(), "host_cpu_model": cpu_model()}
+
+
+def cpu_model():
+    """The host CPU's model name, from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -376,7 +410,10 @@ def main():
     def stage(name, f):
         t0 = time.time()
         print(f"[bench] {name} ...", file=sys.stderr, flush=True)
+        _LAUNCH_STATS.clear()
         r = f()
+        if isinstance(r, dict) and _LAUNCH_STATS:
+            r["launch_ms"] = dict(_LAUNCH_STATS)
         print(f"[bench] {name}: {json.dumps(r)} ({time.time() - t0:.1f} s)", file=sys.stderr,
               flush=True)
         torch.cuda.empty_cache()
@@ -427,6 +464,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": head["ms"],
+        # Single-launch times of config 2 (a second pass, events between launches).
+        "launch_ms": head.get("launch_ms"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
