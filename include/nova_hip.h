@@ -62,6 +62,14 @@ typedef struct NovaMemRef3D {
   int64_t strides[3];
 } NovaMemRef3D;
 
+typedef struct NovaMemRef4D {
+  void *allocated;
+  void *aligned;
+  int64_t offset;
+  int64_t sizes[4];
+  int64_t strides[4];
+} NovaMemRef4D;
+
 /* Status codes. */
 enum {
   NOVA_HIP_SUCCESS = 0,
@@ -74,11 +82,23 @@ enum {
   NOVA_HIP_ENOMEM = 7     /* workspace allocation failed                    */
 };
 
-/* dtype codes (flags bits 0-3: input, 4-7: output, 12-15: bias). */
+/* dtype codes (flags bits 0-3: input, 4-7: output, 12-15: bias; the
+ * integer codes name index / label operands of the program-glue ops). */
 enum {
   NOVA_HIP_DT_F32 = 0,
   NOVA_HIP_DT_BF16 = 1,
-  NOVA_HIP_DT_F16 = 2
+  NOVA_HIP_DT_F16 = 2,
+  NOVA_HIP_DT_I32 = 3,
+  NOVA_HIP_DT_I64 = 4,
+  NOVA_HIP_DT_I16 = 5
+};
+
+/* binary op codes of _mlir_ciface_nova_hip_binary_f32. */
+enum {
+  NOVA_HIP_BIN_ADD = 0,
+  NOVA_HIP_BIN_SUB = 1,
+  NOVA_HIP_BIN_MUL = 2,
+  NOVA_HIP_BIN_DIV = 3
 };
 
 /* epilogue codes (flags bits 8-11). */
@@ -267,6 +287,58 @@ int32_t _mlir_ciface_nova_hip_matmul_backward(const NovaMemRef2D *grad,
                                               NovaMemRef2D *grad_a,
                                               NovaMemRef2D *grad_b,
                                               int32_t flags);
+/* ------------------------------------------------------------------------
+ * Program glue: the elementwise, index and reduction ops a whole training
+ * step needs around the GEMMs and row reductions (the reference's GPT step
+ * ltest/test.mlir uses each of them), so that libnova_run can execute such
+ * programs end to end.  All f32; dense operands read and written with
+ * 16-byte accesses where aligned.
+ * ---------------------------------------------------------------------- */
+/* nova.add / nova.sub / nova.mul / nova.div (Nova_BinaryOp,
+ * NovaOps.td:600-700; one IEEE operation per element, numpy-style
+ * broadcasting): c = a (op) b over c's [4]-shaped index space, op a
+ * NOVA_HIP_BIN_* code.  a and b give stride 0 on a broadcast dimension
+ * (size 1 in the operand); c may alias a or b element for element (the
+ * reference's in_place form). */
+int32_t _mlir_ciface_nova_hip_binary_f32(const NovaMemRef4D *a, const NovaMemRef4D *b,
+                                         NovaMemRef4D *c, int32_t op);
+/* A splat nova.constant (NovaOps.td:331): out[i] = value for all i. */
+int32_t _mlir_ciface_nova_hip_fill_f32(NovaMemRef1D *out, float value);
+/* nova.gelu on its own (NovaGeluForwardPattern, NovaToLinalgGeneric.cpp:
+ * 1277-1337), when its input has other uses and it cannot fold into the
+ * GEMM epilogue: y = (0.5 x)(1 + tanh(0.7978845608028654 (x + 0.044715 x^3)))
+ * in the reference's operation order.  x, y : [n], dense. */
+int32_t _mlir_ciface_nova_hip_gelu_f32(const NovaMemRef1D *x, NovaMemRef1D *y);
+/* nova.gelu_backward (NovaGeluBackwardPattern, NovaToLinalgGeneric.cpp:
+ * 1339-1425): out = grad_out * (0.5 (1 + tanh(g)) + 0.5 x (1 - tanh(g)^2) g'),
+ * g = 0.797884583 (x + 0.044715 x^3), g' = (1 + 0.134145 x^2) 0.797884583,
+ * in the reference's operation order.  All [n], dense. */
+int32_t _mlir_ciface_nova_hip_gelu_backward_f32(const NovaMemRef1D *grad_out,
+                                                const NovaMemRef1D *x, NovaMemRef1D *out);
+/* nova.gather along axis 0 (NovaGatherOpLowering, NovaToLinalgGeneric.cpp:
+ * 2372-2471), the embedding lookup: out[i, :] = table[idx[i], :].
+ *   table : [V, D] f32; idx : [n] of idx_dt (NOVA_HIP_DT_I16, zero-extended
+ *   as the reference's ExtUIOp, :2434-2449; NOVA_HIP_DT_I32; NOVA_HIP_DT_I64);
+ *   out : [n, D] f32.  An index outside [0, V) gives a NaN row. */
+int32_t _mlir_ciface_nova_hip_gather_f32(const NovaMemRef2D *table, const NovaMemRef1D *idx,
+                                         NovaMemRef2D *out, int32_t idx_dt);
+/* nova.scatter_add along axis 0 (NovaScatterAddOpLowering, NovaToLinalg.cpp:
+ * 1086-1290), in place: out[idx[i], :] += src[i, :] by f32 atomic adds, the
+ * reference's memref.atomic_rmw addf; indices outside [0, V) are skipped as
+ * its bounds check does.  The order of adds into one row is not fixed.
+ *   out : [V, D] f32 (holds the op's `input` on entry); idx : [n] as for
+ *   gather; src : [n, D] f32. */
+int32_t _mlir_ciface_nova_hip_scatter_add_f32(NovaMemRef2D *out, const NovaMemRef1D *idx,
+                                              const NovaMemRef2D *src, int32_t idx_dt);
+/* nova.reduce<sum> over one dimension (Nova_ReduceOp, NovaOps.td:191-230):
+ * x viewed as [outer, n, inner], out[o, i] = sum_j x[o, j, i] with j
+ * ascending (one sequential sum per output, the linalg.reduce order). */
+int32_t _mlir_ciface_nova_hip_reduce_sum_f32(const NovaMemRef3D *x, NovaMemRef2D *out);
+/* Labels / indices to i32: NovaSceForwardLowering zero-extends non-i32
+ * labels (NovaToLinalgGeneric.cpp:801-1010); narrow integers are
+ * zero-extended, i64 truncated.  src : [n] of src_dt; dst : [n] i32. */
+int32_t _mlir_ciface_nova_hip_index_to_i32(const NovaMemRef1D *src, NovaMemRef1D *dst,
+                                           int32_t src_dt);
 /* ------------------------------------------------------------------------
  * Runtime.  The reference's host runtime is libmlir_cuda_runtime's mgpu*
  * calls plus cudaMallocAsync / cudaMemcpyAsync declared by FixGpuLaunch.cpp

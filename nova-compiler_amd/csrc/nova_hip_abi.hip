@@ -584,6 +584,192 @@ int32_t _mlir_ciface_nova_hip_matmul_backward(const NovaMemRef2D *grad, const No
   return NOVA_HIP_SUCCESS;
 }
 
+// ---- program glue ---------------------------------------------------------------
+namespace {
+bool index_dt_ok(int32_t dt) {
+  return dt == NOVA_HIP_DT_I16 || dt == NOVA_HIP_DT_I32 || dt == NOVA_HIP_DT_I64;
+}
+int index_size(int32_t dt) { return dt == NOVA_HIP_DT_I16 ? 2 : dt == NOVA_HIP_DT_I32 ? 4 : 8; }
+// A dense 1-D f32 view (unit stride, or a single element).
+int32_t dense1(const NovaMemRef1D *d, const char *w, const char *what) {
+  if (!d) return fail(NOVA_HIP_EINVAL, "%s: null %s", w, what);
+  if (d->sizes[0] < 0) return fail(NOVA_HIP_ESHAPE, "%s: negative size", w);
+  if (d->sizes[0] > 1 && d->strides[0] != 1)
+    return fail(NOVA_HIP_ESTRIDE, "%s: %s must be dense", w, what);
+  if (d->sizes[0] > 0 && !d->aligned) return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+  return NOVA_HIP_SUCCESS;
+}
+}  // namespace
+
+int32_t _mlir_ciface_nova_hip_binary_f32(const NovaMemRef4D *a, const NovaMemRef4D *b,
+                                         NovaMemRef4D *c, int32_t op) {
+  clear_error();
+  const char *w = "binary";
+  if (!a || !b || !c) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  if (op < NOVA_HIP_BIN_ADD || op > NOVA_HIP_BIN_DIV)
+    return fail(NOVA_HIP_EINVAL, "%s: unknown op %d", w, op);
+  BinaryProblem p;
+  int64_t n = 1;
+  for (int d = 0; d < 4; ++d) {
+    const int64_t m = c->sizes[d];
+    if (m < 0 || a->sizes[d] < 0 || b->sizes[d] < 0)
+      return fail(NOVA_HIP_ESHAPE, "%s: negative size", w);
+    if ((a->sizes[d] != m && a->sizes[d] != 1) || (b->sizes[d] != m && b->sizes[d] != 1))
+      return fail(NOVA_HIP_ESHAPE, "%s: dim %d: %lld and %lld do not broadcast to %lld", w, d,
+                  (long long)a->sizes[d], (long long)b->sizes[d], (long long)m);
+    p.size[d] = m;
+    p.sa[d] = a->sizes[d] == 1 ? 0 : a->strides[d];
+    p.sb[d] = b->sizes[d] == 1 ? 0 : b->strides[d];
+    p.sc[d] = c->strides[d];
+    n *= m;
+  }
+  if (n == 0) return NOVA_HIP_SUCCESS;
+  if (!a->aligned || !b->aligned || !c->aligned)
+    return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+  p.a = in_f32(a);
+  p.b = in_f32(b);
+  p.c = out_f32(c);
+  p.op = op;
+  return launch_binary(p, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_fill_f32(NovaMemRef1D *out, float value) {
+  clear_error();
+  if (!out) return fail(NOVA_HIP_EINVAL, "fill: null descriptor");
+  if (out->sizes[0] < 0) return fail(NOVA_HIP_ESHAPE, "fill: negative size");
+  if (out->sizes[0] == 0) return NOVA_HIP_SUCCESS;
+  if (!out->aligned) return fail(NOVA_HIP_EINVAL, "fill: null data pointer");
+  return launch_fill(out_f32(out), out->sizes[0], out->strides[0], value, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_gelu_f32(const NovaMemRef1D *x, NovaMemRef1D *y) {
+  clear_error();
+  int32_t rc;
+  if ((rc = dense1(x, "gelu", "x")) || (rc = dense1(y, "gelu", "y"))) return rc;
+  if (x->sizes[0] != y->sizes[0]) return fail(NOVA_HIP_ESHAPE, "gelu: sizes differ");
+  return launch_gelu(in_f32(x), out_f32(y), x->sizes[0], current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_gelu_backward_f32(const NovaMemRef1D *grad_out,
+                                                const NovaMemRef1D *x, NovaMemRef1D *out) {
+  clear_error();
+  const char *w = "gelu_backward";
+  int32_t rc;
+  if ((rc = dense1(grad_out, w, "grad_out")) || (rc = dense1(x, w, "x")) ||
+      (rc = dense1(out, w, "out")))
+    return rc;
+  if (x->sizes[0] != grad_out->sizes[0] || x->sizes[0] != out->sizes[0])
+    return fail(NOVA_HIP_ESHAPE, "%s: sizes differ", w);
+  return launch_gelu_backward(in_f32(grad_out), in_f32(x), out_f32(out), x->sizes[0],
+                              current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_gather_f32(const NovaMemRef2D *table, const NovaMemRef1D *idx,
+                                         NovaMemRef2D *out, int32_t idx_dt) {
+  clear_error();
+  const char *w = "gather";
+  if (!table || !idx || !out) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  if (!index_dt_ok(idx_dt)) return fail(NOVA_HIP_EDTYPE, "%s: index dtype %d", w, idx_dt);
+  if (!nonneg_sizes(table, 2) || !nonneg_sizes(idx, 1) || !nonneg_sizes(out, 2))
+    return fail(NOVA_HIP_ESHAPE, "%s: negative size", w);
+  const int64_t n = idx->sizes[0], D = table->sizes[1];
+  if (out->sizes[0] != n || out->sizes[1] != D)
+    return fail(NOVA_HIP_ESHAPE, "%s: out is [%lld, %lld], want [%lld, %lld]", w,
+                (long long)out->sizes[0], (long long)out->sizes[1], (long long)n, (long long)D);
+  if (n == 0 || D == 0) return NOVA_HIP_SUCCESS;
+  if ((D > 1 && (table->strides[1] != 1 || out->strides[1] != 1)))
+    return fail(NOVA_HIP_ESTRIDE, "%s: rows must be contiguous", w);
+  if (!table->aligned || !idx->aligned || !out->aligned)
+    return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+  GatherProblem p;
+  p.table = in_f32(table);
+  p.idx = data_of(idx) + idx->offset * index_size(idx_dt);
+  p.out = out_f32(out);
+  p.rows = table->sizes[0];
+  p.D = D;
+  p.n = n;
+  p.st = table->strides[0];
+  p.so = out->strides[0];
+  p.sidx = idx->strides[0];
+  p.idx_dt = idx_dt;
+  return launch_gather(p, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_scatter_add_f32(NovaMemRef2D *out, const NovaMemRef1D *idx,
+                                              const NovaMemRef2D *src, int32_t idx_dt) {
+  clear_error();
+  const char *w = "scatter_add";
+  if (!out || !idx || !src) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  if (!index_dt_ok(idx_dt)) return fail(NOVA_HIP_EDTYPE, "%s: index dtype %d", w, idx_dt);
+  if (!nonneg_sizes(out, 2) || !nonneg_sizes(idx, 1) || !nonneg_sizes(src, 2))
+    return fail(NOVA_HIP_ESHAPE, "%s: negative size", w);
+  const int64_t n = idx->sizes[0], D = out->sizes[1];
+  if (src->sizes[0] != n || src->sizes[1] != D)
+    return fail(NOVA_HIP_ESHAPE, "%s: src is [%lld, %lld], want [%lld, %lld]", w,
+                (long long)src->sizes[0], (long long)src->sizes[1], (long long)n, (long long)D);
+  if (n == 0 || D == 0) return NOVA_HIP_SUCCESS;
+  if (D > 1 && (out->strides[1] != 1 || src->strides[1] != 1))
+    return fail(NOVA_HIP_ESTRIDE, "%s: rows must be contiguous", w);
+  if (!out->aligned || !idx->aligned || !src->aligned)
+    return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+  ScatterAddProblem p;
+  p.out = out_f32(out);
+  p.idx = data_of(idx) + idx->offset * index_size(idx_dt);
+  p.src = in_f32(src);
+  p.rows = out->sizes[0];
+  p.D = D;
+  p.n = n;
+  p.so = out->strides[0];
+  p.ss = src->strides[0];
+  p.sidx = idx->strides[0];
+  p.idx_dt = idx_dt;
+  return launch_scatter_add(p, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_reduce_sum_f32(const NovaMemRef3D *x, NovaMemRef2D *out) {
+  clear_error();
+  const char *w = "reduce_sum";
+  if (!x || !out) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  if (!nonneg_sizes(x, 3) || !nonneg_sizes(out, 2))
+    return fail(NOVA_HIP_ESHAPE, "%s: negative size", w);
+  if (out->sizes[0] != x->sizes[0] || out->sizes[1] != x->sizes[2])
+    return fail(NOVA_HIP_ESHAPE, "%s: out is [%lld, %lld], want [%lld, %lld]", w,
+                (long long)out->sizes[0], (long long)out->sizes[1], (long long)x->sizes[0],
+                (long long)x->sizes[2]);
+  if (x->sizes[0] * x->sizes[2] == 0) return NOVA_HIP_SUCCESS;
+  if (!x->aligned || !out->aligned) return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+  ReduceSumProblem p;
+  p.x = in_f32(x);
+  p.out = out_f32(out);
+  p.outer = x->sizes[0];
+  p.n = x->sizes[1];
+  p.inner = x->sizes[2];
+  p.so = x->strides[0];
+  p.sn = x->strides[1];
+  p.si = x->strides[2];
+  p.soo = out->strides[0];
+  p.soi = out->strides[1];
+  return launch_reduce_sum(p, current_stream());
+}
+
+int32_t _mlir_ciface_nova_hip_index_to_i32(const NovaMemRef1D *src, NovaMemRef1D *dst,
+                                           int32_t src_dt) {
+  clear_error();
+  const char *w = "index_to_i32";
+  if (!src || !dst) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", w);
+  if (!index_dt_ok(src_dt)) return fail(NOVA_HIP_EDTYPE, "%s: index dtype %d", w, src_dt);
+  int32_t rc;
+  if ((rc = dense1(dst, w, "dst"))) return rc;
+  if (src->sizes[0] != dst->sizes[0]) return fail(NOVA_HIP_ESHAPE, "%s: sizes differ", w);
+  if (src->sizes[0] == 0) return NOVA_HIP_SUCCESS;
+  if (!src->aligned) return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+  return launch_index_to_i32(data_of(src) + src->offset * index_size(src_dt), src->strides[0],
+                             src_dt,
+                             reinterpret_cast<int32_t *>(const_cast<char *>(data_of(dst))) +
+                                 dst->offset,
+                             src->sizes[0], current_stream());
+}
+
 void nova_hip_set_stream(void *stream) { t_stream = static_cast<hipStream_t>(stream); }
 
 void *nova_hip_get_stream(void) { return t_stream; }

@@ -105,6 +105,57 @@ struct ColSumProblem {
 };
 int32_t launch_col_sum(const ColSumProblem &p, hipStream_t s);
 
+// ---- program glue (glue.hip) -------------------------------------------------
+// c = a (op) b over a [4]-shaped index space; strides in elements, 0 on a
+// broadcast dimension.
+struct BinaryProblem {
+  const float *a;
+  const float *b;
+  float *c;
+  int64_t size[4];
+  int64_t sa[4], sb[4], sc[4];
+  int op;
+};
+int32_t launch_binary(const BinaryProblem &p, hipStream_t s);
+int32_t launch_fill(float *out, int64_t n, int64_t stride, float v, hipStream_t s);
+int32_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
+int32_t launch_gelu_backward(const float *go, const float *x, float *out, int64_t n,
+                             hipStream_t s);
+
+// out[i, :] = table[idx[i], :] (D columns).
+struct GatherProblem {
+  const float *table;
+  const void *idx;
+  float *out;
+  int64_t rows, D, n;    // table rows, columns, indices
+  int64_t st, so, sidx;  // row strides of table / out, index stride
+  int idx_dt;
+};
+int32_t launch_gather(const GatherProblem &p, hipStream_t s);
+
+// out[idx[i], :] += src[i, :].
+struct ScatterAddProblem {
+  float *out;
+  const void *idx;
+  const float *src;
+  int64_t rows, D, n;
+  int64_t so, ss, sidx;
+  int idx_dt;
+};
+int32_t launch_scatter_add(const ScatterAddProblem &p, hipStream_t s);
+int32_t launch_index_to_i32(const void *src, int64_t stride, int dt, int32_t *dst, int64_t n,
+                            hipStream_t s);
+
+// out[o, i] = sum_j x[o, j, i].
+struct ReduceSumProblem {
+  const float *x;
+  float *out;
+  int64_t outer, n, inner;
+  int64_t so, sn, si;  // strides of x
+  int64_t soo, soi;    // strides of out
+};
+int32_t launch_reduce_sum(const ReduceSumProblem &p, hipStream_t s);
+
 // Per-stream device workspace owned by the library.  Returns null and sets
 // the error text on failure.  The pointer stays valid until the next call
 // with a larger size on the same stream, or nova_hip_release_workspace().

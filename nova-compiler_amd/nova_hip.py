@@ -25,6 +25,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libnova_hip.so")
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
+DT_I32, DT_I64, DT_I16 = 3, 4, 5          # index / label operands of the glue ops
+BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = 0, 1, 2, 3
 EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_GELU = 0, 1, 2, 3
 
 STATUS = {
@@ -50,6 +52,14 @@ EXPORTS = (
     "_mlir_ciface_nova_hip_layer_norm_backward_f32",
     "_mlir_ciface_nova_hip_linear_backward",
     "_mlir_ciface_nova_hip_matmul_backward",
+    "_mlir_ciface_nova_hip_binary_f32",
+    "_mlir_ciface_nova_hip_fill_f32",
+    "_mlir_ciface_nova_hip_gelu_f32",
+    "_mlir_ciface_nova_hip_gelu_backward_f32",
+    "_mlir_ciface_nova_hip_gather_f32",
+    "_mlir_ciface_nova_hip_scatter_add_f32",
+    "_mlir_ciface_nova_hip_reduce_sum_f32",
+    "_mlir_ciface_nova_hip_index_to_i32",
     "nova_hip_set_stream",
     "nova_hip_get_stream",
     "nova_hip_synchronize",
@@ -80,7 +90,8 @@ def _memref_type(rank: int):
 MemRef1D = _memref_type(1)
 MemRef2D = _memref_type(2)
 MemRef3D = _memref_type(3)
-_MEMREF = {1: MemRef1D, 2: MemRef2D, 3: MemRef3D}
+MemRef4D = _memref_type(4)
+_MEMREF = {1: MemRef1D, 2: MemRef2D, 3: MemRef3D, 4: MemRef4D}
 
 
 def make_memref(ptr: int, sizes, strides, offset: int = 0):
@@ -131,6 +142,14 @@ def lib() -> ctypes.CDLL:
     L._mlir_ciface_nova_hip_layer_norm_backward_f32.argtypes = [P, P, P, P, P, P, P, P]
     L._mlir_ciface_nova_hip_linear_backward.argtypes = [P, P, P, P, P, P, ctypes.c_int32]
     L._mlir_ciface_nova_hip_matmul_backward.argtypes = [P, P, P, P, P, ctypes.c_int32]
+    L._mlir_ciface_nova_hip_binary_f32.argtypes = [P, P, P, ctypes.c_int32]
+    L._mlir_ciface_nova_hip_fill_f32.argtypes = [P, ctypes.c_float]
+    L._mlir_ciface_nova_hip_gelu_f32.argtypes = [P, P]
+    L._mlir_ciface_nova_hip_gelu_backward_f32.argtypes = [P, P, P]
+    L._mlir_ciface_nova_hip_gather_f32.argtypes = [P, P, P, ctypes.c_int32]
+    L._mlir_ciface_nova_hip_scatter_add_f32.argtypes = [P, P, P, ctypes.c_int32]
+    L._mlir_ciface_nova_hip_reduce_sum_f32.argtypes = [P, P]
+    L._mlir_ciface_nova_hip_index_to_i32.argtypes = [P, P, ctypes.c_int32]
     for name in EXPORTS:
         if name.startswith("_mlir_ciface_"):
             getattr(L, name).restype = ctypes.c_int32
@@ -368,3 +387,133 @@ def matmul_backward(grad, A, B, *, out_dtype=None, grad_a=None, grad_b=None):
     _bind_stream()
     check(lib()._mlir_ciface_nova_hip_matmul_backward(*[ref(v) for v in d], flags))
     return grad_a, grad_b
+
+
+# --------------------------------------------------------------------------
+# program glue (nova.add / mul / ..., constant, gelu, gelu_backward, gather,
+# scatter_add, reduce<sum>, label widening)
+# --------------------------------------------------------------------------
+
+def _index_dt(t) -> int:
+    torch = _torch()
+    m = {torch.int16: DT_I16, torch.int32: DT_I32, torch.int64: DT_I64}
+    if t.dtype not in m:
+        raise NovaHipError(4, f"unsupported index dtype {t.dtype}")
+    return m[t.dtype]
+
+
+def _memref4(t, shape):
+    """4-D descriptor of t broadcast (right-aligned) to `shape`: stride 0 on
+    the dims t lacks or has as 1."""
+    pad = 4 - len(shape)
+    full = (1,) * pad + tuple(shape)
+    ts = (1,) * (4 - t.dim()) + tuple(t.shape)
+    st = (0,) * (4 - t.dim()) + tuple(t.stride())
+    return make_memref(t.data_ptr(), full, [0 if ts[i] == 1 else st[i] for i in range(4)], 0)
+
+
+def binary(a, b, op: int, out=None):
+    """nova.add / sub / mul / div with numpy-style broadcasting (f32)."""
+    torch = _torch()
+    shape = torch.broadcast_shapes(a.shape, b.shape)
+    if len(shape) > 4:
+        raise NovaHipError(2, "binary: rank above 4")
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=a.device)
+    d = [_memref4(a, shape), _memref4(b, shape), _memref4(out, shape)]
+    d[2].sizes[:] = [1] * (4 - len(shape)) + list(shape)
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_binary_f32(*[ref(v) for v in d], op))
+    return out
+
+
+def fill(out, value: float):
+    """A splat nova.constant written into `out` (dense f32)."""
+    d = make_memref(out.data_ptr(), (out.numel(),), (1,), 0)
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_fill_f32(ref(d), float(value)))
+    return out
+
+
+def gelu(x, out=None):
+    """nova.gelu on its own (the reference's tanh form)."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty_like(x)
+    d = [make_memref(t.data_ptr(), (t.numel(),), (1,), 0) for t in (x, out)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_gelu_f32(*[ref(v) for v in d]))
+    return out
+
+
+def gelu_backward(grad_out, x, out=None):
+    """nova.gelu_backward(grad_out, input)."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty_like(x)
+    d = [make_memref(t.data_ptr(), (t.numel(),), (1,), 0) for t in (grad_out, x, out)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_gelu_backward_f32(*[ref(v) for v in d]))
+    return out
+
+
+def gather(table, idx, out=None):
+    """nova.gather along axis 0: table[idx] (idx of any shape; i16 / i32 /
+    i64, narrow types zero-extended)."""
+    torch = _torch()
+    flat = idx.reshape(-1)
+    if out is None:
+        out = torch.empty((flat.numel(), table.shape[1]), dtype=torch.float32,
+                          device=table.device)
+    d = [memref_of(table), memref_of(flat), memref_of(out.reshape(-1, table.shape[1]))]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_gather_f32(*[ref(v) for v in d], _index_dt(idx)))
+    return out.reshape(tuple(idx.shape) + (table.shape[1],))
+
+
+def scatter_add(base, idx, src, out=None):
+    """nova.scatter_add along axis 0: a copy of base with src[i] added into
+    row idx[i] (f32 atomics; in place when out is base)."""
+    if out is None:
+        out = base.clone()
+    elif out.data_ptr() != base.data_ptr():
+        out.copy_(base)
+    flat = idx.reshape(-1)
+    d = [memref_of(out), memref_of(flat), memref_of(src.reshape(flat.numel(), -1))]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_scatter_add_f32(*[ref(v) for v in d], _index_dt(idx)))
+    return out
+
+
+def reduce_sum(x, dim: int, out=None):
+    """nova.reduce<sum> over one dimension (keepdims false)."""
+    torch = _torch()
+    dim = dim % x.dim()
+    outer = 1
+    for s in x.shape[:dim]:
+        outer *= s
+    inner = 1
+    for s in x.shape[dim + 1:]:
+        inner *= s
+    rshape = tuple(x.shape[:dim]) + tuple(x.shape[dim + 1:])
+    if out is None:
+        out = torch.empty(rshape, dtype=torch.float32, device=x.device)
+    xc = x.contiguous()
+    dx = make_memref(xc.data_ptr(), (outer, x.shape[dim], inner),
+                     (x.shape[dim] * inner, inner, 1), 0)
+    do = make_memref(out.data_ptr(), (outer, inner), (inner, 1), 0)
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_reduce_sum_f32(ref(dx), ref(do)))
+    return out
+
+
+def index_to_i32(idx, out=None):
+    """Labels / indices widened (narrow: zero-extended) or truncated to i32."""
+    torch = _torch()
+    flat = idx.reshape(-1)
+    if out is None:
+        out = torch.empty(flat.numel(), dtype=torch.int32, device=idx.device)
+    d = [memref_of(flat), memref_of(out)]
+    _bind_stream()
+    check(lib()._mlir_ciface_nova_hip_index_to_i32(*[ref(v) for v in d], _index_dt(idx)))
+    return out.reshape(idx.shape)

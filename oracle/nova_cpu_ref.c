@@ -448,3 +448,114 @@ int nova_ref_col_sum(const void *in, int dt, int64_t rows, int64_t cols,
     for (int64_t c = 0; c < cols; ++c) out[c] = load_as_f32(in, dt, r * ld + c) + out[c];
   return 0;
 }
+
+/* ==== Program glue: the ops a whole training step needs around the hot
+ *      ops (the reference's GPT step ltest/test.mlir uses each one).  ==== */
+
+/* Index element: narrow integers zero-extended (arith.extui,
+ * NovaToLinalgGeneric.cpp:2434-2449 for gather, NovaToLinalg.cpp:1240-1244
+ * for scatter_add), i32 / i64 as signed indices.
+ * idx_dt: 3 = i32, 4 = i64, 5 = i16. */
+static int64_t load_index(const void *idx, int dt, int64_t i) {
+  if (dt == 5) return (int64_t)((const uint16_t *)idx)[i];
+  if (dt == 3) return (int64_t)((const int32_t *)idx)[i];
+  return ((const int64_t *)idx)[i];
+}
+
+/* nova.add / sub / mul / div (Nova_BinaryOp, NovaOps.td:600-700): one
+ * IEEE f32 operation per element over operands already broadcast to the
+ * result shape (dense, n elements).  op: 0 add, 1 sub, 2 mul, 3 div. */
+int nova_ref_binary_f32(const float *a, const float *b, float *c, int64_t n, int op) {
+  if (!a || !b || !c || n < 0 || op < 0 || op > 3) return -1;
+  for (int64_t i = 0; i < n; ++i) {
+    const float x = a[i], y = b[i];
+    c[i] = op == 0 ? x + y : op == 1 ? x - y : op == 2 ? x * y : x / y;
+  }
+  return 0;
+}
+
+/* nova.gelu_backward (NovaGeluBackwardPattern, NovaToLinalgGeneric.cpp:
+ * 1339-1425), the generic body of :1383-1420 in its operation order:
+ * x2 = x*x; x3 = x2*x; cubic = 0.044715*x3; inner = x + cubic;
+ * gx = 0.797884583*inner; poly = 1 + x2*0.134145; dgx = poly*0.797884583;
+ * t = tanh(gx); term1 = 0.5*(1 + t); term2 = 0.5*(x*(dgx*(1 - t*t)));
+ * result = grad_out * (term1 + term2). */
+float nova_ref_gelu_backward_f32(float go, float x) {
+  const float k = 0.797884583f;
+  float x2 = x * x;
+  float x3 = x2 * x;
+  float cubic = 4.471500e-02f * x3;
+  float inner = x + cubic;
+  float gx = k * inner;
+  float xsq_c = x2 * 0.134145f;
+  float poly = 1.0f + xsq_c;
+  float dgx = poly * k;
+  float t = tanhf(gx);
+  float t2 = t * t;
+  float one_pt = 1.0f + t;
+  float term1 = 0.5f * one_pt;
+  float om = 1.0f - t2;
+  float t2a = dgx * om;
+  float t2b = x * t2a;
+  float term2 = 0.5f * t2b;
+  float dg = term1 + term2;
+  return go * dg;
+}
+
+void nova_ref_gelu_backward_array(const float *go, const float *x, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = nova_ref_gelu_backward_f32(go[i], x[i]);
+}
+
+/* nova.gather along axis 0 (NovaGatherOpLowering, NovaToLinalgGeneric.cpp:
+ * 2372-2471): out[i, :] = table[idx[i], :].  The reference's tensor.extract
+ * of an index outside [0, V) is undefined; this restatement (and the GPU
+ * kernel) gives a NaN row. */
+int nova_ref_gather_f32(const float *table, int64_t V, int64_t D, const void *idx, int idx_dt,
+                        int64_t n, float *out) {
+  if (!table || !idx || !out || V < 0 || D < 0 || n < 0) return -1;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t r = load_index(idx, idx_dt, i);
+    for (int64_t c = 0; c < D; ++c)
+      out[i * D + c] = (r >= 0 && r < V) ? table[r * D + c] : NAN;
+  }
+  return 0;
+}
+
+/* nova.scatter_add along axis 0 (NovaScatterAddOpLowering, NovaToLinalg.cpp:
+ * 1086-1290), in place on out (the op's input): out[idx[i], :] += src[i, :]
+ * for i ascending (the CPU pipeline runs the forall sequentially); indices
+ * outside [0, V) are skipped (the scf.if of :1262-1276). */
+int nova_ref_scatter_add_f32(float *out, int64_t V, int64_t D, const void *idx, int idx_dt,
+                             int64_t n, const float *src) {
+  if (!out || !idx || !src || V < 0 || D < 0 || n < 0) return -1;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t r = load_index(idx, idx_dt, i);
+    if (r < 0 || r >= V) continue;
+    for (int64_t c = 0; c < D; ++c) out[r * D + c] = out[r * D + c] + src[i * D + c];
+  }
+  return 0;
+}
+
+/* nova.reduce<sum> over one dimension (Nova_ReduceOp, NovaOps.td:191-230):
+ * x as [outer, n, inner], out[o, i] = sum_j x[o, j, i], j ascending from
+ * 0.0f (a sequential linalg.reduce on the CPU pipeline). */
+int nova_ref_reduce_sum_f32(const float *x, int64_t outer, int64_t n, int64_t inner,
+                            float *out) {
+  if (!x || !out || outer < 0 || n < 0 || inner < 0) return -1;
+  for (int64_t o = 0; o < outer; ++o)
+    for (int64_t i = 0; i < inner; ++i) {
+      float acc = 0.0f;
+      for (int64_t j = 0; j < n; ++j) acc = acc + x[(o * n + j) * inner + i];
+      out[o * inner + i] = acc;
+    }
+  return 0;
+}
+
+/* Labels / indices to i32: zero-extension of narrow integers (the label
+ * widening of NovaSceForwardLowering, NovaToLinalgGeneric.cpp:801-1010),
+ * truncation of i64. */
+int nova_ref_index_to_i32(const void *idx, int idx_dt, int64_t n, int32_t *out) {
+  if (!idx || !out || n < 0) return -1;
+  for (int64_t i = 0; i < n; ++i) out[i] = (int32_t)load_index(idx, idx_dt, i);
+  return 0;
+}

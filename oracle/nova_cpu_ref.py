@@ -56,6 +56,19 @@ def lib() -> ctypes.CDLL:
         L.nova_ref_bf16_to_f32.restype = ctypes.c_float
         L.nova_ref_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.nova_ref_f16_to_f32.restype = ctypes.c_float
+        L.nova_ref_binary_f32.argtypes = [P, P, P, I64, I]
+        L.nova_ref_binary_f32.restype = I
+        L.nova_ref_gelu_backward_f32.argtypes = [ctypes.c_float, ctypes.c_float]
+        L.nova_ref_gelu_backward_f32.restype = ctypes.c_float
+        L.nova_ref_gelu_backward_array.argtypes = [P, P, P, I64]
+        L.nova_ref_gather_f32.argtypes = [P, I64, I64, P, I, I64, P]
+        L.nova_ref_gather_f32.restype = I
+        L.nova_ref_scatter_add_f32.argtypes = [P, I64, I64, P, I, I64, P]
+        L.nova_ref_scatter_add_f32.restype = I
+        L.nova_ref_reduce_sum_f32.argtypes = [P, I64, I64, I64, P]
+        L.nova_ref_reduce_sum_f32.restype = I
+        L.nova_ref_index_to_i32.argtypes = [P, I, I64, P]
+        L.nova_ref_index_to_i32.restype = I
         _lib = L
     return _lib
 
@@ -218,3 +231,72 @@ def matmul_backward(grad, A, B, *, dt=None):
     """nova.matmul_backward (rank 2): returns (grad_a = grad . B^T,
     grad_b = A^T . grad) in f32."""
     return gemm(grad, B.T, adt=dt, bdt=dt)[0], gemm(A.T, grad, adt=dt, bdt=dt)[0]
+
+
+# ---- program glue ----------------------------------------------------------
+I32, I64, I16 = 3, 4, 5
+ADD, SUB, MUL, DIV = 0, 1, 2, 3
+
+
+def _idx(idx: np.ndarray):
+    idx = np.ascontiguousarray(idx.reshape(-1))
+    m = {np.dtype(np.int16): I16, np.dtype(np.uint16): I16, np.dtype(np.int32): I32,
+         np.dtype(np.int64): I64}
+    return idx, m[idx.dtype]
+
+
+def binary(a: np.ndarray, b: np.ndarray, op: int) -> np.ndarray:
+    """nova.add / sub / mul / div with numpy-style broadcasting (f32)."""
+    shape = np.broadcast_shapes(a.shape, b.shape)
+    A = np.ascontiguousarray(np.broadcast_to(a.astype(np.float32, copy=False), shape))
+    B = np.ascontiguousarray(np.broadcast_to(b.astype(np.float32, copy=False), shape))
+    C = np.empty(shape, np.float32)
+    assert lib().nova_ref_binary_f32(A.ctypes.data, B.ctypes.data, C.ctypes.data, C.size, op) == 0
+    return C
+
+
+def gelu_backward(grad_out: np.ndarray, x: np.ndarray) -> np.ndarray:
+    go = np.ascontiguousarray(grad_out, np.float32)
+    xx = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(xx)
+    lib().nova_ref_gelu_backward_array(go.ctypes.data, xx.ctypes.data, out.ctypes.data, xx.size)
+    return out
+
+
+def gather(table: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """nova.gather along axis 0 (NaN rows for indices outside the table)."""
+    t = np.ascontiguousarray(table, np.float32)
+    flat, dt = _idx(idx)
+    out = np.empty((flat.size, t.shape[1]), np.float32)
+    assert lib().nova_ref_gather_f32(t.ctypes.data, t.shape[0], t.shape[1], flat.ctypes.data, dt,
+                                     flat.size, out.ctypes.data) == 0
+    return out.reshape(tuple(idx.shape) + (t.shape[1],))
+
+
+def scatter_add(base: np.ndarray, idx: np.ndarray, src: np.ndarray) -> np.ndarray:
+    """nova.scatter_add along axis 0: base with src rows added in order."""
+    out = np.array(base, np.float32, copy=True, order="C")
+    flat, dt = _idx(idx)
+    s = np.ascontiguousarray(src.reshape(flat.size, -1), np.float32)
+    assert lib().nova_ref_scatter_add_f32(out.ctypes.data, out.shape[0], out.shape[1],
+                                          flat.ctypes.data, dt, flat.size, s.ctypes.data) == 0
+    return out
+
+
+def reduce_sum(x: np.ndarray, dim: int) -> np.ndarray:
+    """nova.reduce<sum> over one dimension, sequential."""
+    x = np.ascontiguousarray(x, np.float32)
+    dim = dim % x.ndim
+    outer = int(np.prod(x.shape[:dim], dtype=np.int64))
+    inner = int(np.prod(x.shape[dim + 1:], dtype=np.int64))
+    out = np.empty(x.shape[:dim] + x.shape[dim + 1:], np.float32)
+    assert lib().nova_ref_reduce_sum_f32(x.ctypes.data, outer, x.shape[dim], inner,
+                                         out.ctypes.data) == 0
+    return out
+
+
+def index_to_i32(idx: np.ndarray) -> np.ndarray:
+    flat, dt = _idx(idx)
+    out = np.empty(flat.size, np.int32)
+    assert lib().nova_ref_index_to_i32(flat.ctypes.data, dt, flat.size, out.ctypes.data) == 0
+    return out.reshape(idx.shape)
