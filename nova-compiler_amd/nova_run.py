@@ -20,7 +20,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libnova_run.so")
-NP_DTYPE = {0: np.float32, 1: np.uint16, 2: np.uint16, 3: np.int32, 4: np.int64}
+NP_DTYPE = {0: np.float32, 1: np.uint16, 2: np.uint16, 3: np.int32, 4: np.int64, 5: np.int16}
 DT_NAME = {0: "f32", 1: "bf16", 2: "f16", 3: "i32", 4: "i64"}
 
 _lib = None

@@ -26,6 +26,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <set>
@@ -47,12 +48,13 @@ int32_t fail(int32_t code, const char *fmt, ...) {
   return code;
 }
 
-enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_I32 = 3, DT_I64 = 4 };
+enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_I32 = 3, DT_I64 = 4, DT_I16 = 5 };
 const char *dt_name(int dt) {
-  static const char *n[] = {"f32", "bf16", "f16", "i32", "i64"};
-  return dt >= 0 && dt <= 4 ? n[dt] : "?";
+  static const char *n[] = {"f32", "bf16", "f16", "i32", "i64", "i16"};
+  return dt >= 0 && dt <= 5 ? n[dt] : "?";
 }
 int dt_size(int dt) { return dt == DT_F32 || dt == DT_I32 ? 4 : dt == DT_I64 ? 8 : 2; }
+bool is_index_dt(int dt) { return dt == DT_I32 || dt == DT_I64 || dt == DT_I16; }
 
 struct Type {
   std::vector<int64_t> shape;
@@ -166,6 +168,7 @@ bool parse_type(const std::string &s_in, Type &t) {
     else if (el == "f16") t.dt = DT_F16;
     else if (el == "i32") t.dt = DT_I32;
     else if (el == "i64") t.dt = DT_I64;
+    else if (el == "i16") t.dt = DT_I16;
     else return false;
     return true;
   }
@@ -328,18 +331,48 @@ int32_t parse_op(const std::string &stmt, int line, Op &op) {
       return fail(NOVA_HIP_EINVAL, "line %d: %s has no type list", line, op.name.c_str());
     std::string head = body.substr(0, colon), tail = body.substr(colon + 1);
     parse_attr_dict(head, op.attrs);
-    // keyword attributes of nova.transpose: `axes1 = -1 axes2 = -2`
-    // (written before any attr-dict)
-    for (const char *kw : {"axes1", "axes2"}) {
+    // keyword attributes written before any attr-dict: nova.transpose's
+    // `axes1 = -1 axes2 = -2`, nova.scatter_add's `axis = 0`, nova.reduce's
+    // `dimension = [0] keepdims = true`
+    for (const char *kw : {"axes1", "axes2", "axis", "keepdims", "dimension"}) {
       const size_t lb0 = head.find('{');
-      const size_t k = head.find(kw);
+      size_t k = head.find(kw);
+      while (k != std::string::npos && k > 0 && (isalnum((unsigned char)head[k - 1]) || head[k - 1] == '_'))
+        k = head.find(kw, k + 1);
       if (k == std::string::npos || (lb0 != std::string::npos && k > lb0)) continue;
       const size_t eqk = head.find('=', k);
       if (eqk == std::string::npos) continue;
-      op.attrs[kw] = std::to_string(strtol(head.c_str() + eqk + 1, nullptr, 10));
+      std::string v = trim(head.substr(eqk + 1));
+      if (!v.empty() && v[0] == '[') {
+        v = v.substr(0, match_close(v, 0) + 1);
+      } else {
+        size_t e = 0;
+        while (e < v.size() && (isalnum((unsigned char)v[e]) || v[e] == '-' || v[e] == '_')) ++e;
+        v = v.substr(0, e);
+      }
+      if (strcmp(kw, "axes1") == 0 || strcmp(kw, "axes2") == 0)
+        v = std::to_string(strtol(v.c_str(), nullptr, 10));
+      op.attrs[kw] = v;
     }
     const size_t lb = head.find('{');
-    op.operands = operand_names(lb == std::string::npos ? head : head.substr(0, lb));
+    std::string opnd = lb == std::string::npos ? head : head.substr(0, lb);
+    // the keyword part is not an operand list
+    for (const char *kw : {" dimension", " keepdims", " ignore_nan", " axis"}) {
+      const size_t k = opnd.find(kw);
+      if (k != std::string::npos) opnd = opnd.substr(0, k);
+    }
+    if (op.name == "nova.gather") {
+      // `%table [%indices]`
+      const size_t lsq = opnd.find('[');
+      const size_t rsq = lsq == std::string::npos ? lsq : match_close(opnd, lsq);
+      if (rsq == std::string::npos)
+        return fail(NOVA_HIP_EINVAL, "line %d: nova.gather needs `%%table [%%indices]`", line);
+      op.operands = operand_names(opnd.substr(0, lsq));
+      for (const std::string &n : operand_names(opnd.substr(lsq + 1, rsq - lsq - 1)))
+        op.operands.push_back(n);
+    } else {
+      op.operands = operand_names(opnd);
+    }
     const size_t arrow = find_top(tail, '-');
     std::string res_t;
     if (arrow != std::string::npos && arrow + 1 < tail.size() && tail[arrow + 1] == '>') {
@@ -358,6 +391,11 @@ int32_t parse_op(const std::string &stmt, int line, Op &op) {
       if (!parse_type(res_t, t)) return fail(NOVA_HIP_EINVAL, "line %d: bad result type", line);
       op.result_types.push_back(t);
     }
+    if (op.name == "nova.constant" && op.operands.empty() && op.operand_types.size() == 1 &&
+        op.result_types.empty()) {
+      op.result_types = op.operand_types;  // `nova.constant {value = ...} : type`
+      op.operand_types.clear();
+    }
     if (op.operand_types.size() != op.operands.size())
       return fail(NOVA_HIP_EINVAL, "line %d: %s lists %zu operands and %zu types", line,
                   op.name.c_str(), op.operands.size(), op.operand_types.size());
@@ -365,6 +403,25 @@ int32_t parse_op(const std::string &stmt, int line, Op &op) {
   }
   return fail(NOVA_HIP_EINVAL, "line %d: op '%s' is not part of this path's op surface", line,
               op.name.c_str());
+}
+
+// Reduced dims of a nova.reduce (`dimension = [..]`, all dims when absent),
+// normalised to [0, rank).
+std::vector<int> reduce_dims(const Op &op, int rank) {
+  std::vector<int> dims;
+  auto it = op.attrs.find("dimension");
+  if (it == op.attrs.end()) {
+    for (int i = 0; i < rank; ++i) dims.push_back(i);
+    return dims;
+  }
+  std::string v = it->second;
+  if (!v.empty() && v[0] == '[') v = v.substr(1, v.size() - 2);
+  for (const std::string &t : split_top(v, ',')) {
+    int d = atoi(t.c_str());
+    if (d < 0) d += rank;
+    dims.push_back(d);
+  }
+  return dims;
 }
 
 // ---- result type inference (the reference's inferReturnTypes) -------------------
@@ -440,6 +497,52 @@ int32_t infer(Op &op) {
   } else if (op.name == "nova.matmul_backward") {
     if ((rc = need(3))) return rc;
     R = {T[1], T[2]};
+  } else if (op.name == "nova.add" || op.name == "nova.sub" || op.name == "nova.mul" ||
+             op.name == "nova.div") {
+    // numpy-style broadcasting (Nova_BinaryOp, NovaOps.td:600-700)
+    if ((rc = need(2))) return rc;
+    const std::vector<int64_t> &a = T[0].shape, &b = T[1].shape;
+    Type r;
+    r.dt = T[0].dt;
+    const size_t n = std::max(a.size(), b.size());
+    r.shape.assign(n, 1);
+    for (size_t i = 0; i < n; ++i) {
+      const int64_t x = i < n - a.size() ? 1 : a[i - (n - a.size())];
+      const int64_t y = i < n - b.size() ? 1 : b[i - (n - b.size())];
+      if (x != y && x != 1 && y != 1)
+        return fail(NOVA_HIP_ESHAPE, "line %d: %s shapes do not broadcast", op.line,
+                    op.name.c_str());
+      r.shape[i] = x == 1 ? y : x;
+    }
+    R.push_back(r);
+  } else if (op.name == "nova.gelu_backward") {
+    if ((rc = need(2))) return rc;
+    R.push_back(T[1]);
+  } else if (op.name == "nova.gather") {
+    if ((rc = need(2))) return rc;
+    Type r;
+    r.dt = T[0].dt;
+    r.shape = T[1].shape;
+    for (size_t i = 1; i < T[0].shape.size(); ++i) r.shape.push_back(T[0].shape[i]);
+    R.push_back(r);
+  } else if (op.name == "nova.scatter_add") {
+    if ((rc = need(3))) return rc;
+    R.push_back(T[0]);
+  } else if (op.name.compare(0, 11, "nova.reduce") == 0) {
+    if ((rc = need(1))) return rc;
+    std::vector<int> dims = reduce_dims(op, (int)T[0].shape.size());
+    const bool keep = op.attrs.count("keepdims") && op.attrs.at("keepdims") == "true";
+    Type r;
+    r.dt = T[0].dt;
+    for (int i = 0; i < (int)T[0].shape.size(); ++i) {
+      bool red = false;
+      for (int d : dims) red = red || d == i;
+      if (!red) r.shape.push_back(T[0].shape[i]);
+      else if (keep) r.shape.push_back(1);
+    }
+    R.push_back(r);
+  } else if (op.name == "nova.reshape" || op.name == "nova.constant") {
+    return fail(NOVA_HIP_EINVAL, "line %d: %s needs its result type", op.line, op.name.c_str());
   } else if (op.name.compare(0, 5, "nova.") == 0) {
     return fail(NOVA_HIP_EINVAL, "line %d: op '%s' is not part of this path's op surface",
                 op.line, op.name.c_str());
@@ -544,12 +647,22 @@ struct Buffer {
 };
 
 struct Step {
-  std::string kind;  // gemm, layer_norm, sce, sce_bwd, ln_bwd, lin_bwd, mm_bwd, zero, copy
+  // gemm, layer_norm, sce, sce_bwd, ln_bwd, lin_bwd, mm_bwd, zero, copy, view,
+  // fill, binary, gelu, gelu_bwd, gather, scatter, reduce_sum, idx32
+  std::string kind;
   std::vector<View> in, out;
-  int epi = NOVA_HIP_EPI_NONE;
+  int epi = NOVA_HIP_EPI_NONE;  // GEMM epilogue; binary op code; index dtype
   int out_dt = DT_F32;
   std::string text;
+  float value = 0.0f;           // fill value
+  int64_t dims[3] = {0, 0, 0};  // reduce_sum: outer, reduced, inner
 };
+
+int64_t numel_of(const std::vector<int64_t> &shape) {
+  int64_t n = 1;
+  for (int64_t d : shape) n *= d;
+  return n;
+}
 
 std::vector<int64_t> dense_strides(const std::vector<int64_t> &shape) {
   std::vector<int64_t> st(shape.size(), 1);
@@ -618,6 +731,31 @@ struct Planner {
                   "line %d: %s of %s must be stored f32 (a cast from %s is folded only into GEMM "
                   "operands)",
                   op.line, what, op.name.c_str(), dt_name(v.dt));
+    return NOVA_HIP_SUCCESS;
+  }
+  int32_t need_dense_f32(const Op &op, const View &v, const char *what) {
+    int32_t rc = need_f32(op, v, what);
+    if (rc) return rc;
+    if (!is_dense(v))
+      return fail(NOVA_HIP_ESTRIDE, "line %d: %s of %s is a transposed view (not on this path)",
+                  op.line, what, op.name.c_str());
+    return NOVA_HIP_SUCCESS;
+  }
+  // Labels / indices as i32: non-i32 index types get a widening step (the
+  // reference zero-extends narrow label types, NovaToLinalgGeneric.cpp:801-1010).
+  int32_t as_i32(const Op &op, View &t) {
+    if (t.dt == DT_I32) return NOVA_HIP_SUCCESS;
+    if (!is_index_dt(t.dt) || !is_dense(t))
+      return fail(NOVA_HIP_EDTYPE, "line %d: %s targets must be an integer tensor", op.line,
+                  op.name.c_str());
+    Step s;
+    s.kind = "idx32";
+    s.in = {t};
+    s.out = {fresh(Type{t.shape, DT_I32, false})};
+    s.text = std::string(dt_name(t.dt)) + " labels -> _mlir_ciface_nova_hip_index_to_i32(" +
+             view_str(t) + ") -> " + view_str(s.out[0]);
+    plan.steps.push_back(s);
+    t = s.out[0];
     return NOVA_HIP_SUCCESS;
   }
   // The single consumer of `name` if it has exactly one use, else null.
@@ -761,10 +899,165 @@ struct Planner {
         out.dt = op.result_types[0].dt;
         if ((rc = emit_gemm(op, k, x, w, &bias, out, folded))) return rc;
       } else if (n == "nova.gelu") {
-        return fail(NOVA_HIP_EINVAL,
-                    "line %d: nova.gelu outside a GEMM epilogue is not on this path (it folds only "
-                    "into the nova.linear / matmul it follows)",
-                    op.line);
+        // not folded: its input has other uses (e.g. a gelu_backward)
+        View x;
+        if ((rc = get(op, 0, x)) || (rc = need_dense_f32(op, x, "input"))) return rc;
+        Step s;
+        s.kind = "gelu";
+        s.in = {x};
+        s.out = {fresh(op.result_types[0])};
+        s.text = "nova.gelu -> _mlir_ciface_nova_hip_gelu_f32(" + view_str(x) + ") -> " +
+                 view_str(s.out[0]);
+        env[op.results[0]] = s.out[0];
+        plan.steps.push_back(s);
+      } else if (n == "nova.gelu_backward") {
+        View go, x;
+        if ((rc = get(op, 0, go)) || (rc = get(op, 1, x)) ||
+            (rc = need_dense_f32(op, go, "grad_out")) || (rc = need_dense_f32(op, x, "input")))
+          return rc;
+        if (numel_of(go.shape) != numel_of(x.shape))
+          return fail(NOVA_HIP_ESHAPE, "line %d: nova.gelu_backward operand sizes differ", op.line);
+        Step s;
+        s.kind = "gelu_bwd";
+        s.in = {go, x};
+        s.out = {fresh(op.result_types[0])};
+        s.text = "nova.gelu_backward -> _mlir_ciface_nova_hip_gelu_backward_f32(" + view_str(go) +
+                 ", " + view_str(x) + ") -> " + view_str(s.out[0]);
+        env[op.results[0]] = s.out[0];
+        plan.steps.push_back(s);
+      } else if (n == "nova.add" || n == "nova.sub" || n == "nova.mul" || n == "nova.div") {
+        View a, b;
+        if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = need_dense_f32(op, a, "lhs")) ||
+            (rc = need_dense_f32(op, b, "rhs")))
+          return rc;
+        if (op.result_types[0].shape.size() > 4)
+          return fail(NOVA_HIP_ESHAPE, "line %d: %s above rank 4", op.line, n.c_str());
+        Step s;
+        s.kind = "binary";
+        s.epi = n == "nova.add" ? NOVA_HIP_BIN_ADD : n == "nova.sub" ? NOVA_HIP_BIN_SUB
+              : n == "nova.mul" ? NOVA_HIP_BIN_MUL : NOVA_HIP_BIN_DIV;
+        s.in = {a, b};
+        s.out = {fresh(op.result_types[0])};
+        s.text = n + " -> _mlir_ciface_nova_hip_binary_f32(" + view_str(a) + ", " + view_str(b) +
+                 ") -> " + view_str(s.out[0]);
+        env[op.results[0]] = s.out[0];
+        plan.steps.push_back(s);
+      } else if (n == "nova.constant") {
+        const std::string v = op.attrs.count("value") ? op.attrs.at("value") : "";
+        const Type &t = op.result_types[0];
+        if (v.compare(0, 6, "dense<") != 0 || v.find('[') != std::string::npos)
+          return fail(NOVA_HIP_EINVAL,
+                      "line %d: nova.constant other than a splat dense<value> is not on this path",
+                      op.line);
+        if (t.dt != DT_F32)
+          return fail(NOVA_HIP_EDTYPE, "line %d: nova.constant of %s is not on this path", op.line,
+                      dt_name(t.dt));
+        Step s;
+        s.kind = "fill";
+        s.out = {fresh(t)};
+        s.value = strtof(v.c_str() + 6, nullptr);
+        char buf[64];
+        snprintf(buf, sizeof(buf), "%g", (double)s.value);
+        s.text = std::string("nova.constant splat ") + buf + " -> _mlir_ciface_nova_hip_fill_f32(" +
+                 view_str(s.out[0]) + ")";
+        env[op.results[0]] = s.out[0];
+        plan.steps.push_back(s);
+      } else if (n == "nova.reshape") {
+        View v;
+        if ((rc = get(op, 0, v))) return rc;
+        const Type &t = op.result_types[0];
+        if (!is_dense(v) || v.dt != v.logical)
+          return fail(NOVA_HIP_ESTRIDE,
+                      "line %d: nova.reshape of a view (transpose / folded cast) is not on this path",
+                      op.line);
+        if (numel_of(t.shape) != numel_of(v.shape))
+          return fail(NOVA_HIP_ESHAPE, "line %d: nova.reshape changes the element count", op.line);
+        v.shape = t.shape;
+        v.strides = dense_strides(t.shape);
+        v.producer = -1;
+        env[op.results[0]] = v;
+        plan.steps.push_back(Step{"view", {}, {}, 0, 0, "nova.reshape -> view " + view_str(v)});
+      } else if (n == "nova.gather") {
+        View t, idx;
+        if ((rc = get(op, 0, t)) || (rc = get(op, 1, idx)) || (rc = need_dense_f32(op, t, "input")))
+          return rc;
+        if ((op.attrs.count("axis") && atoi(op.attrs.at("axis").c_str()) != 0) || t.shape.size() != 2)
+          return fail(NOVA_HIP_EINVAL, "line %d: nova.gather of a 2-D table along axis 0 only",
+                      op.line);
+        if (!is_index_dt(idx.dt) || !is_dense(idx))
+          return fail(NOVA_HIP_EDTYPE, "line %d: nova.gather indices must be i16 / i32 / i64",
+                      op.line);
+        Step s;
+        s.kind = "gather";
+        s.epi = idx.dt;
+        s.in = {t, idx};
+        s.out = {fresh(op.result_types[0])};
+        s.text = "nova.gather -> _mlir_ciface_nova_hip_gather_f32(" + view_str(t) + ", " +
+                 view_str(idx) + ") -> " + view_str(s.out[0]);
+        env[op.results[0]] = s.out[0];
+        plan.steps.push_back(s);
+      } else if (n == "nova.scatter_add") {
+        View base, idx, src;
+        if ((rc = get(op, 0, base)) || (rc = get(op, 1, idx)) || (rc = get(op, 2, src)) ||
+            (rc = need_dense_f32(op, base, "input")) || (rc = need_dense_f32(op, src, "src")))
+          return rc;
+        if ((op.attrs.count("axis") && atoi(op.attrs.at("axis").c_str()) != 0) ||
+            base.shape.size() != 2)
+          return fail(NOVA_HIP_EINVAL, "line %d: nova.scatter_add into a 2-D input along axis 0 only",
+                      op.line);
+        if (!is_index_dt(idx.dt) || !is_dense(idx))
+          return fail(NOVA_HIP_EDTYPE, "line %d: nova.scatter_add indices must be i16 / i32 / i64",
+                      op.line);
+        if (numel_of(src.shape) != numel_of(idx.shape) * base.shape[1])
+          return fail(NOVA_HIP_ESHAPE, "line %d: nova.scatter_add src is not [indices, %lld]",
+                      op.line, (long long)base.shape[1]);
+        // the op's result is a new tensor: the input copied, then the adds
+        View out = fresh(op.result_types[0]);
+        Step c;
+        c.kind = "copy";
+        c.in = {base};
+        c.out = {out};
+        c.text = "nova.scatter_add input -> hipMemcpyAsync(" + view_str(out) + " <- " +
+                 view_str(base) + ")";
+        plan.steps.push_back(c);
+        Step s;
+        s.kind = "scatter";
+        s.epi = idx.dt;
+        s.in = {idx, src};
+        s.out = {out};
+        s.text = "nova.scatter_add -> _mlir_ciface_nova_hip_scatter_add_f32(" + view_str(out) +
+                 ", " + view_str(idx) + ", " + view_str(src) + ")";
+        env[op.results[0]] = out;
+        plan.steps.push_back(s);
+      } else if (n.compare(0, 11, "nova.reduce") == 0) {
+        View x;
+        if ((rc = get(op, 0, x)) || (rc = need_dense_f32(op, x, "input"))) return rc;
+        if (n != "nova.reduce<sum>")
+          return fail(NOVA_HIP_EINVAL, "line %d: %s: only the sum reduction is on this path",
+                      op.line, n.c_str());
+        if (op.attrs.count("ignore_nan") && op.attrs.at("ignore_nan") == "true")
+          return fail(NOVA_HIP_EINVAL, "line %d: nova.reduce ignore_nan is not on this path",
+                      op.line);
+        std::vector<int> dims = reduce_dims(op, (int)x.shape.size());
+        std::sort(dims.begin(), dims.end());
+        for (size_t i = 1; i < dims.size(); ++i)
+          if (dims[i] != dims[i - 1] + 1)
+            return fail(NOVA_HIP_EINVAL, "line %d: nova.reduce over non-adjacent dims", op.line);
+        if (dims.empty() || dims[0] < 0 || dims.back() >= (int)x.shape.size())
+          return fail(NOVA_HIP_EINVAL, "line %d: bad nova.reduce dimension", op.line);
+        Step s;
+        s.kind = "reduce_sum";
+        s.dims[0] = numel_of(std::vector<int64_t>(x.shape.begin(), x.shape.begin() + dims[0]));
+        s.dims[1] = numel_of(std::vector<int64_t>(x.shape.begin() + dims[0],
+                                                  x.shape.begin() + dims.back() + 1));
+        s.dims[2] = numel_of(std::vector<int64_t>(x.shape.begin() + dims.back() + 1, x.shape.end()));
+        s.in = {x};
+        s.out = {fresh(op.result_types[0])};
+        s.text = "nova.reduce<sum> -> _mlir_ciface_nova_hip_reduce_sum_f32(" + view_str(x) +
+                 " as [" + std::to_string(s.dims[0]) + "," + std::to_string(s.dims[1]) + "," +
+                 std::to_string(s.dims[2]) + "]) -> " + view_str(s.out[0]);
+        env[op.results[0]] = s.out[0];
+        plan.steps.push_back(s);
       } else if (n == "nova.transpose") {
         View v;
         if ((rc = get(op, 0, v))) return rc;
@@ -811,8 +1104,7 @@ struct Planner {
       } else if (n == "nova.sce") {
         View x, t;
         if ((rc = get(op, 0, x)) || (rc = get(op, 1, t))) return rc;
-        if ((rc = need_f32(op, x, "logits"))) return rc;
-        if (t.dt != DT_I32) return fail(NOVA_HIP_EDTYPE, "line %d: nova.sce targets must be i32", op.line);
+        if ((rc = need_f32(op, x, "logits")) || (rc = as_i32(op, t))) return rc;
         Step s;
         s.kind = "sce";
         s.in = {x, t};
@@ -829,9 +1121,7 @@ struct Planner {
       } else if (n == "nova.sce_backward") {
         View sm, t;
         if ((rc = get(op, 0, sm)) || (rc = get(op, 1, t))) return rc;
-        if ((rc = need_f32(op, sm, "softmax"))) return rc;
-        if (t.dt != DT_I32)
-          return fail(NOVA_HIP_EDTYPE, "line %d: nova.sce_backward targets must be i32", op.line);
+        if ((rc = need_f32(op, sm, "softmax")) || (rc = as_i32(op, t))) return rc;
         if (op.attrs.count("dim")) {
           const int d = atoi(op.attrs.at("dim").c_str());
           if (d != -1 && d != (int)sm.shape.size() - 1)
@@ -885,13 +1175,15 @@ struct Planner {
         if (src.shape != dst.shape || !is_dense(src) || src.dt != dst.dt)
           return fail(NOVA_HIP_ESHAPE, "line %d: materialize_in_destination of a %s value into %s",
                       op.line, view_str(src).c_str(), view_str(dst).c_str());
-        Step s;
-        s.kind = "copy";
-        s.in = {src};
-        s.out = {dst};
-        s.text = "materialize_in_destination -> hipMemcpyAsync(" + view_str(dst) + " <- " +
-                 view_str(src) + ")";
-        plan.steps.push_back(s);
+        if (src.buf != dst.buf) {
+          Step s;
+          s.kind = "copy";
+          s.in = {src};
+          s.out = {dst};
+          s.text = "materialize_in_destination -> hipMemcpyAsync(" + view_str(dst) + " <- " +
+                   view_str(src) + ")";
+          plan.steps.push_back(s);
+        }
         plan.out_args.push_back(plan.bufs[dst.buf].arg);
       } else {
         return fail(NOVA_HIP_EINVAL, "line %d: op '%s' is not part of this path's op surface",
@@ -1031,6 +1323,82 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
         reinterpret_cast<const NovaMemRef2D *>(&go), reinterpret_cast<const NovaMemRef2D *>(&x),
         reinterpret_cast<const NovaMemRef2D *>(&w), reinterpret_cast<NovaMemRef2D *>(&o0),
         reinterpret_cast<NovaMemRef2D *>(&o1), reinterpret_cast<NovaMemRef1D *>(&o2), flags);
+  }
+  auto flat1 = [&](const View &v) {
+    Desc<1> d;
+    d.allocated = d.aligned = ptr[v.buf];
+    d.offset = 0;
+    d.sizes[0] = numel_of(v.shape);
+    d.strides[0] = 1;
+    return d;
+  };
+  if (s.kind == "fill") {
+    Desc<1> o = flat1(s.out[0]);
+    return _mlir_ciface_nova_hip_fill_f32(reinterpret_cast<NovaMemRef1D *>(&o), s.value);
+  }
+  if (s.kind == "binary") {
+    Desc<4> a = desc<4>(s.in[0], ptr), b = desc<4>(s.in[1], ptr), c = desc<4>(s.out[0], ptr);
+    return _mlir_ciface_nova_hip_binary_f32(reinterpret_cast<const NovaMemRef4D *>(&a),
+                                            reinterpret_cast<const NovaMemRef4D *>(&b),
+                                            reinterpret_cast<NovaMemRef4D *>(&c), s.epi);
+  }
+  if (s.kind == "gelu") {
+    Desc<1> x = flat1(s.in[0]), y = flat1(s.out[0]);
+    return _mlir_ciface_nova_hip_gelu_f32(reinterpret_cast<const NovaMemRef1D *>(&x),
+                                          reinterpret_cast<NovaMemRef1D *>(&y));
+  }
+  if (s.kind == "gelu_bwd") {
+    Desc<1> go = flat1(s.in[0]), x = flat1(s.in[1]), o = flat1(s.out[0]);
+    return _mlir_ciface_nova_hip_gelu_backward_f32(reinterpret_cast<const NovaMemRef1D *>(&go),
+                                                   reinterpret_cast<const NovaMemRef1D *>(&x),
+                                                   reinterpret_cast<NovaMemRef1D *>(&o));
+  }
+  if (s.kind == "gather") {
+    Desc<2> t = desc<2>(s.in[0], ptr), o = desc<2>(s.out[0], ptr);
+    Desc<1> i = flat1(s.in[1]);
+    return _mlir_ciface_nova_hip_gather_f32(reinterpret_cast<const NovaMemRef2D *>(&t),
+                                            reinterpret_cast<const NovaMemRef1D *>(&i),
+                                            reinterpret_cast<NovaMemRef2D *>(&o), s.epi);
+  }
+  if (s.kind == "scatter") {
+    Desc<2> o = desc<2>(s.out[0], ptr);
+    Desc<1> i = flat1(s.in[0]);
+    Desc<2> src;
+    src.allocated = src.aligned = ptr[s.in[1].buf];
+    src.offset = 0;
+    src.sizes[0] = numel_of(s.in[0].shape);
+    src.sizes[1] = s.out[0].shape[1];
+    src.strides[0] = src.sizes[1];
+    src.strides[1] = 1;
+    return _mlir_ciface_nova_hip_scatter_add_f32(reinterpret_cast<NovaMemRef2D *>(&o),
+                                                 reinterpret_cast<const NovaMemRef1D *>(&i),
+                                                 reinterpret_cast<const NovaMemRef2D *>(&src),
+                                                 s.epi);
+  }
+  if (s.kind == "reduce_sum") {
+    Desc<3> x;
+    x.allocated = x.aligned = ptr[s.in[0].buf];
+    x.offset = 0;
+    x.sizes[0] = s.dims[0];
+    x.sizes[1] = s.dims[1];
+    x.sizes[2] = s.dims[2];
+    x.strides[0] = s.dims[1] * s.dims[2];
+    x.strides[1] = s.dims[2];
+    x.strides[2] = 1;
+    Desc<2> o;
+    o.allocated = o.aligned = ptr[s.out[0].buf];
+    o.offset = 0;
+    o.sizes[0] = s.dims[0];
+    o.sizes[1] = s.dims[2];
+    o.strides[0] = s.dims[2];
+    o.strides[1] = 1;
+    return _mlir_ciface_nova_hip_reduce_sum_f32(reinterpret_cast<const NovaMemRef3D *>(&x),
+                                                reinterpret_cast<NovaMemRef2D *>(&o));
+  }
+  if (s.kind == "idx32") {
+    Desc<1> src = flat1(s.in[0]), dst = flat1(s.out[0]);
+    return _mlir_ciface_nova_hip_index_to_i32(reinterpret_cast<const NovaMemRef1D *>(&src),
+                                              reinterpret_cast<NovaMemRef1D *>(&dst), s.in[0].dt);
   }
   return fail(NOVA_HIP_EINVAL, "internal: unknown step %s", s.kind.c_str());
 }

@@ -115,3 +115,60 @@ def test_nova_run_cli(cuda):
                         "--reps", "2"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     assert "_mlir_ciface_nova_hip_gemm" in r.stdout and "ms per run" in r.stdout
+
+
+def gpt_step_oracle(tok, tgt, pos, wte, wpe, g1, be1, w1, c1, w2, c2, g2, be2, wlm):
+    """The GPT step composed from the oracle's ops, in the program's order."""
+    B, T = tok.shape
+    V, D = wte.shape
+    N = B * T
+    h = ref.binary(ref.gather(wte, tok), ref.gather(wpe, pos), ref.ADD).reshape(N, D)
+    y1, S1, r1 = ref.layer_norm(h, g1, be1)
+    up = ref.gemm(y1, w1, bias=c1, epilogue=ref.EPI_BIAS)[0]
+    act = ref.gelu(up)
+    dn = ref.gemm(act, w2, bias=c2, epilogue=ref.EPI_BIAS)[0]
+    r = ref.binary(h, dn, ref.ADD)
+    y2, S2, r2 = ref.layer_norm(r, g2, be2)
+    logits = ref.gemm(y2, wlm)[0]
+    t32 = ref.index_to_i32(tgt).reshape(-1)
+    sm, loss, _ = ref.sce(logits, t32, softmax=True)
+    dl = ref.binary(ref.sce_backward(sm, t32), np.ones(1, np.float32), ref.MUL)
+    dflat = ref.gemm(dl, np.ascontiguousarray(wlm.T))[0]
+    dwlm = ref.gemm(np.ascontiguousarray(y2.T), dl)[0]
+    gr = ref.layer_norm_backward(dflat, r, g2, S2, r2)
+    gd = ref.linear_backward(gr[0], act, w2)
+    dup = ref.gelu_backward(gd[0], up)
+    gu = ref.linear_backward(dup, y1, w1)
+    gh = ref.layer_norm_backward(gu[0], h, g1, S1, r1)
+    dh = ref.binary(gr[0], gh[0], ref.ADD)
+    dwpe = ref.scatter_add(np.zeros((T, D), np.float32), pos.reshape(-1),
+                           ref.reduce_sum(dh.reshape(B, T, D), 0))
+    dwte = ref.scatter_add(np.zeros((V, D), np.float32), tok.reshape(-1), dh)
+    return [loss, dwte, dwpe, gh[1], gh[2], gu[1], gu[2], gd[1], gd[2], gr[1], gr[2], dwlm]
+
+
+def test_gpt_step_program_end_to_end(cuda):
+    """A whole GPT training step (embeddings, LayerNorm, MLP with GELU,
+    residual, LM head, SCE loss and the full backward to the embedding
+    gradients) through libnova_run, against the oracle's ops composed in the
+    same order."""
+    from gpt_program import gpt_step
+    B, T, V, D, H = 2, 16, 96, 64, 128
+    r = np.random.default_rng(79)
+    f = lambda *s, k=0.1: (r.standard_normal(s) * k).astype(np.float32)  # noqa: E731
+    tok = r.integers(0, V, (B, T)).astype(np.int16)
+    tgt = r.integers(0, V, (B, T)).astype(np.int16)
+    pos = np.arange(T, dtype=np.int64).reshape(1, T)
+    args = [tok, tgt, pos, f(V, D, k=0.5), f(T, D, k=0.5), 1 + f(D), f(D), f(D, H), f(H),
+            f(H, D), f(D), 1 + f(D), f(D), f(D, V)]
+    got = nova_run.Program(gpt_step(B, T, V, D, H)).run("gpt_step", *args)
+    want = gpt_step_oracle(*args)
+    names = ["loss", "dwte", "dwpe", "dgamma1", "dbeta1", "dw1", "db1", "dw2", "db2",
+             "dgamma2", "dbeta2", "dwlm"]
+    assert len(got) == len(want)
+    for g, w, n in zip(got, want, names):
+        assert g.shape == w.shape, n
+        assert_close_f32(g, w, "gpt_step " + n)
+    # rows of the embedding no token hits get no gradient
+    unused = np.setdiff1d(np.arange(V), tok.reshape(-1))
+    assert (got[1][unused] == 0).all()

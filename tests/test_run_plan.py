@@ -76,8 +76,8 @@ def test_ops_outside_the_path_are_refused():
       %g = nova.gelu %x : tensor<4x8xf32>
       return %g : tensor<4x8xf32>
     }""")
-    with pytest.raises(nova_run.NovaRunError, match="outside a GEMM epilogue"):
-        p.plan("g")
+    # a nova.gelu that cannot fold into a GEMM epilogue is its own kernel
+    assert "nova.gelu -> _mlir_ciface_nova_hip_gelu_f32" in p.plan("g")
     p = nova_run.Program("""func.func @c(%x: tensor<4x8xf32>) -> tensor<4x8xbf16> {
       %c = nova.cast %x : tensor<4x8xf32> -> tensor<4x8xbf16>
       return %c : tensor<4x8xbf16>
@@ -108,3 +108,39 @@ def test_library_exports_every_declared_symbol():
     L = nova_run.lib()
     for n in names:
         assert hasattr(L, n), n
+
+
+def test_gpt_step_plans_every_op():
+    from gpt_program import gpt_step
+    p = nova_run.Program(gpt_step(2, 8, 64, 32, 64))
+    plan = p.plan("gpt_step")
+    for want in ("nova.gather -> _mlir_ciface_nova_hip_gather_f32",
+                 "nova.add -> _mlir_ciface_nova_hip_binary_f32",
+                 "nova.gelu -> _mlir_ciface_nova_hip_gelu_f32",
+                 "i16 labels -> _mlir_ciface_nova_hip_index_to_i32",
+                 "nova.constant splat 1 -> _mlir_ciface_nova_hip_fill_f32",
+                 "nova.mul -> _mlir_ciface_nova_hip_binary_f32",
+                 "nova.gelu_backward -> _mlir_ciface_nova_hip_gelu_backward_f32",
+                 "nova.reduce<sum> -> _mlir_ciface_nova_hip_reduce_sum_f32(b50[2,8,32]f32 as [1,2,256])",
+                 "nova.scatter_add -> _mlir_ciface_nova_hip_scatter_add_f32",
+                 "nova.reshape -> view b0[16]i16"):
+        assert want in plan, want
+    # the linear whose output feeds gelu and gelu_backward keeps its own GELU
+    assert "epilogue=bias+gelu" not in plan
+    assert plan.count("_mlir_ciface_nova_hip_gemm") == 5
+    assert p.args("gpt_step")[0] == (5, (2, 8))
+    assert p.results("gpt_step")[0] == (0, (1,)) and p.results("gpt_step")[1] == (0, (64, 32))
+
+
+@pytest.mark.parametrize("body,msg", [
+    ("%r = nova.reduce<max> %x dimension = [0] : tensor<4x8xf32>", "only the sum reduction"),
+    ("%r = nova.constant {value = dense<[1.0, 2.0]> : tensor<2xf32>} : tensor<2xf32>", "splat"),
+    ("%r = nova.gather %x [%i] {axis = 1} : tensor<4x8xf32>, tensor<3xi32> -> tensor<4x3xf32>",
+     "axis 0 only"),
+])
+def test_glue_forms_outside_the_path_are_refused(body, msg):
+    text = ("func.func @f(%x: tensor<4x8xf32>, %i: tensor<3xi32>) -> tensor<4x8xf32> {\n  "
+            + body + "\n  return %x : tensor<4x8xf32>\n}\n")
+    p = nova_run.Program(text)
+    with pytest.raises(nova_run.NovaRunError, match=msg):
+        p.plan("f")
