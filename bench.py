@@ -53,7 +53,7 @@ def parse():
                     help="skip the CPU oracle timing (cpu_baseline becomes null)")
     ap.add_argument("--only", default="",
                     help="comma list of configs to run (c2,c3,c4,ln,sce,sce_bwd,sce_fwd_bwd,ln_bwd,"
-                         "c3_bwd,c2_vendor; copy = HBM copy calibration)")
+                         "c3_bwd,c2_vendor,gpt_step; copy = HBM copy calibration)")
     return ap.parse_args()
 
 
@@ -349,6 +349,42 @@ def bench_copy(args, torch):
     return {"ms": ms, "bytes": 2 * n * 4, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
 
 
+def bench_gpt_step(args):
+    """A whole GPT training step (the reference GPT step's shapes: batch 8,
+    1024 tokens, vocab 50304, width 384, MLP 1536; forward, SCE loss and the
+    full backward to the embedding gradients) through libnova_run, from host
+    arrays to host arrays: wall time per nova_run_execute, which includes
+    the device allocations and the host<->device copies of its ~0.25 GB of
+    arguments and results.  Weights random (N(0, 0.02)), so the loss is near
+    ln(vocab)."""
+    import numpy as np
+    import nova_run
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from gpt_program import gpt_step
+    B, T, V, D, H = 8, 1024, 50304, 384, 1536
+    r = np.random.default_rng(6)
+
+    def f(*s, k=0.02):
+        return r.standard_normal(s, dtype=np.float32) * np.float32(k)
+
+    inp = [r.integers(0, V, (B, T)).astype(np.int16), r.integers(0, V, (B, T)).astype(np.int16),
+           np.arange(T, dtype=np.int64).reshape(1, T), f(V, D), f(T, D), 1 + f(D), f(D), f(D, H),
+           f(H), f(H, D), f(D), 1 + f(D), f(D), f(D, V)]
+    p = nova_run.Program(gpt_step(B, T, V, D, H))
+    launches = p.plan("gpt_step").count("_mlir_ciface_")
+    out = p.run("gpt_step", *inp)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        out = p.run("gpt_step", *inp)
+        times.append((time.perf_counter() - t0) * 1e3)
+    return {"ms_wall_median": sorted(times)[1], "ms_wall": times, "launches": launches,
+            "loss": float(out[0][0]), "ln_vocab": float(np.log(V)),
+            "finite": bool(all(np.isfinite(o).all() for o in out)),
+            "note": "wall time per nova_run_execute incl. device allocation and host<->device "
+                    "copies; f32 program (the reference GPT step's dtype)"}
+
+
 def cpu_baseline(S):
     """The CPU oracle (restatement of Nova's single-threaded CPU pipeline)
     on a bounded slab of config 2: batch 0, the first R rows, all 4096
@@ -404,7 +440,7 @@ def main():
     nh.lib()
     only = (set(args.only.split(",")) if args.only else
             {"c2", "c3", "c4", "ln", "sce", "sce_bwd", "sce_fwd_bwd", "ln_bwd", "c3_bwd",
-             "c2_vendor"})
+             "c2_vendor", "gpt_step"})
     cfg = {}
 
     def stage(name, f):
@@ -440,6 +476,8 @@ def main():
             "ln_bwd", lambda: bench_ln_bwd(args, torch, nh, S))
     if "c3_bwd" in only:
         cfg["c3_linear_backward_bf16_f32"] = stage("c3_bwd", lambda: bench_c3_bwd(args, torch, nh, S))
+    if "gpt_step" in only:
+        cfg["gpt_step_f32_nova_run_8x1024_v50304"] = stage("gpt_step", lambda: bench_gpt_step(args))
     if "c2_vendor" in only:
         cfg["c2_vendor_hipblaslt_reference"] = stage("c2_vendor", lambda: bench_c2_vendor(args, torch, S))
     if "copy" in only:  # calibration only; not part of the default run
