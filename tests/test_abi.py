@@ -265,3 +265,40 @@ def test_matmul_backward_validation():
     assert f(g, A, B, flags=nh.gemm_flags(nh.DT_F32, nh.DT_BF16)) == 4
     assert f(g, A, B, flags=nh.gemm_flags(nh.DT_F32, nh.DT_F32, nh.EPI_GELU)) == 1
     assert f(g, A, B, ga=d2((8, 31))) == 2
+
+
+def d4(sizes, strides=None, ptr=FAKE):
+    if strides is None:
+        strides = (sizes[1] * sizes[2] * sizes[3], sizes[2] * sizes[3], sizes[3], 1)
+    return nh.make_memref(ptr, sizes, strides)
+
+
+def test_glue_entry_points_validate_before_any_hip_call():
+    L = nh.lib()
+    r = nh.ref
+    # binary: shapes that do not broadcast, unknown op, null data, empty no-op
+    assert L._mlir_ciface_nova_hip_binary_f32(r(d4((1, 2, 3, 4))), r(d4((1, 2, 5, 4))),
+                                              r(d4((1, 2, 3, 4))), nh.BIN_ADD) == 2
+    assert "broadcast" in last_error()
+    assert L._mlir_ciface_nova_hip_binary_f32(r(d4((1, 2, 3, 4))), r(d4((1, 1, 1, 4))),
+                                              r(d4((1, 2, 3, 4))), 9) == 1
+    assert L._mlir_ciface_nova_hip_binary_f32(r(d4((1, 2, 3, 4), ptr=0)), r(d4((1, 1, 1, 4))),
+                                              r(d4((1, 2, 3, 4))), nh.BIN_MUL) == 1
+    assert L._mlir_ciface_nova_hip_binary_f32(r(d4((1, 0, 3, 4))), r(d4((1, 1, 3, 4))),
+                                              r(d4((1, 0, 3, 4))), nh.BIN_MUL) == 0
+    # fill / gelu / gelu_backward / index_to_i32
+    assert L._mlir_ciface_nova_hip_fill_f32(r(d1(-1)), 1.0) == 2
+    assert L._mlir_ciface_nova_hip_gelu_f32(r(d1(8)), r(d1(9))) == 2
+    assert L._mlir_ciface_nova_hip_gelu_backward_f32(r(d1(8)), r(d1(8, stride=2)), r(d1(8))) == 3
+    assert L._mlir_ciface_nova_hip_index_to_i32(r(d1(8)), r(d1(8)), 7) == 4
+    # gather / scatter_add: index dtype, shapes, row strides
+    assert L._mlir_ciface_nova_hip_gather_f32(r(d2((10, 4))), r(d1(3)), r(d2((3, 4))), 2) == 4
+    assert L._mlir_ciface_nova_hip_gather_f32(r(d2((10, 4))), r(d1(3)), r(d2((3, 5))),
+                                              nh.DT_I64) == 2
+    assert L._mlir_ciface_nova_hip_gather_f32(r(d2((10, 4), (8, 2))), r(d1(3)),
+                                              r(d2((3, 4))), nh.DT_I16) == 3
+    assert L._mlir_ciface_nova_hip_scatter_add_f32(r(d2((10, 4))), r(d1(3)), r(d2((2, 4))),
+                                                   nh.DT_I32) == 2
+    # reduce_sum: out must be [outer, inner]
+    assert L._mlir_ciface_nova_hip_reduce_sum_f32(r(d3((2, 5, 7))), r(d2((2, 5)))) == 2
+    assert L._mlir_ciface_nova_hip_reduce_sum_f32(r(d3((0, 5, 7))), r(d2((0, 7)))) == 0
