@@ -244,21 +244,52 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
     const float gs = wave_sum(ls);
     const float safe = fmaxf(gs, 1.0e-7f);
     const float lse = logf(safe);
-    if (a.softmax) {
-      float *sr = a.softmax + (int64_t)row * a.ssm;
-      for (int c = lane; c < a.C; c += 64) sr[c] = exp_shifted(xr[c], gm) / safe;
-    }
-    if (a.grad) {
-      const int t = a.labels[row];
-      const bool bad = t < 0 || t >= a.C;
-      float *gr = a.grad + (int64_t)row * a.sg;
-      for (int c = lane; c < a.C; c += 64)
-        gr[c] = sce_grad(exp_shifted(xr[c], gm) / safe, c == t, bad, a.invN);
-    }
+    // Second pass for the softmax / gradient outputs: the row is read again,
+    // in the first pass's form (U float4s per lane in flight, 16-byte
+    // stores; the launcher picks VEC only with aligned outputs).
+    const int t = a.labels[row];
+    const bool bad = t < 0 || t >= a.C;
+    auto out_pass = [&](float *orow, bool grad) __attribute__((always_inline)) {
+      auto val = [&](float x, int c) __attribute__((always_inline)) {
+        const float sm = exp_shifted(x, gm) / safe;
+        return grad ? sce_grad(sm, c == t, bad, a.invN) : sm;
+      };
+      int c0 = 0;
+      if constexpr (VEC) {
+        const f32x4 *x4 = reinterpret_cast<const f32x4 *>(xr);
+        f32x4 *o4 = reinterpret_cast<f32x4 *>(orow);
+        const int n4 = a.C >> 2;
+        constexpr int U = 8;
+        int base = 0;
+        for (; base + 64 * U <= n4; base += 64 * U) {
+          f32x4 v[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(x4 + base + lane + 64 * u);
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int c = base + lane + 64 * u;
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = val(v[u][e], 4 * c + e);
+            __builtin_nontemporal_store(o, o4 + c);
+          }
+        }
+        for (int c = base + lane; c < n4; c += 64) {
+          const f32x4 v = x4[c];
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = val(v[e], 4 * c + e);
+          o4[c] = o;
+        }
+        c0 = n4 << 2;
+      }
+      for (int c = c0 + lane; c < a.C; c += 64) orow[c] = val(xr[c], c);
+    };
+    if (a.softmax) out_pass(a.softmax + (int64_t)row * a.ssm, false);
+    if (a.grad) out_pass(a.grad + (int64_t)row * a.sg, true);
     if (lane == 0) {
-      const int t = a.labels[row];
       float lr;
-      if (t < 0 || t >= a.C) {
+      if (bad) {
         lr = __builtin_nanf("");
       } else {
         const float shifted = xr[t] - gm;
