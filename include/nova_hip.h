@@ -327,7 +327,9 @@ int32_t _mlir_ciface_nova_hip_gather_f32(const NovaMemRef2D *table, const NovaMe
  * reference's memref.atomic_rmw addf; indices outside [0, V) are skipped as
  * its bounds check does.  The order of adds into one row is not fixed.
  *   out : [V, D] f32 (holds the op's `input` on entry); idx : [n] as for
- *   gather; src : [n, D] f32. */
+ *   gather; src : [n, D] f32.  out must be device memory from hipMalloc
+ *   (coarse-grained): the hardware f32 atomics are not defined on
+ *   fine-grained host memory. */
 int32_t _mlir_ciface_nova_hip_scatter_add_f32(NovaMemRef2D *out, const NovaMemRef1D *idx,
                                               const NovaMemRef2D *src, int32_t idx_dt);
 /* nova.reduce<sum> over one dimension (Nova_ReduceOp, NovaOps.td:191-230):

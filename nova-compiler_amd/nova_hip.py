@@ -421,7 +421,6 @@ def binary(a, b, op: int, out=None):
     if out is None:
         out = torch.empty(shape, dtype=torch.float32, device=a.device)
     d = [_memref4(a, shape), _memref4(b, shape), _memref4(out, shape)]
-    d[2].sizes[:] = [1] * (4 - len(shape)) + list(shape)
     _bind_stream()
     check(lib()._mlir_ciface_nova_hip_binary_f32(*[ref(v) for v in d], op))
     return out
