@@ -56,8 +56,11 @@ __device__ __forceinline__ float gelu_ref(float x) {
 
 __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
 #pragma clang fp contract(off)
-  __shared__ float sa[kKs][kT + 4];
-  __shared__ float sb[kKs][kT + 4];
+  // Two LDS stages: stage s + 1's global loads are in registers while
+  // stage s is multiplied, then written to the other buffer (one barrier
+  // per stage).
+  __shared__ float sa[2][kKs][kT + 4];
+  __shared__ float sb[2][kKs][kT + 4];
 
   const int tiles = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x / tiles;
@@ -73,6 +76,43 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
   const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
   const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
 
+  // 64x16 A tile and 16x64 B tile, 4 elements of each per thread, the
+  // lanes along each operand's unit-stride dimension (coalesced loads).
+  const bool a_kc = a.sak == 1, b_nc = a.sbn == 1;
+  auto a_elem = [&](int e, int &r, int &kk) __attribute__((always_inline)) {
+    const int q = tid + e * 256;
+    if (a_kc) { kk = q & 15; r = q >> 4; } else { r = q & 63; kk = q >> 6; }
+  };
+  auto b_elem = [&](int e, int &c, int &kk) __attribute__((always_inline)) {
+    const int q = tid + e * 256;
+    if (b_nc) { c = q & 63; kk = q >> 6; } else { kk = q & 15; c = q >> 4; }
+  };
+  float ra[4], rb[4];
+  auto load = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int r, kk;
+      a_elem(e, r, kk);
+      const int gm = m0 + r, gk = k0 + kk;
+      ra[e] = (gm < a.M && gk < a.K) ? Ab[(int64_t)gm * a.sam + (int64_t)gk * a.sak] : 0.0f;
+      int c, kb;
+      b_elem(e, c, kb);
+      const int gn = n0 + c, gkb = k0 + kb;
+      rb[e] = (gn < a.N && gkb < a.K) ? Bb[(int64_t)gkb * a.sbk + (int64_t)gn * a.sbn] : 0.0f;
+    }
+  };
+  auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int r, kk;
+      a_elem(e, r, kk);
+      sa[buf][kk][r] = ra[e];
+      int c, kb;
+      b_elem(e, c, kb);
+      sb[buf][kb][c] = rb[e];
+    }
+  };
+
   float acc[4][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -82,26 +122,22 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
     for (int i = 0; i < 4; ++i) acc[i][j] = init;
   }
 
+  load(0);
+  store(0);
+  __syncthreads();
+  int buf = 0;
   for (int k0 = 0; k0 < a.K; k0 += kKs) {
-    // 64x16 A tile and 16x64 B tile, 4 elements of each per thread.
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int q = tid + e * 256;
-      const int r = q & 63, kk = q >> 6;   // A: row r, k kk
-      const int gm = m0 + r, gk = k0 + kk;
-      sa[kk][r] = (gm < a.M && gk < a.K) ? Ab[(int64_t)gm * a.sam + (int64_t)gk * a.sak] : 0.0f;
-      const int c = q & 63, kb = q >> 6;   // B: k kb, column c
-      const int gn = n0 + c, gkb = k0 + kb;
-      sb[kb][c] = (gn < a.N && gkb < a.K) ? Bb[(int64_t)gkb * a.sbk + (int64_t)gn * a.sbn] : 0.0f;
-    }
-    __syncthreads();
+    const bool more = k0 + kKs < a.K;
+    if (more) load(k0 + kKs);
+    // Only the stage's real k: a padded k would add 0 * b, which turns a
+    // -0 accumulator into +0 and an infinite b into NaN.
     const int kend = min(kKs, a.K - k0);
     for (int kk = 0; kk < kend; ++kk) {
       float av[4], bv[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = sa[kk][ty * 4 + i];
+      for (int i = 0; i < 4; ++i) av[i] = sa[buf][kk][ty * 4 + i];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = sb[kk][tx * 4 + j];
+      for (int j = 0; j < 4; ++j) bv[j] = sb[buf][kk][tx * 4 + j];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -110,7 +146,9 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
           acc[i][j] = acc[i][j] + p;
         }
     }
+    if (more) store(buf ^ 1);
     __syncthreads();
+    buf ^= 1;
   }
 
   float *Cb = a.C + (int64_t)b * a.scb;
