@@ -67,6 +67,23 @@ __global__ __launch_bounds__(kThreads) void binary_scalar_kernel(const f32x4 *v,
   }
 }
 
+// One operand repeating over leading dims (the [B,T,D] + [1,T,D] add of a
+// position embedding): the dense operand v with n4 float4s, the repeating
+// one r with period p4 float4s, v-side op order kept by SWAP.
+template <int OP, bool SWAP>
+__global__ __launch_bounds__(kThreads) void binary_periodic_kernel(const f32x4 *v, const f32x4 *r,
+                                                                   f32x4 *c, int64_t n4,
+                                                                   int64_t p4) {
+  for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n4;
+       i += (int64_t)gridDim.x * kThreads) {
+    const f32x4 x = __builtin_nontemporal_load(v + i), y = r[i % p4];
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = SWAP ? apply(y[e], x[e], OP) : apply(x[e], y[e], OP);
+    __builtin_nontemporal_store(o, c + i);
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void binary_strided_kernel(BinaryProblem p) {
   const int64_t n = p.size[0] * p.size[1] * p.size[2] * p.size[3];
   for (int64_t i = blockIdx.x * (int64_t)kThreads + threadIdx.x; i < n;
@@ -93,6 +110,22 @@ bool dense4(const int64_t *size, const int64_t *st) {
   return true;
 }
 
+// Operand strides that repeat a dense block over the leading dims: 0 on
+// dims d < k, dense (c's own strides) on d >= k, for some k.  The period in
+// elements, or 0 if the strides are not of that form.
+int64_t period_of(const int64_t *size, const int64_t *st) {
+  int64_t want = 1;
+  int d = 3;
+  for (; d >= 0; --d) {
+    if (size[d] == 1) continue;
+    if (st[d] != want) break;
+    want *= size[d];
+  }
+  for (; d >= 0; --d)
+    if (size[d] != 1 && st[d] != 0) return 0;
+  return want;
+}
+
 bool all_zero(const int64_t *size, const int64_t *st) {
   for (int d = 0; d < 4; ++d)
     if (size[d] != 1 && st[d] != 0) return false;
@@ -117,6 +150,16 @@ void launch_binary_op(const BinaryProblem &p, int64_t n, hipStream_t s) {
     hipLaunchKernelGGL((binary_scalar_kernel<OP, false>), dim3(g), dim3(kThreads), 0, s,
                        reinterpret_cast<const f32x4 *>(p.b), p.a, reinterpret_cast<f32x4 *>(p.c),
                        n / 4);
+  } else if (dc && da && aligned16(p.b) && period_of(p.size, p.sb) % 4 == 0 &&
+             period_of(p.size, p.sb) > 0) {
+    hipLaunchKernelGGL((binary_periodic_kernel<OP, false>), dim3(g), dim3(kThreads), 0, s,
+                       reinterpret_cast<const f32x4 *>(p.a), reinterpret_cast<const f32x4 *>(p.b),
+                       reinterpret_cast<f32x4 *>(p.c), n / 4, period_of(p.size, p.sb) / 4);
+  } else if (dc && db && aligned16(p.a) && period_of(p.size, p.sa) % 4 == 0 &&
+             period_of(p.size, p.sa) > 0) {
+    hipLaunchKernelGGL((binary_periodic_kernel<OP, true>), dim3(g), dim3(kThreads), 0, s,
+                       reinterpret_cast<const f32x4 *>(p.b), reinterpret_cast<const f32x4 *>(p.a),
+                       reinterpret_cast<f32x4 *>(p.c), n / 4, period_of(p.size, p.sa) / 4);
   } else {
     hipLaunchKernelGGL(binary_strided_kernel, dim3(blocks_for(n, kThreads * 4, 16384)),
                        dim3(kThreads), 0, s, p);
