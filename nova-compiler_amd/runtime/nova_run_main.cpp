@@ -5,8 +5,9 @@
 // --plan prints each function's launch plan (no GPU needed).  Otherwise the
 // function's arguments are filled from a counter-based generator
 // (splitmix64 of seed and element index: floats uniform in [-1, 1) rounded
-// to the argument's dtype, i32 arguments uniform in [0, C) with C the last
-// dim of the first rank-2 float argument), the function runs --reps times,
+// to the argument's dtype, integer arguments (i16 / i32 / i64) uniform in
+// [0, C) with C the smallest dim of the rank-2 float arguments, at most
+// 65536), the function runs --reps times,
 // and each result's sum and max |x| are printed with the time per run
 // (host<->device copies included).
 #include <hip/hip_runtime.h>
@@ -47,8 +48,10 @@ float from_bits(int dt, const void *p, int64_t i) {
   }
   if (dt == 2) return (float)((const _Float16 *)p)[i];
   if (dt == 3) return (float)((const int32_t *)p)[i];
+  if (dt == 5) return (float)((const uint16_t *)p)[i];
   return (float)((const int64_t *)p)[i];
 }
+// dtype codes: 0 f32, 1 bf16, 2 f16, 3 i32, 4 i64, 5 i16
 int esize(int dt) { return dt == 0 || dt == 3 ? 4 : dt == 4 ? 8 : 2; }
 }  // namespace
 
@@ -100,12 +103,17 @@ int main(int argc, char **argv) {
     std::vector<std::vector<char>> args(na), res(nr);
     std::vector<const void *> pa(na);
     std::vector<void *> pr(nr);
-    int64_t classes = 2;
+    // Integer arguments (labels, gather / scatter indices) stay below the
+    // smallest dim of every rank-2 float argument, so they are in range for
+    // any table or class dimension of the program.
+    int64_t classes = 65536;
     for (int a = 0; a < na; ++a) {
       int32_t dt, rank;
       int64_t shape[8];
       nova_run_arg_info(p, name, a, &dt, &rank, shape);
-      if (rank == 2 && dt <= 2 && classes == 2) classes = shape[1];
+      if (rank == 2 && dt <= 2)
+        for (int d = 0; d < 2; ++d)
+          if (shape[d] > 0 && shape[d] < classes) classes = shape[d];
     }
     for (int a = 0; a < na; ++a) {
       int32_t dt, rank;
@@ -120,6 +128,7 @@ int main(int argc, char **argv) {
         else if (dt == 1) ((uint16_t *)args[a].data())[i] = to_bf16(u);
         else if (dt == 2) ((_Float16 *)args[a].data())[i] = (_Float16)u;
         else if (dt == 3) ((int32_t *)args[a].data())[i] = (int32_t)(r % (uint64_t)classes);
+        else if (dt == 5) ((uint16_t *)args[a].data())[i] = (uint16_t)(r % (uint64_t)classes);
         else ((int64_t *)args[a].data())[i] = (int64_t)(r % (uint64_t)classes);
       }
       pa[a] = args[a].data();

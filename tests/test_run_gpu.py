@@ -172,3 +172,15 @@ def test_gpt_step_program_end_to_end(cuda):
     # rows of the embedding no token hits get no gradient
     unused = np.setdiff1d(np.arange(V), tok.reshape(-1))
     assert (got[1][unused] == 0).all()
+
+
+def test_nova_run_cli_gpt_step_with_i16_arguments(cuda, tmp_path):
+    """The CLI fills i16 token / label and i64 position arguments with
+    in-range indices and runs a whole GPT step."""
+    from gpt_program import gpt_step
+    f = tmp_path / "gpt.mlir"
+    f.write_text(gpt_step(2, 8, 64, 32, 64))
+    exe = os.path.join(PKG, "nova-run")
+    r = subprocess.run([exe, str(f), "--reps", "2"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "ms per run" in r.stdout and "nan" not in r.stdout.lower()
