@@ -354,9 +354,9 @@ def bench_gpt_step(args):
     1024 tokens, vocab 50304, width 384, MLP 1536; forward, SCE loss and the
     full backward to the embedding gradients) through libnova_run, from host
     arrays to host arrays: wall time per nova_run_execute, which includes
-    the device allocations and the host<->device copies of its ~0.25 GB of
-    arguments and results.  Weights random (N(0, 0.02)), so the loss is near
-    ln(vocab)."""
+    the host<->device copies of its ~0.25 GB of arguments and results (the
+    device buffers are allocated by the first, untimed execution and reused).
+    Weights random (N(0, 0.02)), so the loss is near ln(vocab)."""
     import numpy as np
     import nova_run
     sys.path.insert(0, os.path.join(REPO, "tests"))
@@ -381,8 +381,9 @@ def bench_gpt_step(args):
     return {"ms_wall_median": sorted(times)[1], "ms_wall": times, "launches": launches,
             "loss": float(out[0][0]), "ln_vocab": float(np.log(V)),
             "finite": bool(all(np.isfinite(o).all() for o in out)),
-            "note": "wall time per nova_run_execute incl. device allocation and host<->device "
-                    "copies; f32 program (the reference GPT step's dtype)"}
+            "note": "wall time per nova_run_execute incl. host<->device copies (device "
+                    "buffers reused from the first, untimed execution); f32 program (the "
+                    "reference GPT step's dtype)"}
 
 
 def cpu_baseline(S):

@@ -56,7 +56,10 @@ int32_t nova_run_plan(const NovaRunProgram *p, const char *func, char *buf, size
 
 /* Run `func`: host_args[i] points to argument i's dense row-major host data,
  * host_results[i] to room for result i.  Copies in, launches on the calling
- * thread's libnova_hip stream, synchronises, copies out. */
+ * thread's libnova_hip stream, synchronises, copies out.  The device buffers
+ * stay with the program and are reused by the next execution of the same
+ * function (a training loop's repeated step); nova_run_free releases them.
+ * Executions of one program are serialised. */
 int32_t nova_run_execute(const NovaRunProgram *p, const char *func, const void *const *host_args,
                          void *const *host_results);
 

@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <set>
 #include <string>
 #include <vector>
@@ -1407,11 +1408,23 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
 
 struct NovaRunProgram {
   std::vector<Func> funcs;
+  // Device buffers of each function's last execution, reused by the next one
+  // when the plan's buffer sizes match (a training loop runs the same step
+  // over and over); freed by nova_run_free.
+  mutable std::mutex mu;
+  mutable std::map<std::string, std::vector<std::pair<void *, int64_t>>> buffers;
   const Func *find(const char *name) const {
     for (const Func &f : funcs)
       if (name && f.name == name) return &f;
     return funcs.size() == 1 && !name ? &funcs[0] : nullptr;
   }
+  void release() {
+    for (auto &kv : buffers)
+      for (auto &b : kv.second)
+        if (b.first) (void)hipFree(b.first);
+    buffers.clear();
+  }
+  ~NovaRunProgram() { release(); }
 };
 
 namespace {
@@ -1538,6 +1551,7 @@ int32_t nova_run_execute(const NovaRunProgram *p, const char *func, const void *
   if ((!host_args && !f->arg_types.empty()) || (!host_results && !pl.results.empty()))
     return fail(NOVA_HIP_EINVAL, "null argument or result array");
   hipStream_t st = static_cast<hipStream_t>(nova_hip_get_stream());
+  std::lock_guard<std::mutex> lock(p->mu);
   std::vector<void *> ptr(pl.bufs.size(), nullptr);
   // Only buffers a step or a result touches get device memory.
   std::vector<bool> used(pl.bufs.size(), false);
@@ -1546,16 +1560,30 @@ int32_t nova_run_execute(const NovaRunProgram *p, const char *func, const void *
     for (const View &v : s.out) if (v.buf >= 0) used[v.buf] = true;
   }
   for (const View &v : pl.results) used[v.buf] = true;
-  auto cleanup = [&]() {
-    for (void *q : ptr)
-      if (q) (void)hipFree(q);
-  };
+  // The buffers of this function's previous execution, if the plan still
+  // has the same sizes; otherwise a fresh set (the old one freed).
+  std::vector<std::pair<void *, int64_t>> &held = p->buffers[f->name];
+  bool reuse = held.size() == pl.bufs.size();
+  for (size_t b = 0; reuse && b < pl.bufs.size(); ++b)
+    reuse = held[b].second == (used[b] ? pl.bufs[b].bytes : 0);
+  if (!reuse) {
+    (void)hipStreamSynchronize(st);
+    for (auto &h : held)
+      if (h.first) (void)hipFree(h.first);
+    held.assign(pl.bufs.size(), {nullptr, 0});
+  }
+  auto cleanup = [&]() {};  // buffers stay with the program
   for (size_t b = 0; b < pl.bufs.size(); ++b) {
     if (pl.bufs[b].bytes == 0 || !used[b]) continue;
-    if (hipMalloc(&ptr[b], (size_t)pl.bufs[b].bytes) != hipSuccess) {
-      cleanup();
-      return fail(NOVA_HIP_ENOMEM, "hipMalloc of %lld bytes failed", (long long)pl.bufs[b].bytes);
+    if (!held[b].first) {
+      if (hipMalloc(&held[b].first, (size_t)pl.bufs[b].bytes) != hipSuccess) {
+        held[b].first = nullptr;
+        return fail(NOVA_HIP_ENOMEM, "hipMalloc of %lld bytes failed",
+                    (long long)pl.bufs[b].bytes);
+      }
+      held[b].second = pl.bufs[b].bytes;
     }
+    ptr[b] = held[b].first;
     if (pl.bufs[b].arg >= 0 &&
         hipMemcpyAsync(ptr[b], host_args[pl.bufs[b].arg], (size_t)pl.bufs[b].bytes,
                        hipMemcpyHostToDevice, st) != hipSuccess) {
