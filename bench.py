@@ -359,7 +359,6 @@ def bench_gpt_step(args):
     Weights random (N(0, 0.02)), so the loss is near ln(vocab)."""
     import numpy as np
     import nova_run
-    sys.path.insert(0, os.path.join(REPO, "tests"))
     from gpt_program import gpt_step
     B, T, V, D, H = 8, 1024, 50304, 384, 1536
     r = np.random.default_rng(6)

@@ -113,6 +113,17 @@ enum {
   ((int32_t)(((in_dt) & 0xf) | (((out_dt) & 0xf) << 4) |                     \
              (((epi) & 0xf) << 8) | (((bias_dt) & 0xf) << 12)))
 
+/* flags bit 16: accumulate in the output dtype.  A linalg.matmul /
+ * batch_matmul whose outs is bf16 or f16 runs its body C += A * B in that
+ * type (NovaMatmulOpLowering builds one for an f16 x f16 nova.matmul, whose
+ * result is f16: NovaToLinalg.cpp:1027-1049, NovaOps.cpp:1198; nova.linear
+ * on f16 / bf16 operands likewise, NovaToLinalgGeneric.cpp:1623-1822):
+ * every product and partial sum is rounded to it, k ascending, from zero or
+ * from the bias (FuseMatmulBias.cpp:184-188).  Needs in == out dtype, bf16
+ * or f16, and an epilogue of none or a bias of that dtype.  Without the bit,
+ * bf16 / f16 inputs accumulate in f32 (the MFMA kernels). */
+#define NOVA_HIP_GEMM_ACC_OUT 0x10000
+
 /* ------------------------------------------------------------------------
  * GEMM family.
  *
@@ -135,7 +146,9 @@ enum {
  *   flags : NOVA_HIP_GEMM_FLAGS(in, out, epilogue, bias dtype).
  * Inputs f32 use an exact f32 kernel (sequential k, unfused multiply-add,
  * the reference's CPU arithmetic); bf16 / f16 inputs use MFMA with f32
- * accumulate.  Low-precision outputs are rounded to nearest-even.
+ * accumulate, or with NOVA_HIP_GEMM_ACC_OUT the same exact kernel with the
+ * accumulator in the input dtype.  Low-precision outputs are rounded to
+ * nearest-even.
  * ---------------------------------------------------------------------- */
 int32_t _mlir_ciface_nova_hip_gemm(const NovaMemRef3D *A, const NovaMemRef3D *B,
                                    NovaMemRef3D *C, const NovaMemRef1D *bias,

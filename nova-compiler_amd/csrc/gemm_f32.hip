@@ -1,9 +1,20 @@
-// Exact f32 GEMM: C[b,m,n] = init + sum_k A[b,m,k] * B[b,k,n], k ascending,
+// Exact GEMM: C[b,m,n] = init + sum_k A[b,m,k] * B[b,k,n], k ascending,
 // every multiply and add separately rounded.  This is the arithmetic of
 // Nova's CPU pipeline for f32 linalg.matmul / batch_matmul (no fast-math,
 // no FMA contraction, sequential k: Pipeline.cpp:61-187), so the result is
 // bit-identical to it, including the bias-initialised accumulator of
-// FuseMatmulBias (FuseMatmulBias.cpp:184-188).  The reference's GPU path
+// FuseMatmulBias (FuseMatmulBias.cpp:184-188).
+//
+// The same kernel, instantiated for bf16 or f16, is linalg.matmul with a
+// narrow outs operand: the upstream named-op body C += A * B runs in the
+// outs element type, so every product and every partial sum is rounded to
+// bf16 / f16 (NovaMatmulOpLowering creates such a matmul for an f16 x f16
+// nova.matmul, whose result type is f16: NovaToLinalg.cpp:1027-1049,
+// NovaOps.cpp:1198).  Each operation is done in f32 and rounded to the
+// narrow type (RNE): a product of two narrow values is exact in f32, and
+// a sum rounded first to f32 (24 bits) then to a p-bit type is the
+// correctly rounded p-bit sum whenever 24 >= 2p + 2 (p = 8 for bf16, 11 for
+// f16), so this is the narrow type's own IEEE arithmetic.  The reference's GPU path
 // would have used tf32 mma.sync for f32 (SURVEY of
 // NovaGPUNestedLayoutDistributionPatterns.cpp:2460); this kernel does not,
 // because tf32 breaks 1e-4 parity.
@@ -24,9 +35,9 @@ constexpr int kT = 64;   // output tile edge
 constexpr int kKs = 16;  // k per LDS stage
 
 struct F32Args {
-  const float *A;
-  const float *B;
-  float *C;
+  const void *A;
+  const void *B;
+  void *C;
   const void *bias;
   int64_t sab, sam, sak;
   int64_t sbb, sbk, sbn;
@@ -54,7 +65,25 @@ __device__ __forceinline__ float gelu_ref(float x) {
   return (0.5f * x) * (1.0f + t);
 }
 
-__global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
+// Element DT of a (at element offset i) as f32 (exact).
+template <int DT>
+__device__ __forceinline__ float elem(const void *p, int64_t i) {
+  if constexpr (DT == NOVA_HIP_DT_F32) return static_cast<const float *>(p)[i];
+  const uint16_t h = static_cast<const uint16_t *>(p)[i];
+  if constexpr (DT == NOVA_HIP_DT_BF16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Round an f32 value to DT (nearest even) and back: the accumulator's type.
+template <int DT>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (DT == NOVA_HIP_DT_BF16) return static_cast<float>(static_cast<__bf16>(x));
+  else if constexpr (DT == NOVA_HIP_DT_F16) return static_cast<float>(static_cast<_Float16>(x));
+  else return x;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_exact_kernel(F32Args a) {
 #pragma clang fp contract(off)
   // Two LDS stages: stage s + 1's global loads are in registers while
   // stage s is multiplied, then written to the other buffer (one barrier
@@ -70,8 +99,9 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
   const int tid = threadIdx.x;
   const int tx = tid & 15, ty = tid >> 4;
 
-  const float *Ab = a.A + (int64_t)b * a.sab;
-  const float *Bb = a.B + (int64_t)b * a.sbb;
+  constexpr int kEsz = DT == NOVA_HIP_DT_F32 ? 4 : 2;
+  const char *Ab = static_cast<const char *>(a.A) + (int64_t)b * a.sab * kEsz;
+  const char *Bb = static_cast<const char *>(a.B) + (int64_t)b * a.sbb * kEsz;
 
   const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
   const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
@@ -94,11 +124,13 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
       int r, kk;
       a_elem(e, r, kk);
       const int gm = m0 + r, gk = k0 + kk;
-      ra[e] = (gm < a.M && gk < a.K) ? Ab[(int64_t)gm * a.sam + (int64_t)gk * a.sak] : 0.0f;
+      ra[e] = (gm < a.M && gk < a.K) ? elem<DT>(Ab, (int64_t)gm * a.sam + (int64_t)gk * a.sak)
+                                     : 0.0f;
       int c, kb;
       b_elem(e, c, kb);
       const int gn = n0 + c, gkb = k0 + kb;
-      rb[e] = (gn < a.N && gkb < a.K) ? Bb[(int64_t)gkb * a.sbk + (int64_t)gn * a.sbn] : 0.0f;
+      rb[e] = (gn < a.N && gkb < a.K) ? elem<DT>(Bb, (int64_t)gkb * a.sbk + (int64_t)gn * a.sbn)
+                                      : 0.0f;
     }
   };
   auto store = [&](int buf) __attribute__((always_inline)) {
@@ -142,8 +174,8 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float p = av[i] * bv[j];
-          acc[i][j] = acc[i][j] + p;
+          const float p = round_to<DT>(av[i] * bv[j]);
+          acc[i][j] = round_to<DT>(acc[i][j] + p);
         }
     }
     if (more) store(buf ^ 1);
@@ -151,7 +183,6 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
     buf ^= 1;
   }
 
-  float *Cb = a.C + (int64_t)b * a.scb;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = m0 + ty * 4 + i;
@@ -161,24 +192,36 @@ __global__ __launch_bounds__(256) void gemm_f32_exact_kernel(F32Args a) {
       const int n = n0 + tx * 4 + j;
       if (n >= a.N) continue;
       float v = acc[i][j];
-      if (has_gelu) v = gelu_ref(v);
-      Cb[(int64_t)m * a.scm + n] = v;
+      const int64_t off = (int64_t)b * a.scb + (int64_t)m * a.scm + n;
+      if constexpr (DT == NOVA_HIP_DT_F32) {
+        if (has_gelu) v = gelu_ref(v);
+        static_cast<float *>(a.C)[off] = v;
+      } else if constexpr (DT == NOVA_HIP_DT_BF16) {
+        static_cast<uint16_t *>(a.C)[off] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+      } else {
+        static_cast<uint16_t *>(a.C)[off] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+      }
     }
   }
 }
 
 }  // namespace
 
-int32_t launch_gemm_f32(const GemmProblem &p, hipStream_t s) {
+int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s) {
   if (p.batch == 0 || p.M == 0 || p.N == 0) return NOVA_HIP_SUCCESS;
   if (p.M > 0x7fffffff || p.N > 0x7fffffff || p.K > 0x7fffffff)
-    return fail(NOVA_HIP_ERANGE, "gemm_f32: dimension exceeds 2^31-1");
-  if (p.out_dt != NOVA_HIP_DT_F32)
-    return fail(NOVA_HIP_EDTYPE, "gemm_f32: f32 inputs produce f32 output only");
+    return fail(NOVA_HIP_ERANGE, "gemm_exact: dimension exceeds 2^31-1");
+  if (p.out_dt != p.in_dt)
+    return fail(NOVA_HIP_EDTYPE, "gemm_exact: the accumulator type must be the input type");
+  if (p.in_dt != NOVA_HIP_DT_F32 &&
+      (p.epi == NOVA_HIP_EPI_GELU || p.epi == NOVA_HIP_EPI_BIAS_GELU ||
+       (p.epi == NOVA_HIP_EPI_BIAS && p.bias_dt != p.in_dt)))
+    return fail(NOVA_HIP_EDTYPE,
+                "gemm: a bf16 / f16 accumulator takes no GELU, and a bias of its own dtype only");
   F32Args a;
-  a.A = static_cast<const float *>(p.A);
-  a.B = static_cast<const float *>(p.B);
-  a.C = static_cast<float *>(p.C);
+  a.A = p.A;
+  a.B = p.B;
+  a.C = p.C;
   a.bias = p.bias;
   a.sab = p.sab;
   a.sbb = p.sbb;
@@ -197,9 +240,14 @@ int32_t launch_gemm_f32(const GemmProblem &p, hipStream_t s) {
   a.bias_dt = p.bias_dt;
   a.epi = p.epi;
   const int64_t total = p.batch * a.tiles_m * a.tiles_n;
-  if (total > 0x7fffffff) return fail(NOVA_HIP_ERANGE, "gemm_f32: grid too large");
-  hipLaunchKernelGGL(gemm_f32_exact_kernel, dim3((unsigned)total), dim3(256), 0, s, a);
-  return check_hip(hipGetLastError(), "gemm_f32 launch");
+  if (total > 0x7fffffff) return fail(NOVA_HIP_ERANGE, "gemm_exact: grid too large");
+  if (p.in_dt == NOVA_HIP_DT_BF16)
+    hipLaunchKernelGGL(gemm_exact_kernel<NOVA_HIP_DT_BF16>, dim3((unsigned)total), dim3(256), 0, s, a);
+  else if (p.in_dt == NOVA_HIP_DT_F16)
+    hipLaunchKernelGGL(gemm_exact_kernel<NOVA_HIP_DT_F16>, dim3((unsigned)total), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(gemm_exact_kernel<NOVA_HIP_DT_F32>, dim3((unsigned)total), dim3(256), 0, s, a);
+  return check_hip(hipGetLastError(), "gemm_exact launch");
 }
 
 }  // namespace nova_hip

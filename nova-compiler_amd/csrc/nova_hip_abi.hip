@@ -103,7 +103,8 @@ bool nonneg_sizes(const D *d, int rank) {
 }
 
 int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt) {
-  if (flags & ~0xffff) return fail(NOVA_HIP_EINVAL, "gemm: unknown flag bits 0x%x", flags);
+  if (flags & ~(0xffff | NOVA_HIP_GEMM_ACC_OUT))
+    return fail(NOVA_HIP_EINVAL, "gemm: unknown flag bits 0x%x", flags);
   in_dt = flags & 0xf;
   out_dt = (flags >> 4) & 0xf;
   epi = (flags >> 8) & 0xf;
@@ -113,6 +114,15 @@ int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt)
     return fail(NOVA_HIP_EDTYPE, "gemm: bad dtype/epilogue code in flags 0x%x", flags);
   if (in_dt == NOVA_HIP_DT_F32 && out_dt != NOVA_HIP_DT_F32)
     return fail(NOVA_HIP_EDTYPE, "gemm: f32 inputs produce f32 output only");
+  if (flags & NOVA_HIP_GEMM_ACC_OUT) {
+    if (in_dt == NOVA_HIP_DT_F32 || out_dt != in_dt)
+      return fail(NOVA_HIP_EDTYPE,
+                  "gemm: accumulating in the output dtype needs bf16 or f16 inputs of that dtype");
+    if (epi == NOVA_HIP_EPI_GELU || epi == NOVA_HIP_EPI_BIAS_GELU ||
+        (epi == NOVA_HIP_EPI_BIAS && bias_dt != out_dt))
+      return fail(NOVA_HIP_EDTYPE,
+                  "gemm: a bf16 / f16 accumulator takes no GELU, and a bias of its own dtype only");
+  }
   return NOVA_HIP_SUCCESS;
 }
 
@@ -160,6 +170,7 @@ int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
   p.out_dt = out_dt;
   p.epi = epi;
   p.bias_dt = bias_dt;
+  p.acc_out = (flags & NOVA_HIP_GEMM_ACC_OUT) != 0;
   const int esz = dtype_size(in_dt);
   const int osz = dtype_size(out_dt);
   p.A = data_of(A) + A->offset * esz;
@@ -207,7 +218,7 @@ int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
   if (empty) return NOVA_HIP_SUCCESS;
 
   hipStream_t s = current_stream();
-  return (in_dt == NOVA_HIP_DT_F32) ? launch_gemm_f32(p, s) : launch_gemm_mfma(p, s);
+  return (in_dt == NOVA_HIP_DT_F32 || p.acc_out) ? launch_gemm_exact(p, s) : launch_gemm_mfma(p, s);
 }
 
 NovaMemRef3D lift(const NovaMemRef2D *d) {
@@ -256,6 +267,8 @@ int32_t gemm2d_to(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C,
 
 // Flags of the backward GEMM entry points: dtypes only, no epilogue.
 int32_t backward_flags(int32_t flags, int &in_dt, int &out_dt, const char *what) {
+  if (flags & NOVA_HIP_GEMM_ACC_OUT)
+    return fail(NOVA_HIP_EINVAL, "%s: no narrow-accumulator form (flags 0x%x)", what, flags);
   int epi, bias_dt;
   int32_t rc = decode_flags(flags, in_dt, out_dt, epi, bias_dt);
   if (rc) return rc;

@@ -39,12 +39,14 @@ struct GemmProblem {
   int64_t scb, scm;       // C batch and row strides (unit on N)
   bool a_kcontig, b_kcontig;
   int in_dt, out_dt, bias_dt, epi;
+  bool acc_out;  // accumulate in the output dtype (NOVA_HIP_GEMM_ACC_OUT)
 };
 
 // Launch the MFMA kernels (bf16/f16 in).  Returns a NOVA_HIP_* status.
 int32_t launch_gemm_mfma(const GemmProblem &p, hipStream_t s);
-// Launch the exact f32 kernel (f32 in).
-int32_t launch_gemm_f32(const GemmProblem &p, hipStream_t s);
+// Launch the exact kernel: f32 in and out, or (acc_out) bf16 / f16 in and
+// out with the accumulator in that type.
+int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s);
 
 // ---- reductions ------------------------------------------------------------
 struct LayerNormProblem {

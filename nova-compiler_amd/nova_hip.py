@@ -69,6 +69,9 @@ EXPORTS = (
 )
 
 
+GEMM_ACC_OUT = 0x10000  # NOVA_HIP_GEMM_ACC_OUT
+
+
 def gemm_flags(in_dt: int, out_dt: int, epi: int = EPI_NONE, bias_dt: int = 0) -> int:
     """NOVA_HIP_GEMM_FLAGS of include/nova_hip.h."""
     return (in_dt & 0xF) | ((out_dt & 0xF) << 4) | ((epi & 0xF) << 8) | ((bias_dt & 0xF) << 12)
@@ -215,12 +218,14 @@ def _as3(t):
     return t if t.dim() == 3 else t.unsqueeze(0)
 
 
-def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None):
+def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None,
+         acc_out: bool = False):
     """Batched GEMM through _mlir_ciface_nova_hip_gemm.
 
     A [Bt,M,K] or [M,K]; B [Bt,K,N] or [K,N] (any unit-stride layout,
     transposed views included); returns C [Bt,M,N] (or [M,N] for rank-2
-    inputs) in ``out_dtype`` (f32 by default).
+    inputs) in ``out_dtype`` (f32 by default).  ``acc_out``: accumulate in
+    the output dtype (NOVA_HIP_GEMM_ACC_OUT; bf16 / f16 in and out).
     """
     torch = _torch()
     in_dt = _dt(A)
@@ -238,7 +243,7 @@ def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None)
         od = _dt(out)
         C3 = _as3(out)
     bias_dt = _dt(bias) if bias is not None else 0
-    flags = gemm_flags(in_dt, od, epilogue, bias_dt)
+    flags = gemm_flags(in_dt, od, epilogue, bias_dt) | (GEMM_ACC_OUT if acc_out else 0)
     dA, dB, dC = memref_of(A3), memref_of(B3), memref_of(C3)
     dbias = memref_of(bias) if bias is not None else None
     _bind_stream()

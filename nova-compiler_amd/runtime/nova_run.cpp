@@ -657,6 +657,7 @@ struct Step {
   std::string text;
   float value = 0.0f;           // fill value
   int64_t dims[3] = {0, 0, 0};  // reduce_sum: outer, reduced, inner
+  bool acc_out = false;         // GEMM accumulating in its bf16 / f16 output dtype
 };
 
 int64_t numel_of(const std::vector<int64_t> &shape) {
@@ -700,6 +701,7 @@ struct Planner {
   std::map<std::string, View> env;
   std::map<std::string, int> uses;
   std::map<std::string, std::string> consts;
+  std::set<int> empty_bufs;  // buffers of tensor.empty results
 
   explicit Planner(const Func &fn) : f(fn) {}
 
@@ -781,15 +783,35 @@ struct Planner {
                   op.name.c_str(), dt_name(a.dt));
     if (a.dt == DT_F32 && out.dt != DT_F32)
       return fail(NOVA_HIP_EDTYPE, "line %d: f32 operands give f32 results only", op.line);
+    // A bf16 / f16 result is a linalg.matmul with narrow outs, whose body
+    // runs in the outs type (NovaToLinalg.cpp:1027-1049): the accumulator is
+    // that dtype.  Only the same-dtype form is on this path: a bf16 x bf16
+    // nova.matmul infers f16 (NovaOps.cpp:1198), and what linalg's element
+    // cast does between two 16-bit float types is not pinned here.
+    const bool narrow = out.dt != DT_F32;
+    if (narrow) {
+      if (a.logical != a.dt || b.logical != b.dt || a.dt != out.dt)
+        return fail(NOVA_HIP_EDTYPE,
+                    "line %d: %s of %s operands with a %s result accumulates in %s through a "
+                    "%s -> %s element cast that is not on this path (spell the f32-accumulate "
+                    "form: nova.cast the operands to f32, or f32 linalg outs)",
+                    op.line, op.name.c_str(), dt_name(a.logical), dt_name(out.dt),
+                    dt_name(out.dt), dt_name(a.logical), dt_name(out.dt));
+      if (bias && (bias->dt != out.dt || bias->logical != bias->dt))
+        return fail(NOVA_HIP_EDTYPE, "line %d: %s with a %s accumulator needs a %s bias",
+                    op.line, op.name.c_str(), dt_name(out.dt), dt_name(out.dt));
+    }
     Step s;
     s.kind = "gemm";
     s.in = {a, b};
     if (bias) s.in.push_back(*bias);
     s.epi = bias ? NOVA_HIP_EPI_BIAS : NOVA_HIP_EPI_NONE;
     s.out_dt = out.dt;
+    s.acc_out = narrow;
     std::string name = op.results[0];
     std::string fused = op.name;
-    const Op *u = sole_user(name, idx + 1);
+    // (GELU and casts fold only into an f32 accumulator.)
+    const Op *u = narrow ? nullptr : sole_user(name, idx + 1);
     if (u && u->name == "nova.gelu") {
       s.epi = bias ? NOVA_HIP_EPI_BIAS_GELU : NOVA_HIP_EPI_GELU;
       folded.insert(u);
@@ -816,6 +838,7 @@ struct Planner {
              s.epi == NOVA_HIP_EPI_NONE ? "none" : s.epi == NOVA_HIP_EPI_BIAS ? "bias"
              : s.epi == NOVA_HIP_EPI_BIAS_GELU ? "bias+gelu" : "gelu");
     s.text = buf;
+    if (narrow) s.text += std::string(" accumulate=") + dt_name(out.dt);
     plan.steps.push_back(s);
     env[op.results[0]] = out;
     env[name] = out;
@@ -844,6 +867,7 @@ struct Planner {
         consts[op.results[0]] = op.literal;
       } else if (n == "tensor.empty") {
         env[op.results[0]] = fresh(op.result_types[0]);
+        empty_bufs.insert(env[op.results[0]].buf);
       } else if (n == "bufferization.to_tensor") {
         View v;
         if ((rc = get(op, 0, v))) return rc;
@@ -855,6 +879,15 @@ struct Planner {
         if (c.empty() || strtod(c.c_str(), nullptr) != 0.0)
           return fail(NOVA_HIP_EINVAL, "line %d: linalg.fill with a value other than 0 is not on this path",
                       op.line);
+        // The fill's result is a new tensor.  It takes over its destination's
+        // buffer only when that is a tensor.empty used by nothing else;
+        // otherwise (a function argument, a value read again later) it gets
+        // a buffer of its own, so the fill and the GEMMs writing into it
+        // leave the destination as it was.
+        if (!empty_bufs.count(dst.buf) || uses[op.operands[1]] != 1) {
+          const int dt = dst.logical;
+          dst = fresh(Type{dst.shape, dt, false});
+        }
         dst.zero = true;
         env[op.results[0]] = dst;
         // The fill only matters if its result is read by something other
@@ -884,6 +917,10 @@ struct Planner {
         if (op.result_types[0].dt != DT_F32 && a.dt != op.result_types[0].dt)
           return fail(NOVA_HIP_EDTYPE, "line %d: %s with %s outs is not on this path", op.line,
                       n.c_str(), dt_name(op.result_types[0].dt));
+        // The product writes its outs buffer in place only when this GEMM is
+        // the fill result's sole user; two GEMMs over one (CSE'd) fill each
+        // get a buffer of their own.
+        if (uses[op.operands[2]] != 1) c.buf = -1;
         if ((rc = emit_gemm(op, k, a, b, nullptr, c, folded))) return rc;
       } else if (n == "nova.matmul") {
         View a, b;
@@ -1266,7 +1303,8 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
                                       reinterpret_cast<const NovaMemRef3D *>(&B),
                                       reinterpret_cast<NovaMemRef3D *>(&C),
                                       reinterpret_cast<const NovaMemRef1D *>(pb),
-                                      NOVA_HIP_GEMM_FLAGS(a.dt, s.out_dt, s.epi, bias_dt));
+                                      NOVA_HIP_GEMM_FLAGS(a.dt, s.out_dt, s.epi, bias_dt) |
+                                          (s.acc_out ? NOVA_HIP_GEMM_ACC_OUT : 0));
   }
   if (s.kind == "layer_norm") {
     Desc<2> x = desc<2>(s.in[0], ptr), y = desc<2>(s.out[0], ptr);

@@ -182,6 +182,41 @@ int nova_ref_gemm(const void *A, int adt, int64_t sab, int64_t sam, int64_t sak,
 }
 
 /*
+ * linalg.matmul / batch_matmul with a bf16 or f16 outs operand (cdt == adt ==
+ * bdt): the named op's body C += A * B is evaluated in the outs type, so the
+ * product and each partial sum are rounded to it (cast_signed of a same-type
+ * operand is the operand itself).  NovaMatmulOpLowering creates this form
+ * for an f16 x f16 nova.matmul, whose inferred result type is f16
+ * (NovaToLinalg.cpp:1027-1049, NovaOps.cpp:1198), and nova.linear for
+ * narrow operands (NovaToLinalgGeneric.cpp:1623-1822), whose bias then
+ * initialises the accumulator (FuseMatmulBias.cpp:184-188; epilogue 1, bias
+ * of dtype cdt).  x86 has no bf16 / f16 arithmetic, so LLVM evaluates each
+ * operation in f32 and rounds it back; that is what this does.
+ */
+int nova_ref_gemm_acc_out(const void *A, const void *B, int64_t sab, int64_t sam, int64_t sak,
+                          int64_t sbb, int64_t sbk, int64_t sbn, const void *bias,
+                          int epilogue, void *C, int cdt, int64_t batch, int64_t M,
+                          int64_t N, int64_t K) {
+  if (!A || !B || !C || batch < 0 || M < 0 || N < 0 || K < 0) return -1;
+  if (cdt != 1 && cdt != 2) return -1;
+  if (epilogue != 0 && epilogue != 1) return -1;
+  if (epilogue == 1 && !bias) return -1;
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t i = 0; i < M; ++i)
+      for (int64_t j = 0; j < N; ++j) {
+        float acc = epilogue == 1 ? load_as_f32(bias, cdt, j) : 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+          float a = load_as_f32(A, cdt, b * sab + i * sam + k * sak);
+          float w = load_as_f32(B, cdt, b * sbb + k * sbk + j * sbn);
+          float p = round_to(cdt, a * w);
+          acc = round_to(cdt, acc + p);
+        }
+        store_from_f32(C, cdt, (b * M + i) * N + j, acc);
+      }
+  return 0;
+}
+
+/*
  * Same arithmetic as nova_ref_gemm for a list of output coordinates
  * idx[3*t + {0,1,2}] = (b, i, j).  out[t] receives the value the reference
  * would store, widened back to f32 (so bf16/f16 outputs are already rounded).

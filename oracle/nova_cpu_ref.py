@@ -58,6 +58,9 @@ def lib() -> ctypes.CDLL:
         L.nova_ref_f16_to_f32.restype = ctypes.c_float
         L.nova_ref_binary_f32.argtypes = [P, P, P, I64, I]
         L.nova_ref_binary_f32.restype = I
+        L.nova_ref_gemm_acc_out.argtypes = [P, P, I64, I64, I64, I64, I64, I64, P, I, P, I,
+                                            I64, I64, I64, I64]
+        L.nova_ref_gemm_acc_out.restype = I
         L.nova_ref_gelu_backward_f32.argtypes = [ctypes.c_float, ctypes.c_float]
         L.nova_ref_gelu_backward_f32.restype = ctypes.c_float
         L.nova_ref_gelu_backward_array.argtypes = [P, P, P, I64]
@@ -112,6 +115,19 @@ def gemm(A, B, *, adt=None, bdt=None, bias=None, biasdt=None, epilogue=EPI_NONE,
     bdtc = _dtcode(bias, biasdt) if bias is not None else 0
     rc = lib().nova_ref_gemm(pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn, pbias, bdtc,
                              epilogue, C.ctypes.data, cdt, batch, M, N, K)
+    assert rc == 0, rc
+    return C
+
+
+def gemm_acc_out(A, B, *, dt, bias=None) -> np.ndarray:
+    """linalg.matmul with bf16 / f16 outs: the accumulator in dtype dt
+    (inputs of that dtype as uint16 bits); returns C [Bt,M,N] uint16 bits."""
+    (pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn, batch, M, N, K) = _gemm_args(A, B, dt, dt)
+    C = np.empty((batch, M, N), dtype=np.uint16)
+    pbias = bias.ctypes.data if bias is not None else None
+    rc = lib().nova_ref_gemm_acc_out(pa, pb, sab, sam, sak, sbb, sbk, sbn, pbias,
+                                     EPI_BIAS if bias is not None else EPI_NONE,
+                                     C.ctypes.data, dt, batch, M, N, K)
     assert rc == 0, rc
     return C
 

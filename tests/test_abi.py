@@ -89,6 +89,15 @@ def test_gemm_bad_flags():
     assert gemm_rc(A, B, C, flags=nh.gemm_flags(7, 0)) == 4
     assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_F32, nh.DT_BF16)) == 4
     assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_BF16, nh.DT_F32, 9)) == 4
+    # the narrow accumulator: same 16-bit dtype in and out, no GELU, own-dtype bias
+    acc = nh.GEMM_ACC_OUT
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_BF16, nh.DT_F32) | acc) == 4
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_BF16, nh.DT_F16) | acc) == 4
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_F32, nh.DT_F32) | acc) == 4
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_F16, nh.DT_F16, nh.EPI_GELU) | acc) == 4
+    assert gemm_rc(A, B, C, d1(8),
+                   nh.gemm_flags(nh.DT_F16, nh.DT_F16, nh.EPI_BIAS, nh.DT_F32) | acc) == 4
+    assert "bias of its own dtype" in last_error()
 
 
 def test_gemm_bias_required_and_checked():

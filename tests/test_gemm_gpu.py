@@ -368,3 +368,46 @@ def test_gemm_staged_misaligned_exact(cuda, layout, shape, offsets):
     got = nh.gemm(A, B).cpu().numpy()
     want = np.einsum("bmk,bkn->bmn", a.astype(np.float64), b.astype(np.float64))
     np.testing.assert_array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("dt", [S.BF16, S.F16])
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN"])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1), (2, 37, 45, 23), (1, 64, 64, 300), (3, 65, 70, 129)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_gemm_narrow_accumulator_bit_exact(cuda, dt, layout, shape, bias):
+    """NOVA_HIP_GEMM_ACC_OUT: linalg.matmul with bf16 / f16 outs accumulates in
+    that type (NovaToLinalg.cpp:1027-1049); same bits as the oracle."""
+    import torch
+    batch, M, N, K = shape
+    A, B = lp_inputs((batch, M, K), (batch, K, N), dt, 91 + K)
+    bvec = S.uniform((N,), 92, dtype=dt) if bias else None
+    dA = view_as(A, layout[0], cuda, dt)
+    dB = view_as(B, layout[1], cuda, dt)
+    tdt = torch.bfloat16 if dt == S.BF16 else torch.float16
+    C = nh.gemm(dA, dB, bias=to_dev(bvec, dt, cuda) if bias else None,
+                epilogue=nh.EPI_BIAS if bias else nh.EPI_NONE, out_dtype=tdt, acc_out=True)
+    got = C.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = ref.gemm_acc_out(A, B, dt=dt, bias=bvec)
+    assert np.array_equal(got, want)
+
+
+def test_gemm_narrow_accumulator_stall_on_gpu(cuda):
+    """4000 ones summed in f16 stop at 2048 (an f32 accumulator gives 4000)."""
+    import torch
+    A = torch.ones((1, 4000), dtype=torch.float16, device=cuda)
+    B = torch.ones((4000, 8), dtype=torch.float16, device=cuda)
+    C = nh.gemm(A, B, out_dtype=torch.float16, acc_out=True)
+    assert (C.float() == 2048).all()
+    assert (nh.gemm(A, B, out_dtype=torch.float16).float() == 4000).all()
+
+
+def test_gemm_narrow_accumulator_refuses_other_forms(cuda):
+    import torch
+    A = torch.ones((4, 8), dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(nh.NovaHipError):
+        nh.gemm(A, A.t().contiguous(), out_dtype=torch.float16, acc_out=True)   # bf16 -> f16
+    with pytest.raises(nh.NovaHipError):
+        nh.gemm(A, A.t().contiguous(), out_dtype=torch.float32, acc_out=True)   # f32 out
+    with pytest.raises(nh.NovaHipError):
+        nh.gemm(A, A.t().contiguous(), out_dtype=torch.bfloat16, acc_out=True,
+                epilogue=nh.EPI_GELU)

@@ -284,3 +284,80 @@ def test_sce_closed_forms():
 def test_sce_rejects_out_of_range_label():
     with pytest.raises(ValueError):
         ref.sce(np.zeros((2, 5), np.float32), np.array([0, 5], np.int32))
+
+
+# ------------------------------------------------- narrow accumulator ------
+# linalg.matmul with bf16 / f16 outs accumulates in that type
+# (NovaToLinalg.cpp:1027-1049).  Pinned by sums that stall where the narrow
+# type runs out of significand bits, by bias-first order, and against
+# numpy's float16 / torch's CPU bfloat16 arithmetic (independent rounding
+# code) on random data.
+
+def _bits(x, dt):
+    x = np.asarray(x, np.float32)
+    f = ref.lib().nova_ref_f32_to_bf16 if dt == BF16 else ref.lib().nova_ref_f32_to_f16
+    return np.vectorize(lambda v: f(float(v)), otypes=[np.uint16])(x)
+
+
+def _widen(h, dt):
+    f = ref.lib().nova_ref_bf16_to_f32 if dt == BF16 else ref.lib().nova_ref_f16_to_f32
+    return np.vectorize(lambda v: f(int(v)), otypes=[np.float32])(h)
+
+
+@pytest.mark.parametrize("dt,K,stall", [(F16, 4000, 2048.0), (BF16, 300, 256.0)])
+def test_narrow_accumulator_stalls(dt, K, stall):
+    """sum of K ones: f16 stops at 2048 (2048 + 1 ties to even), bf16 at 256;
+    an f32 accumulator stored narrow would give K."""
+    A = _bits(np.ones((1, K)), dt)
+    B = _bits(np.ones((K, 3)), dt)
+    got = _widen(ref.gemm_acc_out(A, B, dt=dt), dt)
+    assert np.all(got == stall)
+    wide = _widen(ref.gemm(A, B, adt=dt, bdt=dt, cdt=dt), dt)
+    assert np.all(wide == K)
+
+
+def test_narrow_accumulator_bias_first():
+    """FuseMatmulBias: the bias initialises the accumulator.  2048 + 1 + 1 + 1
+    in f16 stays 2048; bias last (3 + 2048) would give 2052."""
+    A = _bits(np.ones((2, 3)), F16)
+    B = _bits(np.ones((3, 4)), F16)
+    bias = _bits(np.full(4, 2048.0), F16)
+    got = _widen(ref.gemm_acc_out(A, B, dt=F16, bias=bias), F16)
+    assert np.all(got == 2048.0)
+
+
+def test_narrow_accumulator_matches_numpy_float16():
+    g = rng(11)
+    A = g.uniform(-2, 2, (2, 9, 37)).astype(np.float16)
+    B = g.uniform(-2, 2, (2, 37, 7)).astype(np.float16)
+    want = np.zeros((2, 9, 7), np.float16)
+    for b in range(2):
+        for i in range(9):
+            for j in range(7):
+                acc = np.float16(0)
+                for k in range(37):
+                    acc = np.float16(acc + np.float16(A[b, i, k] * B[b, k, j]))
+                want[b, i, j] = acc
+    got = ref.gemm_acc_out(A.view(np.uint16), B.view(np.uint16), dt=F16)
+    assert np.array_equal(got, want.view(np.uint16))
+    # transposed operand views give the same bits
+    At = np.ascontiguousarray(A.view(np.uint16).transpose(0, 2, 1)).transpose(0, 2, 1)
+    assert np.array_equal(ref.gemm_acc_out(At, B.view(np.uint16), dt=F16), got)
+
+
+def test_narrow_accumulator_matches_torch_bfloat16():
+    import torch
+    g = rng(12)
+    A = torch.from_numpy(g.uniform(-2, 2, (5, 23)).astype(np.float32)).to(torch.bfloat16)
+    B = torch.from_numpy(g.uniform(-2, 2, (23, 6)).astype(np.float32)).to(torch.bfloat16)
+    bias = torch.from_numpy(g.uniform(-1, 1, (6,)).astype(np.float32)).to(torch.bfloat16)
+    want = torch.empty((5, 6), dtype=torch.bfloat16)
+    for i in range(5):
+        for j in range(6):
+            acc = bias[j].clone()
+            for k in range(23):
+                acc = acc + A[i, k] * B[k, j]   # each op rounded to bf16 on the CPU
+            want[i, j] = acc
+    bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)
+    got = ref.gemm_acc_out(bits(A), bits(B), dt=BF16, bias=bits(bias))[0]
+    assert np.array_equal(got, bits(want))

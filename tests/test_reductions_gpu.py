@@ -129,3 +129,44 @@ def test_sce_empty_batch_and_bad_label_give_nan(cuda):
 def test_c5_sce_full_size(cuda):
     inp = S.config_inputs("c5_sce")
     check_sce(inp["logits"], inp["labels"], cuda, "c5 sce")
+
+
+@pytest.mark.parametrize("C", [40000, 50304, 32772])
+def test_sce_streaming_rows_above_32k(cuda, C):
+    """Rows of more than 32768 classes with 16-byte aligned rows (C % 4 == 0)
+    take the chunked streaming path (the GPT step's vocab is 50304): loss
+    and softmax against the oracle, plus the fused gradient and
+    sce_backward bit-identical to each other."""
+    import torch
+    rows = 24
+    assert C % 4 == 0 and C > 32768
+    x = S.normal((rows, C), 45, 0, 2)
+    t = S.labels(rows, C, 45, offset=rows * C)
+    t[0], t[1] = 0, C - 1                # the row ends
+    check_sce(x, t, cuda, f"sce {rows}x{C}", softmax=True)
+    sm_ref, loss_ref, _ = ref.sce(x, t, softmax=True)
+    X, T = dev(x, cuda), dev(t, cuda)
+    loss, grad = nh.sce_fwd_bwd(X, T)
+    assert_close_f32(loss.cpu().numpy(), loss_ref, "fused loss")
+    assert_close_f32(grad.cpu().numpy(), ref.sce_backward(sm_ref, t), "fused grad")
+    sm, _ = nh.sce(X, T, softmax=True)
+    g2 = nh.sce_backward(sm, T)
+    assert torch.equal(grad, g2)
+    # sce_backward from the oracle's softmax: the same two f32 operations
+    g3 = nh.sce_backward(dev(sm_ref, cuda), T)
+    assert np.array_equal(g3.cpu().numpy(), ref.sce_backward(sm_ref, t))
+
+
+@pytest.mark.parametrize("mean", [1.0, 3.0])
+def test_layer_norm_offset_data(cuda, mean):
+    """x ~ N(mean, 1).  The reference's one-pass variance var = Q/D - mean^2
+    (NovaToLinalgGeneric.cpp:2064-2113) cancels: Q/D ~ mean^2 + 1, so the
+    rounding error of Q is amplified by (mean^2 + 1) in var.  The GPU sums Q
+    in a different order from the oracle's sequential loop; at D = 4096 the
+    two stay within the 1e-4 bar up to |mean| / sigma = 3 (error ~ 2e-5 at
+    3, growing as mean^2)."""
+    rows, D = 64, 4096
+    x = (S.normal((rows, D), 34) + np.float32(mean)).astype(np.float32)
+    g = (1 + S.normal((D,), 34, 0, 0.1, offset=rows * D)).astype(np.float32)
+    b = S.normal((D,), 34, 0, 0.1, offset=rows * D + D)
+    check_ln(x, g, b, cuda, f"ln N({mean}, 1)")

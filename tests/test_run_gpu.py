@@ -147,13 +147,15 @@ def gpt_step_oracle(tok, tgt, pos, wte, wpe, g1, be1, w1, c1, w2, c2, g2, be2, w
     return [loss, dwte, dwpe, gh[1], gh[2], gu[1], gu[2], gd[1], gd[2], gr[1], gr[2], dwlm]
 
 
-def test_gpt_step_program_end_to_end(cuda):
+@pytest.mark.parametrize("B,T,V,D,H", [(2, 16, 96, 64, 128), (1, 64, 50304, 64, 128)])
+def test_gpt_step_program_end_to_end(cuda, B, T, V, D, H):
     """A whole GPT training step (embeddings, LayerNorm, MLP with GELU,
     residual, LM head, SCE loss and the full backward to the embedding
     gradients) through libnova_run, against the oracle's ops composed in the
-    same order."""
+    same order.  The second size has the reference's vocab (50304): its SCE
+    rows take the streaming path for more than 32768 classes, and the LM
+    head's weight gradient is a K = 64 product over 50304 columns."""
     from gpt_program import gpt_step
-    B, T, V, D, H = 2, 16, 96, 64, 128
     r = np.random.default_rng(79)
     f = lambda *s, k=0.1: (r.standard_normal(s) * k).astype(np.float32)  # noqa: E731
     tok = r.integers(0, V, (B, T)).astype(np.int16)
@@ -184,3 +186,47 @@ def test_nova_run_cli_gpt_step_with_i16_arguments(cuda, tmp_path):
     r = subprocess.run([exe, str(f), "--reps", "2"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     assert "ms per run" in r.stdout and "nan" not in r.stdout.lower()
+
+
+def test_cse_fill_and_argument_fill_programs(cuda):
+    """Two products over one zero fill, and a fill into an argument that a
+    later product reads: every result matches the oracle (f32 bit-exact)."""
+    p = nova_run.Program("""func.func @two(%a: tensor<40x24xf32>, %b: tensor<24x16xf32>, %c: tensor<24x16xf32>) -> (tensor<40x16xf32>, tensor<40x16xf32>) {
+      %z = arith.constant 0.000000e+00 : f32
+      %e = tensor.empty() : tensor<40x16xf32>
+      %f = linalg.fill ins(%z : f32) outs(%e : tensor<40x16xf32>) -> tensor<40x16xf32>
+      %r1 = linalg.matmul ins(%a, %b : tensor<40x24xf32>, tensor<24x16xf32>) outs(%f : tensor<40x16xf32>) -> tensor<40x16xf32>
+      %r2 = linalg.matmul ins(%a, %c : tensor<40x24xf32>, tensor<24x16xf32>) outs(%f : tensor<40x16xf32>) -> tensor<40x16xf32>
+      return %r1, %r2 : tensor<40x16xf32>, tensor<40x16xf32>
+    }
+    func.func @argfill(%a: tensor<32x32xf32>, %x: tensor<32x32xf32>) -> (tensor<32x32xf32>, tensor<32x32xf32>) {
+      %z = arith.constant 0.000000e+00 : f32
+      %f = linalg.fill ins(%z : f32) outs(%x : tensor<32x32xf32>) -> tensor<32x32xf32>
+      %r1 = linalg.matmul ins(%a, %a : tensor<32x32xf32>, tensor<32x32xf32>) outs(%f : tensor<32x32xf32>) -> tensor<32x32xf32>
+      %r2 = nova.matmul %x, %a : tensor<32x32xf32>, tensor<32x32xf32>
+      return %r1, %r2 : tensor<32x32xf32>, tensor<32x32xf32>
+    }""")
+    a = S.uniform((40, 24), 81)
+    b = S.uniform((24, 16), 81, offset=a.size)
+    c = S.uniform((24, 16), 81, offset=a.size + b.size)
+    r1, r2 = p.run("two", a, b, c)
+    assert np.array_equal(r1, ref.gemm(a, b)[0])
+    assert np.array_equal(r2, ref.gemm(a, c)[0])
+    a = S.uniform((32, 32), 82)
+    x = S.uniform((32, 32), 82, offset=a.size)
+    r1, r2 = p.run("argfill", a, x)
+    assert np.array_equal(r1, ref.gemm(a, a)[0])
+    assert np.array_equal(r2, ref.gemm(x, a)[0])
+
+
+def test_f16_nova_matmul_accumulates_in_f16(cuda):
+    """f16 x f16 nova.matmul gives f16 (NovaOps.cpp:1198) from an f16
+    linalg.matmul: the accumulator is f16 (oracle bits)."""
+    p = nova_run.Program("""func.func @h(%a: tensor<3x50x300xf16>, %b: tensor<3x300x40xf16>) -> tensor<3x50x40xf16> {
+      %r = nova.matmul %a, %b : tensor<3x50x300xf16>, tensor<3x300x40xf16>
+      return %r : tensor<3x50x40xf16>
+    }""")
+    A = S.uniform((3, 50, 300), 83, dtype=S.F16)
+    B = S.uniform((3, 300, 40), 83, dtype=S.F16, offset=A.size)
+    (C,) = p.run("h", A, B)
+    assert np.array_equal(np.asarray(C).view(np.uint16), ref.gemm_acc_out(A, B, dt=S.F16))

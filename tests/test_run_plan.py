@@ -61,12 +61,14 @@ def test_memref_entry_writes_output_argument():
 
 
 def test_nova_matmul_bf16_infers_f16_result():
-    """NovaOps.cpp:1198: bf16 x bf16 nova.matmul gives f16."""
+    """NovaOps.cpp:1198: bf16 x bf16 nova.matmul gives f16 (the planner then
+    refuses it: its bf16 -> f16 accumulation is not on this path)."""
     p = nova_run.Program("""func.func @m(%a: tensor<8x16xbf16>, %b: tensor<16x4xbf16>) -> tensor<8x4xf16> {
       %r = nova.matmul %a, %b : tensor<8x16xbf16>, tensor<16x4xbf16>
       return %r : tensor<8x4xf16>
     }""")
-    assert p.results("m") == [(2, (8, 4))]
+    with pytest.raises(nova_run.NovaRunError, match="bf16 operands with a f16 result"):
+        p.plan("m")
 
 
 def test_ops_outside_the_path_are_refused():
@@ -144,3 +146,82 @@ def test_glue_forms_outside_the_path_are_refused(body, msg):
     p = nova_run.Program(text)
     with pytest.raises(nova_run.NovaRunError, match=msg):
         p.plan("f")
+
+
+def _gemm_outputs(plan):
+    """Output buffer id of each GEMM launch in a plan text."""
+    import re
+    outs = []
+    for line in plan.splitlines():
+        if "_mlir_ciface_nova_hip_gemm(" in line:
+            outs.append(int(re.search(r"\) -> b(\d+)\[", line).group(1)))
+    return outs
+
+
+def test_gemms_over_one_cse_fill_get_their_own_buffers():
+    """After CSE (Pipeline.cpp:86) two products may share one zero fill; each
+    result is a new tensor, so they must not land in one buffer."""
+    p = nova_run.Program("""func.func @two(%a: tensor<8x16xf32>, %b: tensor<16x4xf32>, %c: tensor<16x4xf32>) -> (tensor<8x4xf32>, tensor<8x4xf32>) {
+      %z = arith.constant 0.000000e+00 : f32
+      %e = tensor.empty() : tensor<8x4xf32>
+      %f = linalg.fill ins(%z : f32) outs(%e : tensor<8x4xf32>) -> tensor<8x4xf32>
+      %r1 = linalg.matmul ins(%a, %b : tensor<8x16xf32>, tensor<16x4xf32>) outs(%f : tensor<8x4xf32>) -> tensor<8x4xf32>
+      %r2 = linalg.matmul ins(%a, %c : tensor<8x16xf32>, tensor<16x4xf32>) outs(%f : tensor<8x4xf32>) -> tensor<8x4xf32>
+      return %r1, %r2 : tensor<8x4xf32>, tensor<8x4xf32>
+    }""")
+    outs = _gemm_outputs(p.plan("two"))
+    assert len(outs) == 2 and outs[0] != outs[1]
+    assert "hipMemsetAsync" not in p.plan("two")
+
+
+def test_fill_into_an_argument_leaves_the_argument_alone():
+    """linalg.fill outs(%x) makes a new tensor: %x keeps its values for the
+    second product, which reads it."""
+    p = nova_run.Program("""func.func @f(%a: tensor<8x8xf32>, %x: tensor<8x8xf32>) -> (tensor<8x8xf32>, tensor<8x8xf32>) {
+      %z = arith.constant 0.000000e+00 : f32
+      %f = linalg.fill ins(%z : f32) outs(%x : tensor<8x8xf32>) -> tensor<8x8xf32>
+      %r1 = linalg.matmul ins(%a, %a : tensor<8x8xf32>, tensor<8x8xf32>) outs(%f : tensor<8x8xf32>) -> tensor<8x8xf32>
+      %r2 = nova.matmul %x, %a : tensor<8x8xf32>, tensor<8x8xf32>
+      return %r1, %r2 : tensor<8x8xf32>, tensor<8x8xf32>
+    }""")
+    outs = _gemm_outputs(p.plan("f"))
+    assert len(outs) == 2 and 1 not in outs and outs[0] != outs[1]   # b1 is %x
+
+
+def test_sole_fill_user_writes_the_empty_buffer_in_place():
+    p = prog("batch_matmul_bf16.mlir")
+    plan = p.plan("bmm")
+    assert _gemm_outputs(plan) == [2]     # b0, b1 arguments; b2 the tensor.empty
+
+
+def test_narrow_accumulators():
+    """An f16 x f16 nova.matmul (result f16, NovaOps.cpp:1198) and a linalg
+    matmul with bf16 ins and outs accumulate in the narrow type; a bf16 x
+    bf16 nova.matmul (f16 result through a bf16 -> f16 cast) is refused."""
+    p = nova_run.Program("""func.func @h(%a: tensor<8x16xf16>, %b: tensor<16x4xf16>) -> tensor<8x4xf16> {
+      %r = nova.matmul %a, %b : tensor<8x16xf16>, tensor<16x4xf16>
+      return %r : tensor<8x4xf16>
+    }
+    func.func @l(%a: tensor<8x16xbf16>, %b: tensor<16x4xbf16>) -> tensor<8x4xbf16> {
+      %z = arith.constant 0.000000e+00 : bf16
+      %e = tensor.empty() : tensor<8x4xbf16>
+      %f = linalg.fill ins(%z : bf16) outs(%e : tensor<8x4xbf16>) -> tensor<8x4xbf16>
+      %r = linalg.matmul ins(%a, %b : tensor<8x16xbf16>, tensor<16x4xbf16>) outs(%f : tensor<8x4xbf16>) -> tensor<8x4xbf16>
+      return %r : tensor<8x4xbf16>
+    }
+    func.func @lin(%x: tensor<8x16xf16>, %w: tensor<16x4xf16>, %b: tensor<4xf16>) -> tensor<8x4xf16> {
+      %y = nova.linear %x, %w, %b : tensor<8x16xf16>, tensor<16x4xf16>, tensor<4xf16>
+      return %y : tensor<8x4xf16>
+    }
+    func.func @m(%a: tensor<8x16xbf16>, %b: tensor<16x4xbf16>) -> tensor<8x4xf16> {
+      %r = nova.matmul %a, %b : tensor<8x16xbf16>, tensor<16x4xbf16>
+      return %r : tensor<8x4xf16>
+    }""")
+    assert "accumulate=f16" in p.plan("h")
+    assert "accumulate=bf16" in p.plan("l")
+    assert "accumulate=f16" in p.plan("lin") and "epilogue=bias" in p.plan("lin")
+    with pytest.raises(nova_run.NovaRunError, match="bf16 -> f16 element cast"):
+        p.plan("m")
+    # the f32-accumulate forms are unchanged
+    b = prog("batch_matmul_bf16.mlir")
+    assert "accumulate=" not in b.plan("bmm") and "accumulate=" not in b.plan("bmm_nova")
