@@ -234,6 +234,21 @@ int32_t _mlir_ciface_nova_hip_sce_f32(const NovaMemRef2D *logits,
                                       NovaMemRef1D *loss,
                                       NovaMemRef2D *softmax);
 
+/* _mlir_ciface_nova_hip_sce_f32 for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same arguments,
+ * kernels and results; the per-row losses go to a static array the library
+ * holds per GPU for the life of the process (SCE_NOALLOC_MAX_ROWS floats,
+ * 1 MiB) instead of a hipMalloc'd workspace, and the call makes no
+ * allocation.  More than SCE_NOALLOC_MAX_ROWS rows: NOVA_HIP_ERANGE.
+ * Calls on one GPU share the array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller. */
+#define SCE_NOALLOC_MAX_ROWS 262144
+int32_t _mlir_ciface_nova_hip_sce_f32_noalloc(const NovaMemRef2D *logits,
+                                              const NovaMemRef1D *labels,
+                                              NovaMemRef1D *loss,
+                                              NovaMemRef2D *softmax);
+
 /* nova.sce forward and nova.sce_backward fused: the loss as
  * _mlir_ciface_nova_hip_sce_f32 computes it, and grad [R, C] f32 =
  * (softmax - onehot(labels)) * f32(1/R), bit-identical to feeding this

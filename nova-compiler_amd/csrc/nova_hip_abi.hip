@@ -280,7 +280,8 @@ int32_t backward_flags(int32_t flags, int &in_dt, int &out_dt, const char *what)
 // Shared validation of the SCE forward entry points (optional softmax and
 // fused gradient outputs).
 int32_t sce_common(const NovaMemRef2D *logits, const NovaMemRef1D *labels, NovaMemRef1D *loss,
-                   NovaMemRef2D *softmax, NovaMemRef2D *grad, const char *what) {
+                   NovaMemRef2D *softmax, NovaMemRef2D *grad, const char *what,
+                   bool noalloc = false) {
   clear_error();
   if (!logits || !labels || !loss) return fail(NOVA_HIP_EINVAL, "%s: null descriptor", what);
   const int64_t R = logits->sizes[0], C = logits->sizes[1];
@@ -312,7 +313,7 @@ int32_t sce_common(const NovaMemRef2D *logits, const NovaMemRef1D *labels, NovaM
   p.sx = logits->strides[0];
   p.ssm = softmax ? softmax->strides[0] : 0;
   p.sg = grad ? grad->strides[0] : 0;
-  return launch_sce(p, current_stream());
+  return noalloc ? launch_sce_noalloc(p, current_stream()) : launch_sce(p, current_stream());
 }
 
 template <typename D>
@@ -434,6 +435,12 @@ int32_t _mlir_ciface_nova_hip_layer_norm_f32(const NovaMemRef2D *x, const NovaMe
 int32_t _mlir_ciface_nova_hip_sce_f32(const NovaMemRef2D *logits, const NovaMemRef1D *labels,
                                       NovaMemRef1D *loss, NovaMemRef2D *softmax) {
   return sce_common(logits, labels, loss, softmax, nullptr, "sce");
+}
+
+int32_t _mlir_ciface_nova_hip_sce_f32_noalloc(const NovaMemRef2D *logits,
+                                              const NovaMemRef1D *labels, NovaMemRef1D *loss,
+                                              NovaMemRef2D *softmax) {
+  return sce_common(logits, labels, loss, softmax, nullptr, "sce_noalloc", true);
 }
 
 int32_t _mlir_ciface_nova_hip_sce_fwd_bwd_f32(const NovaMemRef2D *logits,

@@ -72,6 +72,9 @@ struct SceProblem {
   int64_t sx, ssm, sg;  // row strides (elements)
 };
 int32_t launch_sce(const SceProblem &p, hipStream_t s);
+// The same with the row losses in the library's static per-device array
+// (rows <= SCE_NOALLOC_MAX_ROWS): no allocation.
+int32_t launch_sce_noalloc(const SceProblem &p, hipStream_t s);
 
 // ---- backward (backward.hip) ------------------------------------------------
 struct SceBackwardProblem {

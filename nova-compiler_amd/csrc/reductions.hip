@@ -11,6 +11,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "nova_hip_internal.h"
 
 namespace nova_hip {
@@ -489,12 +491,9 @@ int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
   return check_hip(hipGetLastError(), "layer_norm launch");
 }
 
-int32_t launch_sce(const SceProblem &p, hipStream_t s) {
-  if (p.rows > 0x7fffffff - kWaves || p.C > 0x7fffffff)
-    return fail(NOVA_HIP_ERANGE, "sce: size exceeds 2^31-1");
-  // Workspace: the per-row losses.
-  float *ws = static_cast<float *>(workspace(s, (size_t)p.rows * 4 + 4));
-  if (!ws) return NOVA_HIP_ENOMEM;
+namespace {
+// Row kernels then the mean, with the per-row losses in ws[0, rows).
+int32_t launch_sce_into(const SceProblem &p, float *ws, hipStream_t s) {
   SceArgs a;
   a.logits = p.logits;
   a.labels = p.labels;
@@ -533,6 +532,58 @@ int32_t launch_sce(const SceProblem &p, hipStream_t s) {
   // division by the element count gives.
   hipLaunchKernelGGL(sce_mean_kernel, dim3(1), dim3(64), 0, s, a.row_loss, a.rows, a.loss);
   return check_hip(hipGetLastError(), "sce mean launch");
+}
+
+// Row losses of the entry point that allocates nothing: one array per GPU,
+// held until the process ends, shared by every call on that GPU (calls
+// that overlap on one GPU race on it).  Every row's loss is written before
+// the mean reads it, so nothing needs clearing between calls.  In host
+// code `scratch` names a host-side stand-in: kernels get the device
+// address from hipGetSymbolAddress, looked up once per device.
+constexpr int64_t kScratchRows = SCE_NOALLOC_MAX_ROWS;
+static __device__ __align__(256) float scratch[kScratchRows];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxDevices] = {nullptr};
+
+int32_t scratch_of_device(float **out) {
+  int dev = -1;
+  int32_t rc = check_hip(hipGetDevice(&dev), "sce_noalloc: hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(NOVA_HIP_EDEVICE, "sce_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
+                   "sce_noalloc: hipGetSymbolAddress(scratch)");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = static_cast<float *>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return NOVA_HIP_SUCCESS;
+}
+}  // namespace
+
+int32_t launch_sce(const SceProblem &p, hipStream_t s) {
+  if (p.rows > 0x7fffffff - kWaves || p.C > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "sce: size exceeds 2^31-1");
+  // Workspace: the per-row losses.
+  float *ws = static_cast<float *>(workspace(s, (size_t)p.rows * 4 + 4));
+  if (!ws) return NOVA_HIP_ENOMEM;
+  return launch_sce_into(p, ws, s);
+}
+
+int32_t launch_sce_noalloc(const SceProblem &p, hipStream_t s) {
+  if (p.rows > kScratchRows)
+    return fail(NOVA_HIP_ERANGE, "sce_noalloc: %lld rows exceed the scratch maximum of %lld",
+                (long long)p.rows, (long long)kScratchRows);
+  if (p.C > 0x7fffffff) return fail(NOVA_HIP_ERANGE, "sce: size exceeds 2^31-1");
+  float *ws = nullptr;
+  int32_t rc = scratch_of_device(&ws);
+  if (rc) return rc;
+  return launch_sce_into(p, ws, s);
 }
 
 }  // namespace nova_hip

@@ -47,6 +47,7 @@ EXPORTS = (
     "_mlir_ciface_nova_hip_linear_bf16_bias_gelu",
     "_mlir_ciface_nova_hip_layer_norm_f32",
     "_mlir_ciface_nova_hip_sce_f32",
+    "_mlir_ciface_nova_hip_sce_f32_noalloc",
     "_mlir_ciface_nova_hip_sce_fwd_bwd_f32",
     "_mlir_ciface_nova_hip_sce_backward_f32",
     "_mlir_ciface_nova_hip_layer_norm_backward_f32",
@@ -291,16 +292,21 @@ def layer_norm(x, gamma, beta, eps: float = 1e-5, *, y=None, mean_sum=None, rstd
     return y.reshape(shape), mean_sum.reshape(shape[:-1]), rstd.reshape(shape[:-1])
 
 
-def sce(logits, labels, *, softmax: bool = False, loss=None):
-    """nova.sce: returns (softmax or None, loss[1])."""
+def sce(logits, labels, *, softmax: bool = False, loss=None, noalloc: bool = False, sm=None):
+    """nova.sce: returns (softmax or None, loss[1]).  ``noalloc``: through
+    _mlir_ciface_nova_hip_sce_f32_noalloc (row losses in the library's static
+    per-GPU array; at most SCE_NOALLOC_MAX_ROWS rows)."""
     torch = _torch()
     if loss is None:
         loss = torch.empty(1, dtype=torch.float32, device=logits.device)
-    sm = torch.empty_like(logits) if softmax else None
+    if sm is None and softmax:
+        sm = torch.empty_like(logits)
     dl, dt, dloss = memref_of(logits), memref_of(labels), memref_of(loss)
     dsm = memref_of(sm) if sm is not None else None
     _bind_stream()
-    check(lib()._mlir_ciface_nova_hip_sce_f32(ref(dl), ref(dt), ref(dloss), ref(dsm)))
+    fn = (lib()._mlir_ciface_nova_hip_sce_f32_noalloc if noalloc
+          else lib()._mlir_ciface_nova_hip_sce_f32)
+    check(fn(ref(dl), ref(dt), ref(dloss), ref(dsm)))
     return sm, loss
 
 

@@ -177,6 +177,17 @@ def test_sce_validation():
     assert sce_rc(d2((4, 0)), d1(4), d1(1)) == 2
 
 
+def test_sce_noalloc_validation_and_row_limit():
+    """The entry point that allocates nothing validates like sce_f32 and
+    refuses more rows than its static array holds, before any HIP call."""
+    L = nh.lib()
+    f = L._mlir_ciface_nova_hip_sce_f32_noalloc
+    assert f(nh.ref(d2((4, 10))), nh.ref(d1(3)), nh.ref(d1(1)), None) == 2
+    rows = 262144 + 1   # SCE_NOALLOC_MAX_ROWS + 1
+    assert f(nh.ref(d2((rows, 10))), nh.ref(d1(rows)), nh.ref(d1(1)), None) == 5
+    assert "scratch maximum of 262144" in last_error()
+
+
 def test_error_text_is_per_call():
     assert gemm_rc(d3((2, 8, 16)), d3((2, 15, 8)), d3((2, 8, 8))) == 2
     assert last_error()
