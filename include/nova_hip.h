@@ -124,6 +124,15 @@ enum {
  * bf16 / f16 inputs accumulate in f32 (the MFMA kernels). */
 #define NOVA_HIP_GEMM_ACC_OUT 0x10000
 
+/* flags bit 17: f32 operands on the f32 matrix cores (v_mfma_f32_32x32x2_f32)
+ * instead of the exact kernel.  Products are exact and sums f32, but in the
+ * MFMA's and the tile loop's order, not the reference's sequential k: the
+ * result is within the f32 parity bar (1e-4 relative), not bit-identical to
+ * Nova's CPU pipeline.  Same results on every run.  f32 in and out; the
+ * epilogues as for the other kernels.  Also accepted by the backward GEMM
+ * entry points. */
+#define NOVA_HIP_GEMM_F32_MFMA 0x20000
+
 /* ------------------------------------------------------------------------
  * GEMM family.
  *

@@ -103,7 +103,7 @@ bool nonneg_sizes(const D *d, int rank) {
 }
 
 int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt) {
-  if (flags & ~(0xffff | NOVA_HIP_GEMM_ACC_OUT))
+  if (flags & ~(0xffff | NOVA_HIP_GEMM_ACC_OUT | NOVA_HIP_GEMM_F32_MFMA))
     return fail(NOVA_HIP_EINVAL, "gemm: unknown flag bits 0x%x", flags);
   in_dt = flags & 0xf;
   out_dt = (flags >> 4) & 0xf;
@@ -114,6 +114,8 @@ int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt)
     return fail(NOVA_HIP_EDTYPE, "gemm: bad dtype/epilogue code in flags 0x%x", flags);
   if (in_dt == NOVA_HIP_DT_F32 && out_dt != NOVA_HIP_DT_F32)
     return fail(NOVA_HIP_EDTYPE, "gemm: f32 inputs produce f32 output only");
+  if ((flags & NOVA_HIP_GEMM_F32_MFMA) && (in_dt != NOVA_HIP_DT_F32 || (flags & NOVA_HIP_GEMM_ACC_OUT)))
+    return fail(NOVA_HIP_EDTYPE, "gemm: the f32 MFMA form takes f32 operands");
   if (flags & NOVA_HIP_GEMM_ACC_OUT) {
     if (in_dt == NOVA_HIP_DT_F32 || out_dt != in_dt)
       return fail(NOVA_HIP_EDTYPE,
@@ -171,6 +173,7 @@ int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
   p.epi = epi;
   p.bias_dt = bias_dt;
   p.acc_out = (flags & NOVA_HIP_GEMM_ACC_OUT) != 0;
+  p.f32_mfma = (flags & NOVA_HIP_GEMM_F32_MFMA) != 0;
   const int esz = dtype_size(in_dt);
   const int osz = dtype_size(out_dt);
   p.A = data_of(A) + A->offset * esz;
@@ -218,6 +221,12 @@ int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
   if (empty) return NOVA_HIP_SUCCESS;
 
   hipStream_t s = current_stream();
+  if (p.f32_mfma) {
+    // An operand slice beyond the 32-bit buffer range takes the exact kernel.
+    rc = launch_gemm_f32_mfma(p, s);
+    if (rc != NOVA_HIP_ERANGE) return rc;
+    clear_error();
+  }
   return (in_dt == NOVA_HIP_DT_F32 || p.acc_out) ? launch_gemm_exact(p, s) : launch_gemm_mfma(p, s);
 }
 

@@ -40,6 +40,7 @@ struct GemmProblem {
   bool a_kcontig, b_kcontig;
   int in_dt, out_dt, bias_dt, epi;
   bool acc_out;  // accumulate in the output dtype (NOVA_HIP_GEMM_ACC_OUT)
+  bool f32_mfma;  // f32 on the matrix cores (NOVA_HIP_GEMM_F32_MFMA)
 };
 
 // Launch the MFMA kernels (bf16/f16 in).  Returns a NOVA_HIP_* status.
@@ -47,6 +48,9 @@ int32_t launch_gemm_mfma(const GemmProblem &p, hipStream_t s);
 // Launch the exact kernel: f32 in and out, or (acc_out) bf16 / f16 in and
 // out with the accumulator in that type.
 int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s);
+// f32 in and out on the f32 MFMA (NOVA_HIP_GEMM_F32_MFMA): within the f32
+// parity bar, not bit-identical to the sequential-k reference arithmetic.
+int32_t launch_gemm_f32_mfma(const GemmProblem &p, hipStream_t s);
 
 // ---- reductions ------------------------------------------------------------
 struct LayerNormProblem {

@@ -71,6 +71,7 @@ EXPORTS = (
 
 
 GEMM_ACC_OUT = 0x10000  # NOVA_HIP_GEMM_ACC_OUT
+GEMM_F32_MFMA = 0x20000  # NOVA_HIP_GEMM_F32_MFMA
 
 
 def gemm_flags(in_dt: int, out_dt: int, epi: int = EPI_NONE, bias_dt: int = 0) -> int:
@@ -220,13 +221,15 @@ def _as3(t):
 
 
 def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None,
-         acc_out: bool = False):
+         acc_out: bool = False, f32_mfma: bool = False):
     """Batched GEMM through _mlir_ciface_nova_hip_gemm.
 
     A [Bt,M,K] or [M,K]; B [Bt,K,N] or [K,N] (any unit-stride layout,
     transposed views included); returns C [Bt,M,N] (or [M,N] for rank-2
     inputs) in ``out_dtype`` (f32 by default).  ``acc_out``: accumulate in
     the output dtype (NOVA_HIP_GEMM_ACC_OUT; bf16 / f16 in and out).
+    ``f32_mfma``: f32 operands on the f32 matrix cores (NOVA_HIP_GEMM_F32_MFMA;
+    within 1e-4, not bit-identical to the sequential-k reference).
     """
     torch = _torch()
     in_dt = _dt(A)
@@ -244,7 +247,8 @@ def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None,
         od = _dt(out)
         C3 = _as3(out)
     bias_dt = _dt(bias) if bias is not None else 0
-    flags = gemm_flags(in_dt, od, epilogue, bias_dt) | (GEMM_ACC_OUT if acc_out else 0)
+    flags = (gemm_flags(in_dt, od, epilogue, bias_dt) | (GEMM_ACC_OUT if acc_out else 0)
+             | (GEMM_F32_MFMA if f32_mfma else 0))
     dA, dB, dC = memref_of(A3), memref_of(B3), memref_of(C3)
     dbias = memref_of(bias) if bias is not None else None
     _bind_stream()
@@ -364,7 +368,7 @@ def layer_norm_backward(grad_y, x, gamma, mean_sum, rstd, *, dx=None, dgamma=Non
 
 
 def linear_backward(grad_out, x, weight, *, out_dtype=None, grad_input=None, grad_weight=None,
-                    grad_bias=None, want=(True, True, True)):
+                    grad_bias=None, want=(True, True, True), f32_mfma: bool = False):
     """nova.linear_backward for weight [K, N]: returns (grad_input [M,K],
     grad_weight [K,N], grad_bias [N]).  ``grad_weight`` may be passed as a
     transposed view of a row-major [N, K] tensor."""
@@ -377,7 +381,7 @@ def linear_backward(grad_out, x, weight, *, out_dtype=None, grad_input=None, gra
         grad_weight = torch.empty((K, N), dtype=od, device=x.device)
     if grad_bias is None and want[2]:
         grad_bias = torch.empty(N, dtype=od, device=x.device)
-    flags = gemm_flags(_dt(x), _dt(torch.empty(0, dtype=od)))
+    flags = gemm_flags(_dt(x), _dt(torch.empty(0, dtype=od))) | (GEMM_F32_MFMA if f32_mfma else 0)
     d = [memref_of(t) if t is not None else None
          for t in (grad_out, x, weight, grad_input, grad_weight, grad_bias)]
     _bind_stream()
@@ -385,7 +389,8 @@ def linear_backward(grad_out, x, weight, *, out_dtype=None, grad_input=None, gra
     return grad_input, grad_weight, grad_bias
 
 
-def matmul_backward(grad, A, B, *, out_dtype=None, grad_a=None, grad_b=None):
+def matmul_backward(grad, A, B, *, out_dtype=None, grad_a=None, grad_b=None,
+                    f32_mfma: bool = False):
     """nova.matmul_backward (rank 2): returns (grad . B^T, A^T . grad)."""
     torch = _torch()
     od = out_dtype if out_dtype is not None else torch.float32
@@ -393,7 +398,7 @@ def matmul_backward(grad, A, B, *, out_dtype=None, grad_a=None, grad_b=None):
         grad_a = torch.empty(tuple(A.shape), dtype=od, device=A.device)
     if grad_b is None:
         grad_b = torch.empty(tuple(B.shape), dtype=od, device=A.device)
-    flags = gemm_flags(_dt(A), _dt(torch.empty(0, dtype=od)))
+    flags = gemm_flags(_dt(A), _dt(torch.empty(0, dtype=od))) | (GEMM_F32_MFMA if f32_mfma else 0)
     d = [memref_of(t) for t in (grad, A, B, grad_a, grad_b)]
     _bind_stream()
     check(lib()._mlir_ciface_nova_hip_matmul_backward(*[ref(v) for v in d], flags))

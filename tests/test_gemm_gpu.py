@@ -411,3 +411,66 @@ def test_gemm_narrow_accumulator_refuses_other_forms(cuda):
     with pytest.raises(nh.NovaHipError):
         nh.gemm(A, A.t().contiguous(), out_dtype=torch.bfloat16, acc_out=True,
                 epilogue=nh.EPI_GELU)
+
+
+# ------------------------------------------------ f32 on the matrix cores --
+# NOVA_HIP_GEMM_F32_MFMA: f32 products, f32 sums in the MFMA's order.  Bar:
+# the f32 one (rtol 1e-4, atol 1e-4 * max|c|), not bit-exactness.
+
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1), (2, 37, 45, 23), (1, 130, 129, 70),
+                                   (3, 128, 256, 96), (1, 200, 96, 4100), (1, 64, 384, 8192)])
+def test_f32_mfma_gemm_layouts(cuda, layout, shape):
+    batch, M, N, K = shape
+    A = S.uniform((batch, M, K), 95)
+    B = S.uniform((batch, K, N), 95, offset=A.size)
+    C = nh.gemm(view_as(A, layout[0], cuda, S.F32), view_as(B, layout[1], cuda, S.F32),
+                f32_mfma=True)
+    assert_close_f32(C.cpu().numpy(), ref.gemm(A, B), f"f32 mfma {layout} {shape}")
+
+
+@pytest.mark.parametrize("epi", [nh.EPI_BIAS, nh.EPI_BIAS_GELU, nh.EPI_GELU])
+@pytest.mark.parametrize("K", [96, 6144])
+def test_f32_mfma_gemm_epilogues(cuda, epi, K):
+    """Bias first (split 0 starts from it) and GELU after the split sum."""
+    M, N = 100, 200
+    A = S.normal((M, K), 96, 0, 0.05)
+    B = S.normal((K, N), 96, 0, 0.05, offset=A.size)
+    bias = S.normal((N,), 96, offset=A.size + B.size)
+    has_bias = epi != nh.EPI_GELU
+    C = nh.gemm(to_dev(A, S.F32, cuda), to_dev(B, S.F32, cuda),
+                bias=to_dev(bias, S.F32, cuda) if has_bias else None, epilogue=epi,
+                f32_mfma=True)
+    want = ref.gemm(A, B, bias=bias if has_bias else None, epilogue=epi)[0]
+    assert_close_f32(C.cpu().numpy(), want, f"f32 mfma epilogue {epi} K={K}")
+
+
+def test_f32_mfma_same_bits_every_run_and_unaligned_rows(cuda):
+    import torch
+    A = S.uniform((65, 3001), 97)
+    B = S.uniform((3001, 77), 97, offset=A.size)
+    dA, dB = to_dev(A, S.F32, cuda), to_dev(B, S.F32, cuda)
+    c1 = nh.gemm(dA, dB, f32_mfma=True)
+    c2 = nh.gemm(dA, dB, f32_mfma=True)
+    assert torch.equal(c1, c2)
+    assert_close_f32(c1.cpu().numpy(), ref.gemm(A, B)[0], "unaligned f32 mfma")
+    # an offset view: rows no longer 16-byte aligned
+    wide = S.uniform((40, 130), 98)
+    dW = to_dev(wide, S.F32, cuda)[:, 1:129]
+    Bs = S.uniform((128, 50), 98, offset=wide.size)
+    c = nh.gemm(dW, to_dev(Bs, S.F32, cuda), f32_mfma=True)
+    assert_close_f32(c.cpu().numpy(), ref.gemm(np.ascontiguousarray(wide[:, 1:129]), Bs)[0],
+                     "offset rows")
+
+
+def test_f32_mfma_backward_entry_points(cuda):
+    M, K, N = 300, 96, 200
+    x = S.normal((M, K), 99)
+    w = S.normal((K, N), 99, 0, 0.1, offset=x.size)
+    go = S.normal((M, N), 99, offset=x.size + w.size)
+    gi, gw, gb = nh.linear_backward(to_dev(go, S.F32, cuda), to_dev(x, S.F32, cuda),
+                                    to_dev(w, S.F32, cuda), f32_mfma=True)
+    gi_r, gw_r, gb_r = ref.linear_backward(go, x, w)
+    assert_close_f32(gi.cpu().numpy(), gi_r, "grad_input")
+    assert_close_f32(gw.cpu().numpy(), gw_r, "grad_weight")
+    assert_close_f32(gb.cpu().numpy(), gb_r, "grad_bias")
