@@ -349,14 +349,17 @@ def bench_copy(args, torch):
     return {"ms": ms, "bytes": 2 * n * 4, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
 
 
-def bench_gpt_step(args):
+def bench_gpt_step(args, torch):
     """A whole GPT training step (the reference GPT step's shapes: batch 8,
     1024 tokens, vocab 50304, width 384, MLP 1536; forward, SCE loss and the
-    full backward to the embedding gradients) through libnova_run, from host
-    arrays to host arrays: wall time per nova_run_execute, which includes
-    the host<->device copies of its ~0.25 GB of arguments and results (the
-    device buffers are allocated by the first, untimed execution and reused).
-    Weights random (N(0, 0.02)), so the loss is near ln(vocab)."""
+    full backward to the embedding gradients) through libnova_run.  Timed
+    with arguments and results resident in device memory
+    (nova_run_execute_device, the reference's address-space-1 contract),
+    once with the f32 GEMMs exact (bit-identical to the CPU pipeline) and
+    once on the f32 matrix cores (1e-4 bar); events around back-to-back
+    steps on the stream the launches go to.  The host-array form
+    (nova_run_execute, PCIe copies of ~0.25 GB included) is timed once for
+    comparison.  Weights random (N(0, 0.02)), so the loss is near ln(vocab)."""
     import numpy as np
     import nova_run
     from gpt_program import gpt_step
@@ -370,19 +373,33 @@ def bench_gpt_step(args):
            np.arange(T, dtype=np.int64).reshape(1, T), f(V, D), f(T, D), 1 + f(D), f(D), f(D, H),
            f(H), f(H, D), f(D), 1 + f(D), f(D), f(D, V)]
     p = nova_run.Program(gpt_step(B, T, V, D, H))
-    launches = p.plan("gpt_step").count("_mlir_ciface_")
-    out = p.run("gpt_step", *inp)
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        out = p.run("gpt_step", *inp)
-        times.append((time.perf_counter() - t0) * 1e3)
-    return {"ms_wall_median": sorted(times)[1], "ms_wall": times, "launches": launches,
-            "loss": float(out[0][0]), "ln_vocab": float(np.log(V)),
-            "finite": bool(all(np.isfinite(o).all() for o in out)),
-            "note": "wall time per nova_run_execute incl. host<->device copies (device "
-                    "buffers reused from the first, untimed execution); f32 program (the "
-                    "reference GPT step's dtype)"}
+    dev = [torch.from_numpy(a).cuda() for a in inp]
+    res = {"launches": None}
+    for mode, name in ((nova_run.F32_GEMM_EXACT, "exact"), (nova_run.F32_GEMM_MFMA, "mfma")):
+        p.set_f32_gemm(mode)
+        res["launches"] = p.plan("gpt_step").count("_mlir_ciface_")
+        out = p.run_device("gpt_step", *dev)        # untimed: allocates the intermediates
+        torch.cuda.synchronize()
+        reps = 5
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            p.run_device("gpt_step", *dev, results=out)
+        e1.record()
+        torch.cuda.synchronize()
+        res[f"ms_per_step_device_{name}"] = e0.elapsed_time(e1) / reps
+        res[f"loss_{name}"] = float(out[0][0].item())
+        res[f"finite_{name}"] = bool(all(torch.isfinite(o).all().item() for o in out))
+    p.set_f32_gemm(nova_run.F32_GEMM_MFMA)
+    p.run("gpt_step", *inp)
+    t0 = time.perf_counter()
+    p.run("gpt_step", *inp)
+    res["ms_wall_host_arrays_mfma"] = (time.perf_counter() - t0) * 1e3
+    res["ln_vocab"] = float(np.log(V))
+    res["note"] = ("device-resident arguments and results, events over back-to-back steps; "
+                   "f32 program (the reference GPT step's dtype); ms_wall_host_arrays includes "
+                   "the host<->device copies")
+    return res
 
 
 def cpu_baseline(S):
@@ -477,7 +494,7 @@ def main():
     if "c3_bwd" in only:
         cfg["c3_linear_backward_bf16_f32"] = stage("c3_bwd", lambda: bench_c3_bwd(args, torch, nh, S))
     if "gpt_step" in only:
-        cfg["gpt_step_f32_nova_run_8x1024_v50304"] = stage("gpt_step", lambda: bench_gpt_step(args))
+        cfg["gpt_step_f32_nova_run_8x1024_v50304"] = stage("gpt_step", lambda: bench_gpt_step(args, torch))
     if "c2_vendor" in only:
         cfg["c2_vendor_hipblaslt_reference"] = stage("c2_vendor", lambda: bench_c2_vendor(args, torch, S))
     if "copy" in only:  # calibration only; not part of the default run

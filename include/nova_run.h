@@ -63,6 +63,29 @@ int32_t nova_run_plan(const NovaRunProgram *p, const char *func, char *buf, size
 int32_t nova_run_execute(const NovaRunProgram *p, const char *func, const void *const *host_args,
                          void *const *host_results);
 
+/* The reference's compiled entry points take memref arguments in address
+ * space 1: device memory the caller allocated (ltest/test_gpu.mlir:2,
+ * robust_driver.cpp:17-39, the packed _mlir_ciface_main(result, args) form
+ * of GenerateDynamicWrapper.cpp:61-95).  This is that contract: dev_args[i]
+ * is argument i's dense row-major data in device memory (a writable memref
+ * argument is written in place), dev_results[i] device memory with room for
+ * result i, which receives it.  Nothing is copied to or from the host;
+ * launches are queued on the calling thread's libnova_hip stream and the
+ * call returns without synchronising (nova_hip_synchronize waits).
+ * Intermediates live in device buffers the program keeps and reuses on the
+ * next execution, as for nova_run_execute. */
+int32_t nova_run_execute_device(const NovaRunProgram *p, const char *func,
+                                void *const *dev_args, void *const *dev_results);
+
+/* How f32 GEMMs (nova.matmul / nova.linear / linalg.matmul on f32 and their
+ * backward ops) are planned.  EXACT (the default): sequential k with
+ * separately rounded multiply and add, bit-identical to Nova's CPU pipeline
+ * (Pipeline.cpp:61-187).  MFMA: the f32 matrix cores
+ * (NOVA_HIP_GEMM_F32_MFMA of nova_hip.h), within the f32 parity bar (1e-4
+ * relative) but not bit-identical, several times faster. */
+enum { NOVA_RUN_F32_GEMM_EXACT = 0, NOVA_RUN_F32_GEMM_MFMA = 1 };
+int32_t nova_run_set_f32_gemm(NovaRunProgram *p, int32_t mode);
+
 #ifdef __cplusplus
 }
 #endif

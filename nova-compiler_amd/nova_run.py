@@ -21,7 +21,19 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libnova_run.so")
 NP_DTYPE = {0: np.float32, 1: np.uint16, 2: np.uint16, 3: np.int32, 4: np.int64, 5: np.int16}
-DT_NAME = {0: "f32", 1: "bf16", 2: "f16", 3: "i32", 4: "i64"}
+DT_NAME = {0: "f32", 1: "bf16", 2: "f16", 3: "i32", 4: "i64", 5: "i16"}
+F32_GEMM_EXACT, F32_GEMM_MFMA = 0, 1  # nova_run_set_f32_gemm modes
+
+
+class _TorchDtypes(dict):
+    def __missing__(self, dt):
+        import torch
+        self.update({0: torch.float32, 1: torch.bfloat16, 2: torch.float16, 3: torch.int32,
+                     4: torch.int64, 5: torch.int16})
+        return self[dt]
+
+
+TORCH_DTYPE = _TorchDtypes()
 
 _lib = None
 
@@ -56,6 +68,10 @@ def lib() -> ctypes.CDLL:
         L.nova_run_plan.restype = I32
         L.nova_run_execute.argtypes = [P, S, ctypes.POINTER(P), ctypes.POINTER(P)]
         L.nova_run_execute.restype = I32
+        L.nova_run_execute_device.argtypes = [P, S, ctypes.POINTER(P), ctypes.POINTER(P)]
+        L.nova_run_execute_device.restype = I32
+        L.nova_run_set_f32_gemm.argtypes = [P, I32]
+        L.nova_run_set_f32_gemm.restype = I32
         _lib = L
     return _lib
 
@@ -104,6 +120,37 @@ class Program:
         if lib().nova_run_plan(self._p, func.encode(), buf, len(buf)):
             _err(f"@{func}")
         return buf.value.decode()
+
+    def set_f32_gemm(self, mode: int) -> None:
+        """F32_GEMM_EXACT (bit-identical to the reference's CPU arithmetic) or
+        F32_GEMM_MFMA (the f32 matrix cores, within 1e-4)."""
+        if lib().nova_run_set_f32_gemm(self._p, mode):
+            _err("set_f32_gemm")
+
+    def run_device(self, func: str, *tensors, results=None):
+        """Run `func` on torch device tensors through nova_run_execute_device:
+        no host copies, launches queued on torch's current stream, no
+        synchronisation.  Returns the result tensors (allocated here unless
+        ``results`` gives them)."""
+        import torch
+        import nova_hip
+        spec = self.args(func)
+        if len(tensors) != len(spec):
+            raise ValueError(f"@{func} takes {len(spec)} arguments, got {len(tensors)}")
+        for t, (dt, shape) in zip(tensors, spec):
+            if (tuple(t.shape) != shape or t.dtype != TORCH_DTYPE[dt] or not t.is_contiguous()
+                    or not t.is_cuda):
+                raise ValueError(f"argument needs a contiguous {DT_NAME[dt]} device tensor "
+                                 f"of shape {shape}")
+        if results is None:
+            results = [torch.empty(shape, dtype=TORCH_DTYPE[dt], device=tensors[0].device)
+                       for dt, shape in self.results(func)]
+        nova_hip._bind_stream()
+        pin = (ctypes.c_void_p * max(len(tensors), 1))(*[t.data_ptr() for t in tensors])
+        pout = (ctypes.c_void_p * max(len(results), 1))(*[r.data_ptr() for r in results])
+        if lib().nova_run_execute_device(self._p, func.encode(), pin, pout):
+            _err(f"@{func}")
+        return results
 
     def run(self, func: str, *arrays):
         """Run `func` on host arrays; returns its results as numpy arrays.

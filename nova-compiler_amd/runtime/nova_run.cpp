@@ -658,6 +658,7 @@ struct Step {
   float value = 0.0f;           // fill value
   int64_t dims[3] = {0, 0, 0};  // reduce_sum: outer, reduced, inner
   bool acc_out = false;         // GEMM accumulating in its bf16 / f16 output dtype
+  bool f32_mfma = false;        // f32 GEMM on the matrix cores (NOVA_HIP_GEMM_F32_MFMA)
 };
 
 int64_t numel_of(const std::vector<int64_t> &shape) {
@@ -702,8 +703,10 @@ struct Planner {
   std::map<std::string, int> uses;
   std::map<std::string, std::string> consts;
   std::set<int> empty_bufs;  // buffers of tensor.empty results
+  std::set<std::string> ones;  // splat 1.0 constants whose every use is an identity multiply
+  bool f32_mfma = false;       // plan f32 GEMMs onto the matrix cores
 
-  explicit Planner(const Func &fn) : f(fn) {}
+  explicit Planner(const Func &fn, bool mfma = false) : f(fn), f32_mfma(mfma) {}
 
   int new_buf(const Type &t, int arg = -1) {
     Buffer b;
@@ -770,6 +773,30 @@ struct Planner {
     return nullptr;
   }
 
+  // Every use of `name` (from op index `from` on) is a nova.mul whose other
+  // operand is an f32 value of the result's shape (so the multiply by a
+  // broadcast splat leaves it unchanged), and it is not returned.
+  bool identity_muls_only(const std::string &name, size_t from) {
+    if (uses[name] == 0) return false;
+    for (const std::string &r : f.rets)
+      if (r == name) return false;
+    int seen = 0;
+    for (size_t k = from; k < f.ops.size(); ++k) {
+      const Op &o = f.ops[k];
+      for (size_t i = 0; i < o.operands.size(); ++i) {
+        if (o.operands[i] != name) continue;
+        if (o.name != "nova.mul" || o.operands.size() != 2 || o.operands[0] == o.operands[1])
+          return false;
+        const size_t other = 1 - i;
+        if (other >= o.operand_types.size() || o.result_types.empty()) return false;
+        const Type &ot = o.operand_types[other];
+        if (ot.dt != DT_F32 || ot.shape != o.result_types[0].shape) return false;
+        ++seen;
+      }
+    }
+    return seen == uses[name];
+  }
+
   // A GEMM-family step writing `out` (reusing its buffer when it has one of
   // the output dtype, as a linalg init does); then folds of a following
   // gelu / narrowing cast.
@@ -808,6 +835,7 @@ struct Planner {
     s.epi = bias ? NOVA_HIP_EPI_BIAS : NOVA_HIP_EPI_NONE;
     s.out_dt = out.dt;
     s.acc_out = narrow;
+    s.f32_mfma = f32_mfma && a.dt == DT_F32;
     std::string name = op.results[0];
     std::string fused = op.name;
     // (GELU and casts fold only into an f32 accumulator.)
@@ -839,6 +867,7 @@ struct Planner {
              : s.epi == NOVA_HIP_EPI_BIAS_GELU ? "bias+gelu" : "gelu");
     s.text = buf;
     if (narrow) s.text += std::string(" accumulate=") + dt_name(out.dt);
+    if (s.f32_mfma) s.text += " f32=mfma";
     plan.steps.push_back(s);
     env[op.results[0]] = out;
     env[name] = out;
@@ -963,6 +992,14 @@ struct Planner {
                  ", " + view_str(x) + ") -> " + view_str(s.out[0]);
         env[op.results[0]] = s.out[0];
         plan.steps.push_back(s);
+      } else if (n == "nova.mul" && (ones.count(op.operands[0]) || ones.count(op.operands[1]))) {
+        const size_t keep = ones.count(op.operands[0]) ? 1 : 0;
+        View v;
+        if ((rc = get(op, keep, v))) return rc;
+        v.producer = -1;
+        env[op.results[0]] = v;
+        plan.steps.push_back(Step{"view", {}, {}, 0, 0,
+                                  "nova.mul by splat 1.0 -> view " + view_str(v)});
       } else if (n == "nova.add" || n == "nova.sub" || n == "nova.mul" || n == "nova.div") {
         View a, b;
         if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = need_dense_f32(op, a, "lhs")) ||
@@ -990,10 +1027,25 @@ struct Planner {
         if (t.dt != DT_F32)
           return fail(NOVA_HIP_EDTYPE, "line %d: nova.constant of %s is not on this path", op.line,
                       dt_name(t.dt));
+        const float value = strtof(v.c_str() + 6, nullptr);
+        // x * 1.0 == x for every f32 x: a splat 1.0 whose every use is a
+        // nova.mul that leaves the other operand's shape unchanged needs
+        // neither the fill nor the multiplies (each becomes a view).
+        if (value == 1.0f && identity_muls_only(op.results[0], k + 1)) {
+          ones.insert(op.results[0]);
+          View one;
+          one.shape = t.shape;
+          one.strides = dense_strides(t.shape);
+          one.dt = one.logical = DT_F32;
+          env[op.results[0]] = one;  // never read: no buffer
+          plan.steps.push_back(Step{"view", {}, {}, 0, 0,
+                                    "nova.constant splat 1 -> elided (identity multiplies only)"});
+          continue;
+        }
         Step s;
         s.kind = "fill";
         s.out = {fresh(t)};
-        s.value = strtof(v.c_str() + 6, nullptr);
+        s.value = value;
         char buf[64];
         snprintf(buf, sizeof(buf), "%g", (double)s.value);
         s.text = std::string("nova.constant splat ") + buf + " -> _mlir_ciface_nova_hip_fill_f32(" +
@@ -1143,6 +1195,27 @@ struct Planner {
         View x, t;
         if ((rc = get(op, 0, x)) || (rc = get(op, 1, t))) return rc;
         if ((rc = need_f32(op, x, "logits")) || (rc = as_i32(op, t))) return rc;
+        // nova.sce whose softmax feeds only a nova.sce_backward over the same
+        // labels: one fused launch writes the loss and the gradient, and the
+        // softmax is never materialised.
+        const Op *bw = op.results[0].empty() ? nullptr : sole_user(op.results[0], k + 1);
+        if (bw && bw->name == "nova.sce_backward" && bw->operands.size() == 2 &&
+            bw->operands[0] == op.results[0] && bw->operands[1] == op.operands[1] &&
+            (!bw->attrs.count("dim") || atoi(bw->attrs.at("dim").c_str()) == -1 ||
+             atoi(bw->attrs.at("dim").c_str()) == (int)x.shape.size() - 1)) {
+          Step s;
+          s.kind = "sce_fwd_bwd";
+          s.in = {x, t};
+          s.out = {fresh(bw->result_types[0]), fresh(op.result_types[1])};
+          s.text = "nova.sce + nova.sce_backward -> _mlir_ciface_nova_hip_sce_fwd_bwd_f32(" +
+                   view_str(x) + ", " + view_str(t) + ") -> " + view_str(s.out[0]) + ", " +
+                   view_str(s.out[1]) + " (softmax not materialised)";
+          folded.insert(bw);
+          env[bw->results[0]] = s.out[0];
+          env[op.results[1]] = s.out[1];
+          plan.steps.push_back(s);
+          continue;
+        }
         Step s;
         s.kind = "sce";
         s.in = {x, t};
@@ -1202,9 +1275,11 @@ struct Planner {
         s.in = {go, x, w};
         for (size_t r = 0; r < op.result_types.size(); ++r) s.out.push_back(fresh(op.result_types[r]));
         s.out_dt = op.result_types[0].dt;
+        s.f32_mfma = f32_mfma && x.dt == DT_F32;
         s.text = n + " -> _mlir_ciface_nova_hip_" + (lin ? "linear" : "matmul") + "_backward(" +
                  view_str(go) + ", " + view_str(x) + ", " + view_str(w) + ") -> ";
         for (size_t r = 0; r < s.out.size(); ++r) s.text += (r ? ", " : "") + view_str(s.out[r]);
+        if (s.f32_mfma) s.text += " f32=mfma";
         for (size_t r = 0; r < op.results.size() && r < s.out.size(); ++r) env[op.results[r]] = s.out[r];
         plan.steps.push_back(s);
       } else if (n == "bufferization.materialize_in_destination") {
@@ -1304,7 +1379,8 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
                                       reinterpret_cast<NovaMemRef3D *>(&C),
                                       reinterpret_cast<const NovaMemRef1D *>(pb),
                                       NOVA_HIP_GEMM_FLAGS(a.dt, s.out_dt, s.epi, bias_dt) |
-                                          (s.acc_out ? NOVA_HIP_GEMM_ACC_OUT : 0));
+                                          (s.acc_out ? NOVA_HIP_GEMM_ACC_OUT : 0) |
+                                          (s.f32_mfma ? NOVA_HIP_GEMM_F32_MFMA : 0));
   }
   if (s.kind == "layer_norm") {
     Desc<2> x = desc<2>(s.in[0], ptr), y = desc<2>(s.out[0], ptr);
@@ -1325,6 +1401,14 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
                                          reinterpret_cast<const NovaMemRef1D *>(&t),
                                          reinterpret_cast<NovaMemRef1D *>(&loss),
                                          has_sm ? reinterpret_cast<NovaMemRef2D *>(&sm) : nullptr);
+  }
+  if (s.kind == "sce_fwd_bwd") {
+    Desc<2> x = desc<2>(s.in[0], ptr), g = desc<2>(s.out[0], ptr);
+    Desc<1> t = desc<1>(s.in[1], ptr), loss = desc<1>(s.out[1], ptr);
+    return _mlir_ciface_nova_hip_sce_fwd_bwd_f32(reinterpret_cast<const NovaMemRef2D *>(&x),
+                                                 reinterpret_cast<const NovaMemRef1D *>(&t),
+                                                 reinterpret_cast<NovaMemRef1D *>(&loss),
+                                                 reinterpret_cast<NovaMemRef2D *>(&g));
   }
   if (s.kind == "sce_bwd") {
     Desc<2> sm = desc<2>(s.in[0], ptr), g = desc<2>(s.out[0], ptr);
@@ -1351,7 +1435,8 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
   if (s.kind == "lin_bwd" || s.kind == "mm_bwd") {
     Desc<2> go = desc<2>(s.in[0], ptr), x = desc<2>(s.in[1], ptr), w = desc<2>(s.in[2], ptr);
     Desc<2> o0 = desc<2>(s.out[0], ptr), o1 = desc<2>(s.out[1], ptr);
-    const int32_t flags = NOVA_HIP_GEMM_FLAGS(s.in[1].dt, s.out_dt, 0, 0);
+    const int32_t flags = NOVA_HIP_GEMM_FLAGS(s.in[1].dt, s.out_dt, 0, 0) |
+                          (s.f32_mfma ? NOVA_HIP_GEMM_F32_MFMA : 0);
     if (s.kind == "mm_bwd")
       return _mlir_ciface_nova_hip_matmul_backward(
           reinterpret_cast<const NovaMemRef2D *>(&go), reinterpret_cast<const NovaMemRef2D *>(&x),
@@ -1451,6 +1536,7 @@ struct NovaRunProgram {
   // over and over); freed by nova_run_free.
   mutable std::mutex mu;
   mutable std::map<std::string, std::vector<std::pair<void *, int64_t>>> buffers;
+  int f32_gemm = NOVA_RUN_F32_GEMM_EXACT;  // nova_run_set_f32_gemm
   const Func *find(const char *name) const {
     for (const Func &f : funcs)
       if (name && f.name == name) return &f;
@@ -1471,7 +1557,7 @@ int32_t plan_of(const NovaRunProgram *p, const char *func, Plan &out, const Func
   if (!p) return fail(NOVA_HIP_EINVAL, "null program");
   const Func *f = p->find(func);
   if (!f) return fail(NOVA_HIP_EINVAL, "no function @%s", func ? func : "(null)");
-  Planner pl(*f);
+  Planner pl(*f, p->f32_gemm == NOVA_RUN_F32_GEMM_MFMA);
   int32_t rc = pl.run();
   if (rc) return rc;
   out = pl.plan;
@@ -1524,6 +1610,16 @@ NovaRunProgram *nova_run_parse(const char *text_in) {
 }
 
 void nova_run_free(NovaRunProgram *p) { delete p; }
+
+int32_t nova_run_set_f32_gemm(NovaRunProgram *p, int32_t mode) {
+  t_err[0] = 0;
+  if (!p) return fail(NOVA_HIP_EINVAL, "null program");
+  if (mode != NOVA_RUN_F32_GEMM_EXACT && mode != NOVA_RUN_F32_GEMM_MFMA)
+    return fail(NOVA_HIP_EINVAL, "unknown f32 GEMM mode %d", mode);
+  std::lock_guard<std::mutex> lock(p->mu);
+  p->f32_gemm = mode;
+  return NOVA_HIP_SUCCESS;
+}
 
 const char *nova_run_last_error(void) { return t_err; }
 
@@ -1658,6 +1754,81 @@ int32_t nova_run_execute(const NovaRunProgram *p, const char *func, const void *
   const hipError_t e = hipStreamSynchronize(st);
   cleanup();
   return e == hipSuccess ? NOVA_HIP_SUCCESS : fail(NOVA_HIP_EDEVICE, "%s", hipGetErrorString(e));
+}
+
+int32_t nova_run_execute_device(const NovaRunProgram *p, const char *func,
+                                void *const *dev_args, void *const *dev_results) {
+  Plan pl;
+  const Func *f = nullptr;
+  int32_t rc = plan_of(p, func, pl, &f);
+  if (rc) return rc;
+  if ((!dev_args && !f->arg_types.empty()) || (!dev_results && !pl.results.empty()))
+    return fail(NOVA_HIP_EINVAL, "null argument or result array");
+  for (size_t i = 0; i < f->arg_types.size(); ++i)
+    if (!dev_args[i] && f->arg_types[i].numel() > 0)
+      return fail(NOVA_HIP_EINVAL, "argument %zu is a null pointer", i);
+  for (size_t i = 0; i < pl.results.size(); ++i)
+    if (!dev_results[i] && pl.bufs[pl.results[i].buf].bytes > 0)
+      return fail(NOVA_HIP_EINVAL, "result %zu is a null pointer", i);
+  hipStream_t st = static_cast<hipStream_t>(nova_hip_get_stream());
+  std::lock_guard<std::mutex> lock(p->mu);
+  const size_t nb = pl.bufs.size();
+  std::vector<void *> ptr(nb, nullptr);
+  std::vector<bool> used(nb, false), mine(nb, false);
+  for (const Step &s : pl.steps) {
+    for (const View &v : s.in) if (v.buf >= 0) used[v.buf] = true;
+    for (const View &v : s.out) if (v.buf >= 0) used[v.buf] = true;
+  }
+  // Arguments are the caller's device memory (writable memref arguments are
+  // written in place).  A result computed into a buffer of its own is
+  // computed straight into the caller's result memory; a result that is an
+  // argument, or a value returned twice, is copied there at the end.
+  for (size_t b = 0; b < nb; ++b)
+    if (pl.bufs[b].arg >= 0) ptr[b] = dev_args[pl.bufs[b].arg];
+  for (size_t i = 0; i < pl.results.size(); ++i) {
+    const int b = pl.results[i].buf;
+    if (pl.bufs[b].arg < 0 && !ptr[b]) ptr[b] = dev_results[i];
+  }
+  for (size_t b = 0; b < nb; ++b) mine[b] = used[b] && !ptr[b] && pl.bufs[b].bytes > 0;
+  // The program's own buffers, kept from the last device execution of this
+  // function while the plan's sizes match.
+  std::vector<std::pair<void *, int64_t>> &held = p->buffers[f->name + "#device"];
+  bool reuse = held.size() == nb;
+  for (size_t b = 0; reuse && b < nb; ++b)
+    reuse = held[b].second == (mine[b] ? pl.bufs[b].bytes : 0);
+  if (!reuse) {
+    (void)hipStreamSynchronize(st);
+    for (auto &h : held)
+      if (h.first) (void)hipFree(h.first);
+    held.assign(nb, {nullptr, 0});
+  }
+  for (size_t b = 0; b < nb; ++b) {
+    if (!mine[b]) continue;
+    if (!held[b].first) {
+      if (hipMalloc(&held[b].first, (size_t)pl.bufs[b].bytes) != hipSuccess) {
+        held[b].first = nullptr;
+        return fail(NOVA_HIP_ENOMEM, "hipMalloc of %lld bytes failed",
+                    (long long)pl.bufs[b].bytes);
+      }
+      held[b].second = pl.bufs[b].bytes;
+    }
+    ptr[b] = held[b].first;
+  }
+  for (const Step &s : pl.steps) {
+    if ((rc = run_step(s, ptr, st))) {
+      const std::string why = nova_hip_last_error();
+      if (why.size()) fail(rc, "%s: %s", s.text.c_str(), why.c_str());
+      return rc;
+    }
+  }
+  for (size_t i = 0; i < pl.results.size(); ++i) {
+    const View &v = pl.results[i];
+    if (ptr[v.buf] == dev_results[i] || pl.bufs[v.buf].bytes == 0) continue;
+    if (hipMemcpyAsync(dev_results[i], ptr[v.buf], (size_t)pl.bufs[v.buf].bytes,
+                       hipMemcpyDeviceToDevice, st) != hipSuccess)
+      return fail(NOVA_HIP_EDEVICE, "copy of result %zu failed", i);
+  }
+  return NOVA_HIP_SUCCESS;
 }
 
 }  // extern "C"

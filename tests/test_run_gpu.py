@@ -177,6 +177,70 @@ def test_gpt_step_program_end_to_end(cuda, B, T, V, D, H):
     assert (got[1][unused] == 0).all()
 
 
+@pytest.mark.parametrize("B,T,V,D,H", [(2, 16, 96, 64, 128), (1, 64, 50304, 64, 128)])
+def test_gpt_step_device_resident_f32_mfma(cuda, B, T, V, D, H):
+    """The same step through nova_run_execute_device (device-resident
+    arguments and results, no host copies) with the f32 GEMMs on the matrix
+    cores: every result within the f32 bar of the oracle; a second execution
+    into the same result tensors gives the same bits; the exact mode gives
+    what the host-array path gives."""
+    import torch
+    from gpt_program import gpt_step
+    r = np.random.default_rng(80)
+    f = lambda *s, k=0.1: (r.standard_normal(s) * k).astype(np.float32)  # noqa: E731
+    tok = r.integers(0, V, (B, T)).astype(np.int16)
+    tgt = r.integers(0, V, (B, T)).astype(np.int16)
+    pos = np.arange(T, dtype=np.int64).reshape(1, T)
+    args = [tok, tgt, pos, f(V, D, k=0.5), f(T, D, k=0.5), 1 + f(D), f(D), f(D, H), f(H),
+            f(H, D), f(D), 1 + f(D), f(D), f(D, V)]
+    p = nova_run.Program(gpt_step(B, T, V, D, H))
+    dev = [torch.from_numpy(a).to(cuda) for a in args]
+    want = gpt_step_oracle(*args)
+    names = ["loss", "dwte", "dwpe", "dgamma1", "dbeta1", "dw1", "db1", "dw2", "db2",
+             "dgamma2", "dbeta2", "dwlm"]
+    p.set_f32_gemm(nova_run.F32_GEMM_MFMA)
+    out = p.run_device("gpt_step", *dev)
+    torch.cuda.synchronize()
+    first = [o.clone() for o in out]
+    for g, w, n in zip(out, want, names):
+        assert_close_f32(g.cpu().numpy(), w, "device mfma " + n)
+    p.run_device("gpt_step", *dev, results=out)
+    torch.cuda.synchronize()
+    for a, b in zip(first, out):
+        assert torch.equal(a, b)
+    p.set_f32_gemm(nova_run.F32_GEMM_EXACT)
+    out = p.run_device("gpt_step", *dev)
+    host = p.run("gpt_step", *args)
+    torch.cuda.synchronize()
+    for g, h, n in zip(out, host, names):
+        if n not in ("dwte", "dwpe"):   # scatter_add's atomics add in no fixed order
+            assert np.array_equal(g.cpu().numpy(), h), n
+
+
+def test_device_execute_writable_argument_and_returned_argument(cuda):
+    """A writable memref argument is written in place; an argument returned
+    as a result is copied into the result memory."""
+    import torch
+    p = prog("memref_main.mlir")
+    x = S.uniform((64, 96), 84)
+    w = S.uniform((96, 80), 84, offset=x.size)
+    b = S.uniform((80,), 84, offset=x.size + w.size)
+    dx, dw, db = (torch.from_numpy(a).to(cuda) for a in (x, w, b))
+    dout = torch.zeros((64, 80), device=cuda)
+    assert p.run_device("main", dx, dw, db, dout) == []
+    torch.cuda.synchronize()
+    assert np.array_equal(dout.cpu().numpy(), ref.gemm(x, w, bias=b, epilogue=ref.EPI_BIAS)[0])
+    q = nova_run.Program("""func.func @id(%x: tensor<8x8xf32>) -> (tensor<8x8xf32>, tensor<8x8xf32>) {
+      %y = nova.gelu %x : tensor<8x8xf32>
+      return %x, %y : tensor<8x8xf32>, tensor<8x8xf32>
+    }""")
+    xs = S.normal((8, 8), 85)
+    rx, ry = q.run_device("id", torch.from_numpy(xs).to(cuda))
+    torch.cuda.synchronize()
+    assert np.array_equal(rx.cpu().numpy(), xs)
+    assert_close_f32(ry.cpu().numpy(), ref.gelu(xs), "gelu")
+
+
 def test_nova_run_cli_gpt_step_with_i16_arguments(cuda, tmp_path):
     """The CLI fills i16 token / label and i64 position arguments with
     in-range indices and runs a whole GPT step."""

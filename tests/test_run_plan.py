@@ -45,7 +45,9 @@ def test_reductions_and_backward_plans():
     assert p.results("ln") == [(0, (64, 1024)), (0, (64,)), (0, (64,))]
     assert "_mlir_ciface_nova_hip_layer_norm_backward_f32" in p.plan("ln_train")
     plan = p.plan("sce_train")
-    assert "_mlir_ciface_nova_hip_sce_f32" in plan and "_mlir_ciface_nova_hip_sce_backward_f32" in plan
+    # the softmax feeds only sce_backward: one fused launch
+    assert "_mlir_ciface_nova_hip_sce_fwd_bwd_f32" in plan
+    assert "_mlir_ciface_nova_hip_sce_backward_f32" not in plan
     assert p.results("sce_train") == [(0, (1,)), (0, (32, 5000))]
     b = prog("backward.mlir")
     assert b.results("lin_bwd") == [(0, (40, 36)), (0, (36, 24)), (0, (24,))]
@@ -120,10 +122,11 @@ def test_gpt_step_plans_every_op():
                  "nova.add -> _mlir_ciface_nova_hip_binary_f32",
                  "nova.gelu -> _mlir_ciface_nova_hip_gelu_f32",
                  "i16 labels -> _mlir_ciface_nova_hip_index_to_i32",
-                 "nova.constant splat 1 -> _mlir_ciface_nova_hip_fill_f32",
-                 "nova.mul -> _mlir_ciface_nova_hip_binary_f32",
+                 "nova.constant splat 1 -> elided",
+                 "nova.mul by splat 1.0 -> view",
                  "nova.gelu_backward -> _mlir_ciface_nova_hip_gelu_backward_f32",
-                 "nova.reduce<sum> -> _mlir_ciface_nova_hip_reduce_sum_f32(b50[2,8,32]f32 as [1,2,256])",
+                 "nova.reduce<sum> -> _mlir_ciface_nova_hip_reduce_sum_f32(",
+                 "[2,8,32]f32 as [1,2,256])",
                  "nova.scatter_add -> _mlir_ciface_nova_hip_scatter_add_f32",
                  "nova.reshape -> view b0[16]i16"):
         assert want in plan, want
@@ -225,3 +228,54 @@ def test_narrow_accumulators():
     # the f32-accumulate forms are unchanged
     b = prog("batch_matmul_bf16.mlir")
     assert "accumulate=" not in b.plan("bmm") and "accumulate=" not in b.plan("bmm_nova")
+
+
+def test_gpt_step_fused_sce_and_elided_unit_multiply():
+    """nova.sce whose softmax feeds only nova.sce_backward over the same labels
+    is one fused launch (no softmax written); the multiply by a splat 1.0 and
+    its fill disappear."""
+    from gpt_program import gpt_step
+    plan = nova_run.Program(gpt_step(2, 8, 64, 32, 64)).plan("gpt_step")
+    assert "_mlir_ciface_nova_hip_sce_fwd_bwd_f32" in plan
+    assert "_mlir_ciface_nova_hip_sce_f32(" not in plan
+    assert "_mlir_ciface_nova_hip_sce_backward_f32" not in plan
+    assert "splat 1 -> elided" in plan and "nova.mul by splat 1.0 -> view" in plan
+    assert "nova.constant splat 1 -> _mlir_ciface_nova_hip_fill_f32" not in plan
+    assert plan.count("i16 labels -> _mlir_ciface_nova_hip_index_to_i32") == 1
+
+
+def test_unit_multiply_kept_when_it_broadcasts_or_escapes():
+    p = nova_run.Program("""func.func @b(%x: tensor<4x1xf32>) -> tensor<4x8xf32> {
+      %one = nova.constant {value = dense<1.000000e+00> : tensor<4x8xf32>} : tensor<4x8xf32>
+      %y = nova.mul %x, %one : tensor<4x1xf32>, tensor<4x8xf32>
+      return %y : tensor<4x8xf32>
+    }
+    func.func @r(%x: tensor<4x8xf32>) -> (tensor<4x8xf32>, tensor<1xf32>) {
+      %one = nova.constant {value = dense<1.000000e+00> : tensor<1xf32>} : tensor<1xf32>
+      %y = nova.mul %x, %one : tensor<4x8xf32>, tensor<1xf32>
+      return %y, %one : tensor<4x8xf32>, tensor<1xf32>
+    }
+    func.func @s(%x: tensor<8x5xf32>, %t: tensor<8xi32>) -> (tensor<8x5xf32>, tensor<1xf32>, tensor<8x5xf32>) {
+      %sce:2 = nova.sce %x, %t : tensor<8x5xf32>, tensor<8xi32>
+      %g = nova.sce_backward %sce#0, %t : tensor<8x5xf32>, tensor<8xi32>
+      return %sce#0, %sce#1, %g : tensor<8x5xf32>, tensor<1xf32>, tensor<8x5xf32>
+    }""")
+    assert "_mlir_ciface_nova_hip_binary_f32" in p.plan("b")    # broadcasting: a real multiply
+    assert "_mlir_ciface_nova_hip_binary_f32" in p.plan("r")    # the constant is returned
+    plan = p.plan("s")                                          # softmax also returned: no fold
+    assert "_mlir_ciface_nova_hip_sce_f32" in plan and "sce_backward_f32" in plan
+
+
+def test_f32_gemm_mode_marks_every_f32_product():
+    from gpt_program import gpt_step
+    p = nova_run.Program(gpt_step(2, 8, 64, 32, 64))
+    assert "f32=mfma" not in p.plan("gpt_step")
+    p.set_f32_gemm(nova_run.F32_GEMM_MFMA)
+    plan = p.plan("gpt_step")
+    gemm_lines = [l for l in plan.splitlines() if "_mlir_ciface_nova_hip_gemm(" in l
+                  or "_backward(" in l and ("linear_backward" in l or "matmul_backward" in l)]
+    assert gemm_lines and all("f32=mfma" in l for l in gemm_lines)
+    p.set_f32_gemm(nova_run.F32_GEMM_EXACT)
+    assert "f32=mfma" not in p.plan("gpt_step")
+    with pytest.raises(nova_run.NovaRunError, match="mode"):
+        p.set_f32_gemm(7)
