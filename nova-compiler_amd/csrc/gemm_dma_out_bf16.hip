@@ -1,5 +1,6 @@
 // Instantiates the LDS-DMA GEMM kernels (gemm_dma.h, and its persistent form
-// gemm_pers.h for problems without an epilogue op) for bf16 output: both
+// gemm_pers.h for problems of at least one full round of tiles, with or
+// without a bias / GELU epilogue) for bf16 output: both
 // input dtypes and the four operand layouts.
 #include "gemm_pers.h"
 

@@ -1,6 +1,6 @@
-// Persistent form of the LDS-DMA GEMM (gemm_dma.h) for problems without a
-// bias or GELU epilogue: one workgroup per CU computes its output tiles one
-// after another, so the DMA of the next tile's first two K steps is in
+// Persistent form of the LDS-DMA GEMM (gemm_dma.h), with or without a bias /
+// GELU epilogue: one workgroup per CU computes its output tiles one after
+// another, so the DMA of the next tile's first two K steps is in
 // flight while the current tile's epilogue runs, and no workgroup is
 // dispatched, set up or retired between rounds.
 //
@@ -14,8 +14,9 @@
 //     (both halves) before the epilogue, so the first K step after the
 //     epilogue waits for the DMA with vmcnt(#stores) while the epilogue
 //     stores (the youngest memory operations) may still be in flight;
-//   * the epilogue stages through its own 32 KB of LDS (8 KB per wave), not
-//     the ring, which holds the next tile's data.  160 KB of LDS in all.
+//   * the epilogue stages through its own 16 KB of LDS (4 KB per wave), not
+//     the ring, which holds the next tile's data; the tile's bias goes to
+//     LDS as f32, double-buffered by tile parity.  146 KB of LDS in all.
 #pragma once
 #include <type_traits>
 
