@@ -379,6 +379,58 @@ int32_t _mlir_ciface_nova_hip_reduce_sum_f32(const NovaMemRef3D *x, NovaMemRef2D
 int32_t _mlir_ciface_nova_hip_index_to_i32(const NovaMemRef1D *src, NovaMemRef1D *dst,
                                            int32_t src_dt);
 /* ------------------------------------------------------------------------
+ * Typed aliases for lowered modules (nova-compiler_amd/mlir/
+ * NovaHipLowering.cpp).  An MLIR module declares each callee once, with one
+ * type, so the generic entry points above get one name per operand dtype
+ * combination; the flags must name the same dtypes (NOVA_HIP_EINVAL
+ * otherwise).  No reference counterpart: they are the symbols the lowering
+ * emits in place of the NVPTX code generation of Passes.cpp:115-372.
+ *   _mlir_ciface_nova_hip_gemm_<in>_<out>_b<bias>   (as _mlir_ciface_nova_hip_gemm)
+ *   _mlir_ciface_nova_hip_linear_backward_<in>_<out>, _matmul_backward_<in>_<out>
+ * with <in>, <out>, <bias> one of f32, bf16, f16 (backward: f32_f32 or a
+ * 16-bit input with any output). */
+#define NOVA_HIP_DECLARE_GEMM_ALIAS(SUF)                                          \
+  int32_t _mlir_ciface_nova_hip_gemm_##SUF(const NovaMemRef3D *A,                 \
+                                           const NovaMemRef3D *B, NovaMemRef3D *C, \
+                                           const NovaMemRef1D *bias, int32_t flags);
+#define NOVA_HIP_DECLARE_GEMM_ALIASES_OUT(I, O) \
+  NOVA_HIP_DECLARE_GEMM_ALIAS(I##_##O##_bf32)   \
+  NOVA_HIP_DECLARE_GEMM_ALIAS(I##_##O##_bbf16)  \
+  NOVA_HIP_DECLARE_GEMM_ALIAS(I##_##O##_bf16)
+#define NOVA_HIP_DECLARE_GEMM_ALIASES_IN(I)     \
+  NOVA_HIP_DECLARE_GEMM_ALIASES_OUT(I, f32)     \
+  NOVA_HIP_DECLARE_GEMM_ALIASES_OUT(I, bf16)    \
+  NOVA_HIP_DECLARE_GEMM_ALIASES_OUT(I, f16)
+NOVA_HIP_DECLARE_GEMM_ALIASES_IN(f32)
+NOVA_HIP_DECLARE_GEMM_ALIASES_IN(bf16)
+NOVA_HIP_DECLARE_GEMM_ALIASES_IN(f16)
+#define NOVA_HIP_DECLARE_BWD_ALIAS(SUF)                                                       \
+  int32_t _mlir_ciface_nova_hip_linear_backward_##SUF(                                        \
+      const NovaMemRef2D *grad_out, const NovaMemRef2D *x, const NovaMemRef2D *weight,        \
+      NovaMemRef2D *grad_input, NovaMemRef2D *grad_weight, NovaMemRef1D *grad_bias,          \
+      int32_t flags);                                                                         \
+  int32_t _mlir_ciface_nova_hip_matmul_backward_##SUF(                                        \
+      const NovaMemRef2D *grad, const NovaMemRef2D *A, const NovaMemRef2D *B,                 \
+      NovaMemRef2D *grad_a, NovaMemRef2D *grad_b, int32_t flags);
+NOVA_HIP_DECLARE_BWD_ALIAS(f32_f32)
+NOVA_HIP_DECLARE_BWD_ALIAS(bf16_f32)
+NOVA_HIP_DECLARE_BWD_ALIAS(bf16_bf16)
+NOVA_HIP_DECLARE_BWD_ALIAS(bf16_f16)
+NOVA_HIP_DECLARE_BWD_ALIAS(f16_f32)
+NOVA_HIP_DECLARE_BWD_ALIAS(f16_bf16)
+NOVA_HIP_DECLARE_BWD_ALIAS(f16_f16)
+/* _mlir_ciface_nova_hip_index_to_i32 by source element type (i16, i64). */
+int32_t _mlir_ciface_nova_hip_index_to_i32_i16(const NovaMemRef1D *src, NovaMemRef1D *dst,
+                                               int32_t src_dt);
+int32_t _mlir_ciface_nova_hip_index_to_i32_i64(const NovaMemRef1D *src, NovaMemRef1D *dst,
+                                               int32_t src_dt);
+/* nova.sce whose softmax is unused (the op is Pure): the loss alone, as
+ * _mlir_ciface_nova_hip_sce_f32 with a NULL softmax (a lowered module cannot
+ * pass a null descriptor). */
+int32_t _mlir_ciface_nova_hip_sce_loss_f32(const NovaMemRef2D *logits,
+                                           const NovaMemRef1D *labels, NovaMemRef1D *loss);
+
+/* ------------------------------------------------------------------------
  * Runtime.  The reference's host runtime is libmlir_cuda_runtime's mgpu*
  * calls plus cudaMallocAsync / cudaMemcpyAsync declared by FixGpuLaunch.cpp
  * (:49, :214); this library needs only a stream to launch on.

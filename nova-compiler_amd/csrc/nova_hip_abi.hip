@@ -810,6 +810,80 @@ int32_t nova_hip_synchronize(void) {
 
 const char *nova_hip_last_error(void) { return t_err; }
 
+// ---- Typed aliases for lowered modules --------------------------------------
+// A module declares each callee once, with one type; these aliases give the
+// generic entry points one name per operand dtype combination.  The flags
+// must name the alias's dtypes (the bias dtype only when the epilogue has a
+// bias).
+#define NOVA_GEMM_ALIAS(SUF, IN, OUT, BIAS)                                                    \
+  int32_t _mlir_ciface_nova_hip_gemm_##SUF(const NovaMemRef3D *A, const NovaMemRef3D *B,       \
+                                           NovaMemRef3D *C, const NovaMemRef1D *bias,          \
+                                           int32_t flags) {                                    \
+    const int epi = (flags >> 8) & 0xf;                                                        \
+    const bool has_bias = epi == NOVA_HIP_EPI_BIAS || epi == NOVA_HIP_EPI_BIAS_GELU;          \
+    if ((flags & 0xf) != (IN) || ((flags >> 4) & 0xf) != (OUT) ||                              \
+        (has_bias && ((flags >> 12) & 0xf) != (BIAS))) {                                       \
+      clear_error();                                                                           \
+      return fail(NOVA_HIP_EINVAL, "gemm_" #SUF ": flags 0x%x name other dtypes", flags);     \
+    }                                                                                          \
+    return gemm_core(A, B, C, bias, flags);                                                    \
+  }
+#define NOVA_GEMM_ALIASES_OUT(IS, IN, OS, OUT)               \
+  NOVA_GEMM_ALIAS(IS##_##OS##_bf32, IN, OUT, NOVA_HIP_DT_F32) \
+  NOVA_GEMM_ALIAS(IS##_##OS##_bbf16, IN, OUT, NOVA_HIP_DT_BF16) \
+  NOVA_GEMM_ALIAS(IS##_##OS##_bf16, IN, OUT, NOVA_HIP_DT_F16)
+#define NOVA_GEMM_ALIASES_IN(IS, IN)                     \
+  NOVA_GEMM_ALIASES_OUT(IS, IN, f32, NOVA_HIP_DT_F32)   \
+  NOVA_GEMM_ALIASES_OUT(IS, IN, bf16, NOVA_HIP_DT_BF16) \
+  NOVA_GEMM_ALIASES_OUT(IS, IN, f16, NOVA_HIP_DT_F16)
+NOVA_GEMM_ALIASES_IN(f32, NOVA_HIP_DT_F32)
+NOVA_GEMM_ALIASES_IN(bf16, NOVA_HIP_DT_BF16)
+NOVA_GEMM_ALIASES_IN(f16, NOVA_HIP_DT_F16)
+
+#define NOVA_BWD_ALIAS(SUF, IN, OUT)                                                             \
+  int32_t _mlir_ciface_nova_hip_linear_backward_##SUF(                                           \
+      const NovaMemRef2D *go, const NovaMemRef2D *x, const NovaMemRef2D *w, NovaMemRef2D *gi,    \
+      NovaMemRef2D *gw, NovaMemRef1D *gb, int32_t flags) {                                       \
+    if ((flags & 0xf) != (IN) || ((flags >> 4) & 0xf) != (OUT)) {                                \
+      clear_error();                                                                             \
+      return fail(NOVA_HIP_EINVAL, "linear_backward_" #SUF ": flags 0x%x name other dtypes",    \
+                  flags);                                                                        \
+    }                                                                                            \
+    return _mlir_ciface_nova_hip_linear_backward(go, x, w, gi, gw, gb, flags);                  \
+  }                                                                                              \
+  int32_t _mlir_ciface_nova_hip_matmul_backward_##SUF(const NovaMemRef2D *g,                     \
+                                                      const NovaMemRef2D *A,                     \
+                                                      const NovaMemRef2D *B, NovaMemRef2D *ga,   \
+                                                      NovaMemRef2D *gb, int32_t flags) {         \
+    if ((flags & 0xf) != (IN) || ((flags >> 4) & 0xf) != (OUT)) {                                \
+      clear_error();                                                                             \
+      return fail(NOVA_HIP_EINVAL, "matmul_backward_" #SUF ": flags 0x%x name other dtypes",    \
+                  flags);                                                                        \
+    }                                                                                            \
+    return _mlir_ciface_nova_hip_matmul_backward(g, A, B, ga, gb, flags);                       \
+  }
+NOVA_BWD_ALIAS(f32_f32, NOVA_HIP_DT_F32, NOVA_HIP_DT_F32)
+NOVA_BWD_ALIAS(bf16_f32, NOVA_HIP_DT_BF16, NOVA_HIP_DT_F32)
+NOVA_BWD_ALIAS(bf16_bf16, NOVA_HIP_DT_BF16, NOVA_HIP_DT_BF16)
+NOVA_BWD_ALIAS(bf16_f16, NOVA_HIP_DT_BF16, NOVA_HIP_DT_F16)
+NOVA_BWD_ALIAS(f16_f32, NOVA_HIP_DT_F16, NOVA_HIP_DT_F32)
+NOVA_BWD_ALIAS(f16_bf16, NOVA_HIP_DT_F16, NOVA_HIP_DT_BF16)
+NOVA_BWD_ALIAS(f16_f16, NOVA_HIP_DT_F16, NOVA_HIP_DT_F16)
+
+int32_t _mlir_ciface_nova_hip_index_to_i32_i16(const NovaMemRef1D *src, NovaMemRef1D *dst,
+                                               int32_t src_dt) {
+  return _mlir_ciface_nova_hip_index_to_i32(src, dst, src_dt);
+}
+int32_t _mlir_ciface_nova_hip_index_to_i32_i64(const NovaMemRef1D *src, NovaMemRef1D *dst,
+                                               int32_t src_dt) {
+  return _mlir_ciface_nova_hip_index_to_i32(src, dst, src_dt);
+}
+
+int32_t _mlir_ciface_nova_hip_sce_loss_f32(const NovaMemRef2D *logits,
+                                           const NovaMemRef1D *labels, NovaMemRef1D *loss) {
+  return sce_common(logits, labels, loss, nullptr, nullptr, "sce");
+}
+
 const char *nova_hip_version(void) { return "libnova_hip 0.1.0 (gfx950)"; }
 
 int32_t nova_hip_release_workspace(void) {
