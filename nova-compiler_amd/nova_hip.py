@@ -48,6 +48,9 @@ EXPORTS = (
     "_mlir_ciface_nova_hip_layer_norm_f32",
     "_mlir_ciface_nova_hip_sce_f32",
     "_mlir_ciface_nova_hip_sce_f32_noalloc",
+    "_mlir_ciface_nova_hip_sce_loss_f32",
+    "_mlir_ciface_nova_hip_index_to_i32_i16",
+    "_mlir_ciface_nova_hip_index_to_i32_i64",
     "_mlir_ciface_nova_hip_sce_fwd_bwd_f32",
     "_mlir_ciface_nova_hip_sce_backward_f32",
     "_mlir_ciface_nova_hip_layer_norm_backward_f32",
