@@ -474,3 +474,19 @@ def test_f32_mfma_backward_entry_points(cuda):
     assert_close_f32(gi.cpu().numpy(), gi_r, "grad_input")
     assert_close_f32(gw.cpu().numpy(), gw_r, "grad_weight")
     assert_close_f32(gb.cpu().numpy(), gb_r, "grad_bias")
+
+
+def test_typed_gemm_alias_matches_generic_entry_point(cuda):
+    """The typed alias a lowered module calls gives the generic entry point's
+    bits (bf16 in, bf16 bias + GELU epilogue, bf16 out)."""
+    import torch
+    A, B = lp_inputs((1, 96, 160), (1, 160, 200), S.BF16, 93)
+    bias = S.uniform((200,), 94, dtype=S.BF16)
+    dA, dB, db = to_dev(A, S.BF16, cuda), to_dev(B, S.BF16, cuda), to_dev(bias, S.BF16, cuda)
+    want = nh.gemm(dA, dB, bias=db, epilogue=nh.EPI_BIAS_GELU, out_dtype=torch.bfloat16)
+    got = torch.empty_like(want)
+    flags = nh.gemm_flags(nh.DT_BF16, nh.DT_BF16, nh.EPI_BIAS_GELU, nh.DT_BF16)
+    d = [nh.memref_of(t) for t in (dA, dB, got, db)]
+    nh._bind_stream()
+    nh.check(nh.lib()._mlir_ciface_nova_hip_gemm_bf16_bf16_bbf16(*[nh.ref(v) for v in d], flags))
+    assert torch.equal(got, want)

@@ -170,3 +170,19 @@ def test_layer_norm_offset_data(cuda, mean):
     g = (1 + S.normal((D,), 34, 0, 0.1, offset=rows * D)).astype(np.float32)
     b = S.normal((D,), 34, 0, 0.1, offset=rows * D + D)
     check_ln(x, g, b, cuda, f"ln N({mean}, 1)")
+
+
+def test_sce_loss_only_entry_point(cuda):
+    """_mlir_ciface_nova_hip_sce_loss_f32 (what a lowered module calls for a
+    nova.sce with a dead softmax) gives sce_f32's loss."""
+    import ctypes
+    import torch
+    x = S.normal((50, 3000), 46, 0, 2)
+    t = S.labels(50, 3000, 46, offset=50 * 3000)
+    X, T = dev(x, cuda), dev(t, cuda)
+    _, want = nh.sce(X, T)
+    loss = torch.empty(1, device=cuda)
+    nh._bind_stream()
+    nh.check(nh.lib()._mlir_ciface_nova_hip_sce_loss_f32(
+        nh.ref(nh.memref_of(X)), nh.ref(nh.memref_of(T)), nh.ref(nh.memref_of(loss))))
+    assert torch.equal(loss, want)
