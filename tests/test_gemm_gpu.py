@@ -321,6 +321,36 @@ def test_persistent_epilogue_bf16_out(cuda, epi, odt):
     assert_close_lp(g, want, f"persistent {odt} epilogue {epi}")
 
 
+@pytest.mark.parametrize("epi,odt", [(nh.EPI_BIAS_GELU, "bf16"), (nh.EPI_BIAS, "f32"),
+                                     (nh.EPI_GELU, "f16")])
+def test_persistent_nn_epilogue(cuda, epi, odt):
+    """The persistent kernel's NN form (row-major [K,N] weight, B staged in
+    half-stages of 32 k) with bias / GELU epilogues: 272 tiles (16 workgroups
+    take two, so the next tile's bias goes to the other LDS buffer) and five
+    K steps, against the oracle at the output dtype's bar."""
+    import torch
+    cdt, tdt = {"bf16": (S.BF16, torch.bfloat16), "f16": (S.F16, torch.float16),
+                "f32": (S.F32, torch.float32)}[odt]
+    M, N, K = 4096, 4352, 320
+    x = S.normal((M, K), 35, dtype=S.BF16)
+    w = S.normal((K, N), 35, 0.0, 0.06, dtype=S.BF16, offset=M * K)
+    bias = S.normal((N,), 35, 0.0, 0.5, dtype=S.BF16, offset=M * K + N * K)
+    has_bias = epi in (nh.EPI_BIAS, nh.EPI_BIAS_GELU)
+    Bs = to_dev(bias, S.BF16, cuda) if has_bias else None
+    got = nh.gemm(to_dev(x, S.BF16, cuda), to_dev(w, S.BF16, cuda), bias=Bs, epilogue=epi,
+                  out_dtype=tdt)
+    idx = sample_idx(1, M, N, 65536, 36)
+    it = torch.from_numpy(idx).to(cuda)
+    g = got[it[:, 1], it[:, 2]].float().cpu().numpy()
+    want = ref.gemm_sampled(x, w, idx, adt=S.BF16, bdt=S.BF16,
+                            bias=bias if has_bias else None, biasdt=S.BF16 if has_bias else None,
+                            epilogue=epi, cdt=cdt)
+    if odt == "f32":
+        assert_close_f32(g, want, f"persistent NN epilogue {epi}")
+    else:
+        assert_close_lp(g, want, f"persistent NN {odt} epilogue {epi}")
+
+
 @pytest.mark.parametrize("cfg", ["c4a", "c4b"])
 def test_c4_fp16_unaligned_full(cuda, cfg):
     """Config 4: fp16 batch GEMM with non-tile-aligned shapes (edge tiles)."""
