@@ -351,6 +351,33 @@ def test_persistent_nn_epilogue(cuda, epi, odt):
         assert_close_lp(g, want, f"persistent NN {odt} epilogue {epi}")
 
 
+@pytest.mark.parametrize("epi,odt", [(nh.EPI_BIAS_GELU, "bf16"), (nh.EPI_BIAS, "f16"),
+                                     (nh.EPI_GELU, "f32"), (nh.EPI_BIAS_GELU, "f32")])
+@pytest.mark.parametrize("shape", [(3, 197, 197, 64), (2, 70, 61, 197), (1, 33, 257, 40)])
+def test_gemm_small_epilogues(cuda, epi, odt, shape):
+    """The small-K staged kernel (rows not 16-byte aligned) with bias / GELU
+    epilogues and every output dtype: odd N puts a partial quad of four
+    columns at the row end (element stores), and 16-bit rows of odd length
+    leave some quads without 4-byte alignment."""
+    import torch
+    cdt, tdt = {"bf16": (S.BF16, torch.bfloat16), "f16": (S.F16, torch.float16),
+                "f32": (S.F32, torch.float32)}[odt]
+    batch, M, N, K = shape
+    a, b = lp_inputs((batch, M, K), (batch, K, N), S.F16, seed=41)
+    bias = S.normal((N,), 41, 0.0, 0.5, dtype=S.F16, offset=7)
+    has_bias = epi in (nh.EPI_BIAS, nh.EPI_BIAS_GELU)
+    Bs = to_dev(bias, S.F16, cuda) if has_bias else None
+    got = nh.gemm(to_dev(a, S.F16, cuda), to_dev(b, S.F16, cuda), bias=Bs, epilogue=epi,
+                  out_dtype=tdt).float().cpu().numpy()
+    want = ref.gemm(a, b, adt=S.F16, bdt=S.F16, bias=bias if has_bias else None,
+                    biasdt=S.F16 if has_bias else None, epilogue=epi, cdt=cdt)
+    want = S.widen(want, cdt) if cdt != S.F32 else want
+    if odt == "f32":
+        assert_close_f32(got, want, f"small {shape} epilogue {epi}")
+    else:
+        assert_close_lp(got, want, f"small {shape} {odt} epilogue {epi}")
+
+
 @pytest.mark.parametrize("cfg", ["c4a", "c4b"])
 def test_c4_fp16_unaligned_full(cuda, cfg):
     """Config 4: fp16 batch GEMM with non-tile-aligned shapes (edge tiles)."""
