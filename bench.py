@@ -11,8 +11,11 @@ its roofline fraction, the ``roofline`` object of the dominant kernel, and a
 
 Timing: torch.cuda.Event pairs on torch's current stream, which is the
 stream libnova_hip launches on (nova_hip.py binds it before every call).
-Reduction inputs rotate over 3 buffer sets so the 256 MB MALL cannot serve
-repeated reads as if they were HBM traffic.
+Each timed pass of back-to-back launches follows the --warmup calls and as
+many more untimed ones as make up 0.2 s of work (MIN_WARM_MS), so that it
+measures the clock the board settles at under sustained load.  Inputs of
+every config whose working set is under 1 GB rotate over 3 buffer sets so
+the 256 MB MALL cannot serve repeated reads as if they were HBM traffic.
 """
 from __future__ import annotations
 
@@ -70,14 +73,34 @@ def to_dev(a, dt, torch):
 _LAUNCH_STATS = {}
 
 
+# Untimed back-to-back work before each timed pass, at least (ms): the first
+# tens of milliseconds after a stage starts run slow while the clock settles
+# under the board's power limit (config 3: 25 launches after 5 warm-up calls
+# measured 0.384 ms per launch, 200 launches after 0.2 s of warm-up 0.325 ms,
+# on one box).
+MIN_WARM_MS = 200.0
+
+
 def time_launches(fn, steps, warmup, torch):
-    """Average ms per call over `steps` back-to-back calls after `warmup`
-    calls (the returned figure).  A second pass of `steps` calls, each
-    between two events, gives the median and p10 / p90 of single launches
-    in _LAUNCH_STATS; those events add a little to each launch, so the
-    average is taken from the first pass only."""
-    for i in range(warmup):
-        fn(i)
+    """Average ms per call over `steps` back-to-back calls (the returned
+    figure), after `warmup` calls and then as many more untimed calls as
+    make up MIN_WARM_MS of back-to-back work.  A second pass of `steps`
+    calls, each between two events, gives the median and p10 / p90 of
+    single launches in _LAUNCH_STATS; those events add a little to each
+    launch, so the average is taken from the first pass only."""
+    w0 = torch.cuda.Event(enable_timing=True)
+    w1 = torch.cuda.Event(enable_timing=True)
+    done, n, batch = 0.0, 0, max(warmup, 1)
+    while n < warmup or done < MIN_WARM_MS:
+        w0.record()
+        for i in range(batch):
+            fn(n + i)
+        w1.record()
+        torch.cuda.synchronize()
+        done += w0.elapsed_time(w1)
+        n += batch
+        per = done / n
+        batch = max(1, min(10000, int((MIN_WARM_MS - done) / max(per, 1e-3)) + 1))
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
