@@ -12,17 +12,12 @@
 #include <type_traits>
 
 #include "nova_hip_internal.h"
+#include "wave.h"
 
 namespace nova_hip {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -14,6 +14,7 @@
 #include <mutex>
 
 #include "nova_hip_internal.h"
+#include "wave.h"
 
 namespace nova_hip {
 namespace {
@@ -22,17 +23,6 @@ constexpr int kWaves = 4;  // rows per 256-thread workgroup
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
 
 // ---------------------------------------------------------------------------
 // LayerNorm.  Per row (NovaLayerNormPattern, NovaToLinalgGeneric.cpp:
