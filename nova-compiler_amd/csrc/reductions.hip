@@ -293,12 +293,17 @@ __global__ __launch_bounds__(256) void sce_kernel(SceArgs a) {
 
 }
 
-// Row held in registers across one 512-thread workgroup (rows of up to
-// 2048*NV classes): every logit is read from HBM once, with NV 16-byte loads
-// per thread in flight, and max / sum of exp are exact two-pass
-// reductions over the registers (no running rescale).  The row's loss goes
-// to the workspace for sce_mean_kernel.
+// Row held on chip by one 512-thread workgroup (rows of up to
+// 2048*(NV + NL) classes): NV 16-byte chunks per thread in registers and, for
+// rows past the registers' 2048*NV classes, NL more per thread in LDS,
+// loaded there by LDS-DMA (buffer_load ... lds, no VGPRs).  Every logit is
+// read from HBM once, and max / sum of exp are exact two-pass reductions
+// over the on-chip row (no running rescale).  With NV = 16 (115 VGPRs, 4
+// waves per SIMD) and NL = 9 (72 KB of LDS) two rows fit per CU, up to
+// 51200 classes (the GPT vocab of 50304 included).  The row's loss goes to
+// the workspace for sce_mean_kernel.
 constexpr int kRowThreads = 512;
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) {
   // wave64 reduction, then across the 8 waves through LDS.
@@ -313,14 +318,31 @@ __device__ __forceinline__ float block_reduce(float v, float *red, bool is_max) 
   return r;
 }
 
-template <int NV>
-__global__ __launch_bounds__(kRowThreads) void sce_row_kernel(SceArgs a) {
+template <int NV, int NL = 0>
+__global__ __launch_bounds__(kRowThreads, 4) void sce_row_kernel(SceArgs a) {
   __shared__ float red[kRowThreads / 64];
+  __shared__ f32x4 part[NL > 0 ? kRowThreads * NL : 1];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int n4 = a.C >> 2;
   const float *xr = a.logits + (int64_t)row * a.sx;
   const f32x4 *x4 = reinterpret_cast<const f32x4 *>(xr);
+  // LDS part: chunk f = 512 NV + tid + 512 j goes to part[tid + 512 j] (a
+  // wave's DMA writes 64 consecutive chunks, lane l at l * 16 bytes), issued
+  // first; chunks past the row read as zero and are skipped below.
+  auto in_part = [&](int j) __attribute__((always_inline)) {
+    return kRowThreads * NV + tid + kRowThreads * j < n4;
+  };
+  if constexpr (NL > 0) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(xr), (short)0, n4 * 16, 0x00020000);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (lds_void *)(part + wave * 64 + kRowThreads * j), 16,
+          (uint32_t)(kRowThreads * NV + tid + kRowThreads * j) * 16u, 0, 0, 0);
+  }
   f32x4 v[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -339,12 +361,32 @@ __global__ __launch_bounds__(kRowThreads) void sce_row_kernel(SceArgs a) {
   float m = fmaxf(fmaxf(tail[0], tail[1]), tail[2]);
 #pragma unroll
   for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+  if constexpr (NL > 0) {
+    // This lane's LDS chunks were written by its own wave's DMA: its own
+    // vmcnt wait makes them visible.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      if (in_part(j)) {
+        const f32x4 w = part[tid + kRowThreads * j];
+        m = fmaxf(m, fmaxf(fmaxf(w.x, w.y), fmaxf(w.z, w.w)));
+      }
+  }
   const float gm = block_reduce(m, red, true);
   float s = exp_shifted(tail[0], gm) + exp_shifted(tail[1], gm) + exp_shifted(tail[2], gm);
 #pragma unroll
   for (int i = 0; i < NV; ++i)
     s += (exp_shifted(v[i].x, gm) + exp_shifted(v[i].y, gm)) +
          (exp_shifted(v[i].z, gm) + exp_shifted(v[i].w, gm));
+  if constexpr (NL > 0) {
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      if (in_part(j)) {
+        const f32x4 w = part[tid + kRowThreads * j];
+        s += (exp_shifted(w.x, gm) + exp_shifted(w.y, gm)) +
+             (exp_shifted(w.z, gm) + exp_shifted(w.w, gm));
+      }
+  }
   const float gs = block_reduce(s, red, false);
   const float safe = fmaxf(gs, 1.0e-7f);
   if (a.softmax) {
@@ -361,6 +403,19 @@ __global__ __launch_bounds__(kRowThreads) void sce_row_kernel(SceArgs a) {
         o.w = exp_shifted(v[i].w, gm) / safe;
         __builtin_nontemporal_store(o, s4 + c);
       }
+    }
+    if constexpr (NL > 0) {
+#pragma unroll
+      for (int j = 0; j < NL; ++j)
+        if (in_part(j)) {
+          const f32x4 w = part[tid + kRowThreads * j];
+          f32x4 o;
+          o.x = exp_shifted(w.x, gm) / safe;
+          o.y = exp_shifted(w.y, gm) / safe;
+          o.z = exp_shifted(w.z, gm) / safe;
+          o.w = exp_shifted(w.w, gm) / safe;
+          __builtin_nontemporal_store(o, s4 + kRowThreads * NV + tid + kRowThreads * j);
+        }
     }
     if (tid == 0)
       for (int c = n4 * 4; c < a.C; ++c) sr[c] = exp_shifted(xr[c], gm) / safe;
@@ -380,6 +435,19 @@ __global__ __launch_bounds__(kRowThreads) void sce_row_kernel(SceArgs a) {
           o[e] = sce_grad(exp_shifted(v[i][e], gm) / safe, 4 * c + e == t, bad, a.invN);
         __builtin_nontemporal_store(o, g4 + c);
       }
+    }
+    if constexpr (NL > 0) {
+#pragma unroll
+      for (int j = 0; j < NL; ++j)
+        if (in_part(j)) {
+          const int c = kRowThreads * NV + tid + kRowThreads * j;
+          const f32x4 w = part[tid + kRowThreads * j];
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = sce_grad(exp_shifted(w[e], gm) / safe, 4 * c + e == t, bad, a.invN);
+          __builtin_nontemporal_store(o, g4 + c);
+        }
     }
     if (tid == 0)
       for (int c = n4 * 4; c < a.C; ++c)
@@ -501,16 +569,19 @@ int32_t launch_sce_into(const SceProblem &p, float *ws, hipStream_t s) {
   const bool vec = (p.sx % 4 == 0) && aligned16(p.logits) &&
                    (!p.softmax || (p.ssm % 4 == 0 && aligned16(p.softmax))) &&
                    (!p.grad || (p.sg % 4 == 0 && aligned16(p.grad)));
-  // Rows of 2K..32K classes: one workgroup per row, row in registers.
+  // Rows of 2K..51200 classes: one workgroup per row, row on chip (in
+  // registers, past 32768 classes partly in LDS).
   const int64_t n4 = p.C / 4;
-  if (vec && p.rows > 0 && p.C > 2048 && n4 <= (int64_t)kRowThreads * 16) {
+  if (vec && p.rows > 0 && p.C > 2048 && n4 <= (int64_t)kRowThreads * 25) {
     const unsigned g = (unsigned)p.rows;
     if (n4 <= kRowThreads * 4)
       hipLaunchKernelGGL(sce_row_kernel<4>, dim3(g), dim3(kRowThreads), 0, s, a);
     else if (n4 <= kRowThreads * 8)
       hipLaunchKernelGGL(sce_row_kernel<8>, dim3(g), dim3(kRowThreads), 0, s, a);
-    else
+    else if (n4 <= kRowThreads * 16)
       hipLaunchKernelGGL(sce_row_kernel<16>, dim3(g), dim3(kRowThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((sce_row_kernel<16, 9>), dim3(g), dim3(kRowThreads), 0, s, a);
   } else if (vec && p.rows > 0) {
     hipLaunchKernelGGL(sce_kernel<true>, dim3(grid), dim3(256), 0, s, a);
   } else if (p.rows > 0) {

@@ -131,11 +131,13 @@ def test_c5_sce_full_size(cuda):
     check_sce(inp["logits"], inp["labels"], cuda, "c5 sce")
 
 
-@pytest.mark.parametrize("C", [40000, 50304, 32772])
+@pytest.mark.parametrize("C", [40000, 50304, 32772, 51200, 51204, 65540])
 def test_sce_streaming_rows_above_32k(cuda, C):
-    """Rows of more than 32768 classes with 16-byte aligned rows (C % 4 == 0)
-    take the chunked streaming path (the GPT step's vocab is 50304): loss
-    and softmax against the oracle, plus the fused gradient and
+    """Rows of more than 32768 classes with 16-byte aligned rows (C % 4 == 0):
+    up to 51200 classes the row kernel keeps the part of the row past its
+    registers in LDS (the GPT step's vocab is 50304; 51200 fills both
+    exactly), above that the chunked streaming path reads the row twice.
+    Loss and softmax against the oracle, plus the fused gradient and
     sce_backward bit-identical to each other."""
     import torch
     rows = 24
