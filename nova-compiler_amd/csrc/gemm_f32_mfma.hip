@@ -319,15 +319,30 @@ int32_t launch_gemm_f32_mfma(const GemmProblem &p, hipStream_t s) {
   a.epi = p.epi;
   const int64_t tiles = p.batch * a.tiles_m * a.tiles_n;
   // Split K when the tiles alone leave the chip mostly idle (two
-  // workgroups fit a CU) and K is long enough to share.
+  // workgroups fit a CU) and K is long enough to share: up to 8 splits of
+  // at least 1024, the count that minimises the estimated time, i.e. the
+  // rounds of resident workgroups times the K stages each runs (~3 us per
+  // 32-deep stage of a 128x128 tile with two workgroups per CU, measured on
+  // the GPT step's grad_input GEMM) plus the split reduction's HBM traffic
+  // (splits + 1 passes over the output at ~5 TB/s).  Rounds count whole:
+  // 576 workgroups on 512 slots take two rounds, so 192 tiles run fastest
+  // with 8 splits (3 rounds of 197 stages), not 3 (2 rounds of 524).
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   int splits = 1;
   if (tiles < 2 * cus && p.K >= 2048) {
-    splits = (int)((2 * cus + tiles - 1) / tiles);
-    splits = splits > 8 ? 8 : splits;
-    const int max_by_k = (int)(p.K / 1024);
-    splits = splits > max_by_k ? max_by_k : splits;
-    if (splits < 1) splits = 1;
+    const int64_t slots = 2 * (int64_t)cus;
+    const int64_t stages = (p.K + kBK - 1) / kBK;
+    const double out_bytes = (double)p.batch * p.M * p.N * 4.0;
+    double best = 0.0;
+    for (int sp = 1; sp <= 8 && (sp == 1 || p.K / sp >= 1024); ++sp) {
+      const int64_t rounds = (tiles * sp + slots - 1) / slots;
+      const double us = (double)(rounds * ((stages + sp - 1) / sp)) * 3.0 +
+                        (sp > 1 ? (sp + 1) * out_bytes / 5e12 * 1e6 : 0.0);
+      if (sp == 1 || us < best) {
+        best = us;
+        splits = sp;
+      }
+    }
   }
   const int64_t k_split = ((p.K + splits - 1) / splits + kBK - 1) / kBK * kBK;
   a.k_split = (int)(k_split > 0 ? k_split : kBK);
