@@ -219,6 +219,59 @@ def test_f32_gemm_layouts_bias_gelu_bit_exact(cuda):
     assert_close_f32(got_g, want_g, "f32 bias+gelu")
 
 
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("bias_dt", [None, S.F32, S.BF16])
+def test_f32_gemm_128_tiles_bit_exact(cuda, layout, bias_dt):
+    """The exact f32 GEMM's 128x128 form (aligned rows, >= two of its tiles
+    per CU: here 17 x 33 = 561 tiles, M and N 4 past a tile edge, K = 100 =
+    six 16-deep stages and a partial one) against the oracle's sequential
+    arithmetic, bit for bit, on 65,536 sampled outputs and the corners."""
+    import torch
+    batch, M, N, K = 1, 2052, 4100, 100
+    g = np.random.default_rng(57)
+    a = g.uniform(-1, 1, (batch, M, K)).astype(np.float32)
+    b = g.uniform(-1, 1, (batch, K, N)).astype(np.float32)
+    bias = g.uniform(-1, 1, N).astype(np.float32) if bias_dt is not None else None
+    if bias_dt == S.BF16:
+        bias = S.round_to(bias, S.BF16)
+    A = view_as(a, layout[0], cuda, S.F32)
+    B = view_as(b, layout[1], cuda, S.F32)
+    epi = nh.EPI_BIAS if bias is not None else nh.EPI_NONE
+    Bs = to_dev(bias, bias_dt, cuda) if bias is not None else None
+    got = nh.gemm(A, B, bias=Bs, epilogue=epi)
+    idx = sample_idx(batch, M, N, 65536, 58)
+    it = torch.from_numpy(idx).to(cuda)
+    gs = got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy()
+    want = ref.gemm_sampled(a, b, idx, bias=bias, biasdt=bias_dt, epilogue=ref.EPI_BIAS if bias is not None else ref.EPI_NONE)
+    assert np.array_equal(gs, want), (layout, float(np.abs(gs - want).max()))
+
+
+def test_f32_gemm_128_tiles_padded_rows_and_gelu(cuda):
+    """The 128x128 form with K = 101 (rows padded to 104 floats, so the last
+    16-byte load of a row reaches past K) over a batch of 4, with a bias and
+    GELU epilogue: bias-only outputs bit-exact, GELU within the f32 bar
+    (tanhf on both sides)."""
+    import torch
+    batch, M, N, K = 4, 1024, 2048, 101
+    g = np.random.default_rng(59)
+    a = g.uniform(-1, 1, (batch, M, K)).astype(np.float32)
+    b = g.uniform(-1, 1, (batch, K, N)).astype(np.float32)
+    bias = g.uniform(-1, 1, N).astype(np.float32)
+    store = torch.zeros(batch, M, 104, device=cuda)
+    store[:, :, :K] = torch.from_numpy(a).to(cuda)
+    A = store[:, :, :K]
+    B = to_dev(b, S.F32, cuda)
+    idx = sample_idx(batch, M, N, 65536, 60)
+    it = torch.from_numpy(idx).to(cuda)
+    got = nh.gemm(A, B, bias=to_dev(bias, S.F32, cuda), epilogue=nh.EPI_BIAS)
+    want = ref.gemm_sampled(a, b, idx, bias=bias, biasdt=S.F32, epilogue=ref.EPI_BIAS)
+    gs = got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy()
+    assert np.array_equal(gs, want), float(np.abs(gs - want).max())
+    got = nh.gemm(A, B, bias=to_dev(bias, S.F32, cuda), epilogue=nh.EPI_BIAS_GELU)
+    want = ref.gemm_sampled(a, b, idx, bias=bias, biasdt=S.F32, epilogue=ref.EPI_BIAS_GELU)
+    assert_close_f32(got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy(), want, "128-tile gelu")
+
+
 def test_wrapper_kat_on_gpu(cuda):
     """test/wrapper.c:94-100 through the linear entry point, at full size."""
     import torch
