@@ -531,17 +531,27 @@ int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
   // stores wait for all of its loads (the reduction sits between them), and
   // the queued waves cover that gap.  At D = 4096 on MI355X, 8 per CU ran
   // ~2% faster than 4 per CU.
+  //
+  // Rows of 1025..4096 (16 float4 per lane; 236 VGPRs, two waves per SIMD,
+  // two workgroups per CU) instead go three to a workgroup: one row for
+  // each of three waves, the fourth only helps stage gamma and beta and
+  // exits, so six rows per CU are in flight rather than eight.  HBM serves
+  // the row streams better at that depth: at 16384 x 4096, 3 rows per
+  // workgroup ran 88.8 us, 2 rows 90.0, 4 rows 96.4, 5 rows 92.3, 8 rows
+  // (the persistent grid) 94.4, and one resident workgroup per CU (three
+  // rows) 93.9 (in-process A/B, 3 x 300 launches each).
   const unsigned cus = (unsigned)(device_cu_count() > 0 ? device_cu_count() : 256);
   const unsigned pgrid8 = grid < 8u * cus ? grid : 8u * cus;
   const unsigned pgrid2 = grid < 2u * cus ? grid : 2u * cus;
+  const unsigned grid3 = (unsigned)((p.rows + 2) / 3);
   if (vec && p.D == 256 * 4)
     hipLaunchKernelGGL((layer_norm_reg_kernel<4, true>), dim3(pgrid8), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 4)
     hipLaunchKernelGGL((layer_norm_reg_kernel<4, false>), dim3(pgrid8), dim3(256), 0, s, a);
   else if (vec && p.D == 256 * 16)
-    hipLaunchKernelGGL((layer_norm_reg_kernel<16, true>), dim3(pgrid8), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<16, true>), dim3(grid3), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 16)
-    hipLaunchKernelGGL((layer_norm_reg_kernel<16, false>), dim3(pgrid8), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((layer_norm_reg_kernel<16, false>), dim3(grid3), dim3(256), 0, s, a);
   else if (vec && p.D <= 256 * 32)
     hipLaunchKernelGGL((layer_norm_reg_kernel<32, false>), dim3(pgrid2), dim3(256), 0, s, a);
   else
