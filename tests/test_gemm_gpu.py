@@ -600,3 +600,66 @@ def test_typed_gemm_alias_matches_generic_entry_point(cuda):
     nh._bind_stream()
     nh.check(nh.lib()._mlir_ciface_nova_hip_gemm_bf16_bf16_bbf16(*[nh.ref(v) for v in d], flags))
     assert torch.equal(got, want)
+
+
+def _random_cases(n, seed):
+    """Seeded GEMM problems spread over every kernel path: small and odd
+    shapes (register-staged and small-K kernels), multiples of 256 with
+    enough tiles for the LDS-DMA and persistent kernels, the f32 exact and
+    matrix-core forms; random layout, batch, bias dtype, epilogue and output
+    dtype."""
+    g = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        dt = [S.BF16, S.F16, S.F32][i % 3]
+        kind = g.integers(0, 4)
+        if kind == 0:      # small / odd
+            batch, M, N, K = int(g.integers(1, 4)), int(g.integers(1, 300)), int(g.integers(1, 300)), int(g.integers(1, 300))
+        elif kind == 1:    # unaligned rows, small K
+            batch, M, N, K = int(g.integers(1, 9)), int(g.integers(100, 260)) | 1, int(g.integers(60, 260)) | 1, int(g.integers(8, 200))
+        elif kind == 2:    # tile-aligned, many tiles
+            batch, M, N, K = int(g.integers(2, 5)), 256 * int(g.integers(4, 9)), 256 * int(g.integers(4, 9)), 64 * int(g.integers(2, 6))
+        else:              # medium, ragged
+            batch, M, N, K = 1, int(g.integers(500, 1400)), int(g.integers(500, 1400)), int(g.integers(30, 400))
+        layout = "NT"[g.integers(0, 2)] + "NT"[g.integers(0, 2)]
+        epi = [nh.EPI_NONE, nh.EPI_BIAS, nh.EPI_BIAS_GELU, nh.EPI_GELU][g.integers(0, 4)]
+        odt = dt if dt == S.F32 else [S.F32, dt][g.integers(0, 2)]
+        mfma = dt == S.F32 and bool(g.integers(0, 2))
+        cases.append((i, dt, layout, (batch, M, N, K), epi, odt, mfma))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases(48, 61), ids=lambda c: f"r{c[0]}")
+def test_gemm_random_sweep(cuda, case):
+    """Random problems across the GEMM family against the oracle on sampled
+    outputs: bf16/f16 at the low-precision bar, f32 bit-exact (the exact
+    kernels; GELU through tanhf within the f32 bar) or at the f32 bar (the
+    matrix-core form)."""
+    import torch
+    i, dt, layout, (batch, M, N, K), epi, odt, mfma = case
+    g = np.random.default_rng(1000 + i)
+    if dt == S.F32:
+        a = g.uniform(-1, 1, (batch, M, K)).astype(np.float32)
+        b = g.uniform(-1, 1, (batch, K, N)).astype(np.float32)
+    else:
+        a, b = lp_inputs((batch, M, K), (batch, K, N), dt, seed=1000 + i)
+    has_bias = epi in (nh.EPI_BIAS, nh.EPI_BIAS_GELU)
+    bias = (S.normal((N,), 1000 + i, 0.0, 0.5, dtype=dt, offset=3) if dt != S.F32
+            else g.uniform(-1, 1, N).astype(np.float32)) if has_bias else None
+    tdt = {S.F32: torch.float32, S.BF16: torch.bfloat16, S.F16: torch.float16}[odt]
+    A = view_as(a, layout[0], cuda, dt)
+    B = view_as(b, layout[1], cuda, dt)
+    got = nh.gemm(A, B, bias=to_dev(bias, dt, cuda) if has_bias else None, epilogue=epi,
+                  out_dtype=tdt, f32_mfma=mfma)
+    idx = sample_idx(batch, M, N, 4096, 2000 + i)
+    it = torch.from_numpy(idx).to(cuda)
+    gs = got[it[:, 0], it[:, 1], it[:, 2]].float().cpu().numpy()
+    want = ref.gemm_sampled(a, b, idx, adt=None if dt == S.F32 else dt, bdt=None if dt == S.F32 else dt,
+                            bias=bias, biasdt=dt if has_bias else None, epilogue=epi, cdt=odt)
+    what = f"case {i}: {dt} {layout} {(batch, M, N, K)} epi {epi} out {odt} mfma {mfma}"
+    if dt != S.F32:
+        assert_close_lp(gs, want, what)
+    elif mfma or epi in (nh.EPI_GELU, nh.EPI_BIAS_GELU):
+        assert_close_f32(gs, want, what)
+    else:
+        assert np.array_equal(gs, want), (what, float(np.abs(gs - want).max()))
