@@ -3,8 +3,8 @@
 // compute, and their rows are rarely 16-byte aligned (197 fp16 = 394 B), so
 // the tiled kernels would fall back to 2-byte loads and several passes.
 //
-// One workgroup owns a 64 x NT output tile of one batch (NT = 64..256) and
-// the whole K range.  Both operands are staged into LDS once, normalised:
+// One workgroup owns a 64 (or 128) x NT output tile of one batch (NT =
+// 64..256) and the whole K range.  Both operands are staged into LDS once, normalised:
 //   * an operand is a set of "lines", each contiguous in memory -- rows of
 //     a K-contiguous operand (A rows / B columns), or k-lines of an M/N-
 //     contiguous one;
@@ -17,9 +17,10 @@
 //     blocks, hence the pages, holding the slice's first and last bytes).
 // The LDS layouts are then the ones the MFMA wants: [row][k] read with
 // ds_read_b128, or [k][row] read with the transposing ds_read_b64_tr_b16.
-// Eight waves stage; four of them, in a 2x2 grid, then each own 32 rows x
-// NT/2 columns as NT/64 tiles of v_mfma_f32_32x32x16, and the epilogue
-// writes bounds-checked coalesced stores.
+// Eight waves stage.  In a 64-row window four of them, in a 2x2 grid, then
+// each own 32 rows x NT/2 columns as NT/64 tiles of v_mfma_f32_32x32x16; in
+// a 128-row window all eight do, in a 4x2 grid.  The epilogue writes
+// bounds-checked coalesced stores.
 #include "gemm_common.h"
 
 namespace nova_hip {
@@ -40,6 +41,7 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 struct SmallArgs {
   GemmArgs g;
+  int bm;          // output rows per workgroup: 64 (2x2 computing waves) or 128 (4x2)
   int a_kc, b_kc;  // unit stride on K
   int pa, pb;      // LDS bytes per staged line of A / B (multiple of 16)
   int kp;          // K rounded up to 16
@@ -188,8 +190,8 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
   const int t = blockIdx.x - bidx * per_batch;
   const int tm = __builtin_amdgcn_readfirstlane(t / a.tiles_n);
   const int tn = __builtin_amdgcn_readfirstlane(t - tm * a.tiles_n);
-  const int m0 = tm * kBM, n0 = tn * s.nt;
-  const int m_valid = min(kBM, a.M - m0), n_valid = min(s.nt, a.N - n0);
+  const int m0 = tm * s.bm, n0 = tn * s.nt;
+  const int m_valid = min(s.bm, a.M - m0), n_valid = min(s.nt, a.N - n0);
 
   const uint16_t *A = a.A + (int64_t)bidx * a.sab;
   const uint16_t *B = a.B + (int64_t)bidx * a.sbb;
@@ -208,10 +210,13 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
                           : make_lines(B, a.b_bytes, n0, a.sb_outer, a.K, s.kp, n_valid, kb,
                                        s.pb);
   char *lds_a = smem;
-  char *lds_b = smem + (s.a_kc ? kBM : s.kp) * s.pa;
+  char *lds_b = smem + (s.a_kc ? s.bm : s.kp) * s.pa;
   stage(la, lb, lds_a, lds_b, tid);
   __syncthreads();
-  if (wave >= 4) return;
+  // 64-row windows: waves 0-3 compute (2x2); 128-row windows: all eight
+  // (4x2), a wave past the window's valid rows stops here.
+  if (s.bm == 64 && wave >= 4) return;
+  if (wm * 32 >= m_valid) return;
 
   f32x16 acc[1][TNW];
 #pragma unroll
@@ -254,12 +259,12 @@ struct SmallPlan {
   size_t lds;
 };
 
-SmallPlan plan_small(int64_t N, int64_t K, bool akc, bool bkc) {
+SmallPlan plan_small(int64_t N, int64_t K, bool akc, bool bkc, int bm = kBM) {
   SmallPlan p;
   p.nt = N >= kMaxNT ? kMaxNT : (int)(((N + 63) / 64) * 64);
   p.kp = (int)(((K + 15) / 16) * 16);
-  p.pa = (akc ? p.kp : kBM) * 2 + 16;
-  p.a_lines = akc ? kBM : p.kp;
+  p.pa = (akc ? p.kp : bm) * 2 + 16;
+  p.a_lines = akc ? bm : p.kp;
   p.pb = (bkc ? p.kp : p.nt) * 2 + 16;
   p.b_lines = bkc ? p.nt : p.kp;
   p.lds = (size_t)p.a_lines * p.pa + (size_t)p.b_lines * p.pb;
@@ -282,14 +287,32 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
                           hipStream_t st) {
   SmallArgs s;
   s.g = a_in;
-  const SmallPlan p = plan_small(a_in.N, a_in.K, akc, bkc);
+  SmallPlan p = plan_small(a_in.N, a_in.K, akc, bkc);
+  s.bm = kBM;
+  // 128-row windows (eight computing waves) when they still fit the staging
+  // budget and cut the workgroups a CU must run: each wave's share of the
+  // work is the same, so the time follows the most loaded CU.  Config 4a:
+  // 192 workgroups instead of 384 on 256 CUs, 11.40 -> 10.35 us, the same
+  // bits (in-process A/B).  Config 4b's A window does not fit (85 KB; with
+  // the larger LDS it measured 9.70 against 9.54 us).
+  {
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const int64_t tn = (a_in.N + p.nt - 1) / p.nt;
+    const int64_t t64 = (int64_t)a_in.batch * ((a_in.M + kBM - 1) / kBM) * tn;
+    const int64_t t128 = (int64_t)a_in.batch * ((a_in.M + 2 * kBM - 1) / (2 * kBM)) * tn;
+    const SmallPlan p2 = plan_small(a_in.N, a_in.K, akc, bkc, 2 * kBM);
+    if (p2.lds <= (size_t)kLdsBytes && (t128 + cus - 1) / cus < (t64 + cus - 1) / cus) {
+      p = p2;
+      s.bm = 2 * kBM;
+    }
+  }
   s.a_kc = akc;
   s.b_kc = bkc;
   s.pa = p.pa;
   s.pb = p.pb;
   s.nt = p.nt;
   s.kp = p.kp;
-  s.g.tiles_m = (a_in.M + kBM - 1) / kBM;
+  s.g.tiles_m = (a_in.M + s.bm - 1) / s.bm;
   s.g.tiles_n = (a_in.N + p.nt - 1) / p.nt;
   if ((int64_t)s.g.batch * s.g.tiles_m * s.g.tiles_n > 0x7fffffff)
     return fail(NOVA_HIP_ERANGE, "gemm: too many output tiles");
