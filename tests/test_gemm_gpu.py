@@ -219,16 +219,49 @@ def test_f32_gemm_layouts_bias_gelu_bit_exact(cuda):
     assert_close_f32(got_g, want_g, "f32 bias+gelu")
 
 
+# The exact f32 GEMM's vector forms (16-byte aligned rows): rows x columns
+# per thread and the relative rate the library's choice weighs them by.
+VEC_FORMS = [(8, 8, 1.0), (4, 8, 0.95), (4, 6, 0.93), (4, 4, 0.8)]
+
+
+def vec_form(batch, M, N, cus):
+    """The form the library picks: least (waves of two tiles per CU) x tile
+    area / rate."""
+    best, best_cost = None, None
+    for f, (rm, cn, rate) in enumerate(VEC_FORMS):
+        tm, tn = 16 * rm, 16 * cn
+        tiles = batch * -(-M // tm) * -(-N // tn)
+        cost = -(-tiles // (2 * cus)) * tm * tn / rate
+        if best is None or cost < best_cost:
+            best, best_cost = f, cost
+    return best
+
+
+# One problem per form (on a 256-CU part), M and N off the tile edges, K
+# ending in a partial stage (stages of 16, 16, 32 and 64 k).
+VEC_CASES = [(0, (1, 2044, 4092, 37)), (1, (1, 2044, 2044, 70)), (2, (1, 1020, 3070, 101)),
+             (3, (2, 500, 777, 130))]
+
+
+def _vec_case(cuda, form, shape):
+    import torch
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    if vec_form(*shape[:3], cus) != form:
+        pytest.skip(f"a {cus}-CU device picks another form for {shape}")
+    return shape
+
+
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
 @pytest.mark.parametrize("bias_dt", [None, S.F32, S.BF16])
-def test_f32_gemm_128_tiles_bit_exact(cuda, layout, bias_dt):
-    """The exact f32 GEMM's 128x128 form (aligned rows, >= two of its tiles
-    per CU: here 17 x 33 = 561 tiles, M and N 4 past a tile edge, K = 100 =
-    six 16-deep stages and a partial one) against the oracle's sequential
-    arithmetic, bit for bit, on 65,536 sampled outputs and the corners."""
+@pytest.mark.parametrize("form,shape", VEC_CASES, ids=["128x128", "64x128", "64x96", "64x64"])
+def test_f32_gemm_vector_forms_bit_exact(cuda, layout, bias_dt, form, shape):
+    """The exact f32 GEMM's vector forms (aligned rows; 128x128, 64x128, 64x96
+    and 64x64 tiles) against the oracle's sequential arithmetic, bit for bit,
+    on 65,536 sampled outputs and the corners, in all four layouts, with no
+    bias, an f32 bias and a bf16 bias."""
     import torch
-    batch, M, N, K = 1, 2052, 4100, 100
-    g = np.random.default_rng(57)
+    batch, M, N, K = _vec_case(cuda, form, shape)
+    g = np.random.default_rng(57 + form)
     a = g.uniform(-1, 1, (batch, M, K)).astype(np.float32)
     b = g.uniform(-1, 1, (batch, K, N)).astype(np.float32)
     bias = g.uniform(-1, 1, N).astype(np.float32) if bias_dt is not None else None
@@ -239,6 +272,8 @@ def test_f32_gemm_128_tiles_bit_exact(cuda, layout, bias_dt):
     epi = nh.EPI_BIAS if bias is not None else nh.EPI_NONE
     Bs = to_dev(bias, bias_dt, cuda) if bias is not None else None
     got = nh.gemm(A, B, bias=Bs, epilogue=epi)
+    if batch == 1:
+        got = got.reshape(1, M, N)
     idx = sample_idx(batch, M, N, 65536, 58)
     it = torch.from_numpy(idx).to(cuda)
     gs = got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy()
@@ -246,14 +281,16 @@ def test_f32_gemm_128_tiles_bit_exact(cuda, layout, bias_dt):
     assert np.array_equal(gs, want), (layout, float(np.abs(gs - want).max()))
 
 
-def test_f32_gemm_128_tiles_padded_rows_and_gelu(cuda):
-    """The 128x128 form with K = 101 (rows padded to 104 floats, so the last
-    16-byte load of a row reaches past K) over a batch of 4, with a bias and
-    GELU epilogue: bias-only outputs bit-exact, GELU within the f32 bar
-    (tanhf on both sides)."""
+@pytest.mark.parametrize("form,shape", VEC_CASES, ids=["128x128", "64x128", "64x96", "64x64"])
+def test_f32_gemm_vector_forms_padded_rows_and_gelu(cuda, form, shape):
+    """The vector forms with K = 101 and A's rows padded to 104 floats (the
+    last 16-byte load of a row reaches past K), with a bias and GELU
+    epilogue: bias-only outputs bit-exact, GELU within the f32 bar (tanhf on
+    both sides)."""
     import torch
-    batch, M, N, K = 4, 1024, 2048, 101
-    g = np.random.default_rng(59)
+    batch, M, N, _ = _vec_case(cuda, form, shape)
+    K = 101
+    g = np.random.default_rng(59 + form)
     a = g.uniform(-1, 1, (batch, M, K)).astype(np.float32)
     b = g.uniform(-1, 1, (batch, K, N)).astype(np.float32)
     bias = g.uniform(-1, 1, N).astype(np.float32)
@@ -269,7 +306,25 @@ def test_f32_gemm_128_tiles_padded_rows_and_gelu(cuda):
     assert np.array_equal(gs, want), float(np.abs(gs - want).max())
     got = nh.gemm(A, B, bias=to_dev(bias, S.F32, cuda), epilogue=nh.EPI_BIAS_GELU)
     want = ref.gemm_sampled(a, b, idx, bias=bias, biasdt=S.F32, epilogue=ref.EPI_BIAS_GELU)
-    assert_close_f32(got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy(), want, "128-tile gelu")
+    assert_close_f32(got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy(), want, "vector-form gelu")
+
+
+def test_f32_gemm_gpt_step_input_gradient_shape(cuda):
+    """The LM-head input-gradient shape of the GPT step at reduced K:
+    [8192, K] x [K, 384] with B a transposed view (the 64x96 form, two tiles
+    per CU), bit-exact against the oracle on sampled outputs."""
+    import torch
+    M, N, K = 8192, 384, 200
+    g = np.random.default_rng(61)
+    a = g.uniform(-1, 1, (1, M, K)).astype(np.float32)
+    b = g.uniform(-1, 1, (1, K, N)).astype(np.float32)
+    A = to_dev(a[0], S.F32, cuda)
+    B = view_as(b[0], "T", cuda, S.F32)
+    got = nh.gemm(A, B).reshape(1, M, N)
+    idx = sample_idx(1, M, N, 65536, 62)
+    it = torch.from_numpy(idx).to(cuda)
+    want = ref.gemm_sampled(a, b, idx)
+    assert np.array_equal(got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy(), want)
 
 
 def test_wrapper_kat_on_gpu(cuda):
