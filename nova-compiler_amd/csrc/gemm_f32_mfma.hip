@@ -318,18 +318,19 @@ int32_t launch_gemm_f32_mfma(const GemmProblem &p, hipStream_t s) {
   a.bias_dt = p.bias_dt;
   a.epi = p.epi;
   const int64_t tiles = p.batch * a.tiles_m * a.tiles_n;
-  // Split K when the tiles alone leave the chip mostly idle (two
-  // workgroups fit a CU) and K is long enough to share: up to 8 splits of
-  // at least 1024, the count that minimises the estimated time, i.e. the
-  // rounds of resident workgroups times the K stages each runs (~3 us per
-  // 32-deep stage of a 128x128 tile with two workgroups per CU, measured on
-  // the GPT step's grad_input GEMM) plus the split reduction's HBM traffic
-  // (splits + 1 passes over the output at ~5 TB/s).  Rounds count whole:
-  // 576 workgroups on 512 slots take two rounds, so 192 tiles run fastest
-  // with 8 splits (3 rounds of 197 stages), not 3 (2 rounds of 524).
+  // Split K when K is long enough to share: up to 8 splits of at least
+  // 1024, the count that minimises the estimated time, i.e. the rounds of
+  // resident workgroups (two per CU) times the K stages each runs (~3 us
+  // per 32-deep stage of a 128x128 tile with two workgroups per CU,
+  // measured on the GPT step's grad_input GEMM) plus the split reduction's
+  // HBM traffic (splits + 1 passes over the output at ~5 TB/s).  Rounds
+  // count whole: 576 workgroups on 512 slots take two rounds, so 192 tiles
+  // run fastest with 8 splits (3 rounds of 197 stages), not 3 (2 rounds of
+  // 524); and 1179 tiles of K = 8192 (2.3 rounds) with 3 (7 rounds of 86
+  // stages instead of 3 of 256).
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   int splits = 1;
-  if (tiles < 2 * cus && p.K >= 2048) {
+  if (p.K >= 2048) {
     const int64_t slots = 2 * (int64_t)cus;
     const int64_t stages = (p.K + kBK - 1) / kBK;
     const double out_bytes = (double)p.batch * p.M * p.N * 4.0;

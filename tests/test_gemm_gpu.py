@@ -628,6 +628,24 @@ def test_f32_mfma_same_bits_every_run_and_unaligned_rows(cuda):
                      "offset rows")
 
 
+def test_f32_mfma_split_k_with_many_tiles(cuda):
+    """K split over workgroups also when the tiles alone fill more than a
+    round (600 tiles of K = 4096: the time model picks 4 splits on a
+    256-CU part), checked on 65,536 sampled outputs against the oracle's
+    sequential sum at the f32 bar, with a bias that only split 0 adds."""
+    import torch
+    M, N, K = 384, 25600, 4096
+    A = S.uniform((1, M, K), 101)
+    B = S.uniform((1, K, N), 101, offset=A.size)
+    bias = S.uniform((N,), 102)
+    C = nh.gemm(to_dev(A[0], S.F32, cuda), view_as(B[0], "T", cuda, S.F32),
+                bias=to_dev(bias, S.F32, cuda), epilogue=nh.EPI_BIAS, f32_mfma=True).reshape(1, M, N)
+    idx = sample_idx(1, M, N, 65536, 103)
+    it = torch.from_numpy(idx).to(cuda)
+    want = ref.gemm_sampled(A, B, idx, bias=bias, biasdt=S.F32, epilogue=ref.EPI_BIAS)
+    assert_close_f32(C[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy(), want, "split-K, many tiles")
+
+
 def test_f32_mfma_backward_entry_points(cuda):
     M, K, N = 300, 96, 200
     x = S.normal((M, K), 99)
