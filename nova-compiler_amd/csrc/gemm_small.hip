@@ -17,6 +17,9 @@
 //     blocks, hence the pages, holding the slice's first and last bytes).
 // The LDS layouts are then the ones the MFMA wants: [row][k] read with
 // ds_read_b128, or [k][row] read with the transposing ds_read_b64_tr_b16.
+// A K-contiguous A with 16-byte aligned rows and K a multiple of 16 (up to
+// 64) is not staged: each computing wave loads its A fragments straight from
+// memory before the B staging starts (config 4a: 10.4 -> 9.7 us, same bits).
 // Eight waves stage.  In a 64-row window four of them, in a 2x2 grid, then
 // each own 32 rows x NT/2 columns as NT/64 tiles of v_mfma_f32_32x32x16; in
 // a 128-row window all eight do, in a 4x2 grid.  The epilogue writes
@@ -46,6 +49,7 @@ struct SmallArgs {
   int pa, pb;      // LDS bytes per staged line of A / B (multiple of 16)
   int kp;          // K rounded up to 16
   int nt;          // output columns per workgroup
+  int a_direct;    // A fragments loaded from memory, A not staged
 };
 
 // Staging geometry of one operand for one workgroup.
@@ -174,7 +178,7 @@ __device__ __forceinline__ u32x4 read_frag(const char *lds, int pitch, bool kc, 
   return u32x4{l2[0], l2[1], h2[0], h2[1]};
 }
 
-template <int DT, int TNW>
+template <int DT, int TNW, bool AD>
 __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmArgs &a = s.g;
@@ -201,16 +205,35 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
   // Likewise B with N and NT.  LDS rows or columns past the valid ones are
   // left unwritten: they only feed outputs the epilogue discards.
   const int ka = (m_valid + 7) / 8, kb = (n_valid + 7) / 8;
-  const Lines la = s.a_kc ? make_lines(A, a.a_bytes, (int64_t)m0 * a.sa_outer, a.sa_outer,
-                                       m_valid, m_valid, a.K, s.kp / 8, s.pa)
-                          : make_lines(A, a.a_bytes, m0, a.sa_outer, a.K, s.kp, m_valid, ka,
-                                       s.pa);
+  // A read directly (AD) has no lines to stage.
+  const Lines la = AD       ? make_lines(A, a.a_bytes, 0, a.sa_outer, 0, 0, a.K, s.kp / 8, s.pa)
+                   : s.a_kc ? make_lines(A, a.a_bytes, (int64_t)m0 * a.sa_outer, a.sa_outer,
+                                         m_valid, m_valid, a.K, s.kp / 8, s.pa)
+                            : make_lines(A, a.a_bytes, m0, a.sa_outer, a.K, s.kp, m_valid, ka,
+                                         s.pa);
   const Lines lb = s.b_kc ? make_lines(B, a.b_bytes, (int64_t)n0 * a.sb_outer, a.sb_outer,
                                        n_valid, n_valid, a.K, s.kp / 8, s.pb)
                           : make_lines(B, a.b_bytes, n0, a.sb_outer, a.K, s.kp, n_valid, kb,
                                        s.pb);
   char *lds_a = smem;
-  char *lds_b = smem + (s.a_kc ? s.bm : s.kp) * s.pa;
+  char *lds_b = AD ? smem : smem + (s.a_kc ? s.bm : s.kp) * s.pa;
+  // Direct A fragments (K-contiguous A, 16-byte aligned rows, K % 16 == 0,
+  // K <= 64): lane l of a computing wave loads row m0 + 32 wm + l % 32,
+  // k = 16 kk + 8 (l / 32) .. + 7 for every k16 step, issued before the B
+  // staging so that the latencies overlap.  Rows past the slice read zero;
+  // rows past M inside it feed discarded outputs.
+  u32x4 fad[4];
+  if constexpr (AD) {
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(A), (short)0, (int)a.a_bytes, 0x00020000);
+    const bool computes = !(s.bm == 64 && wave >= 4) && wm * 32 < m_valid;
+    const uint32_t rowoff = (uint32_t)((m0 + wm * 32 + (lane & 31)) * a.sa_outer * 2) +
+                            16u * (lane >> 5);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      if (computes && kk * 16 < s.kp)
+        fad[kk] = __builtin_amdgcn_raw_buffer_load_b128(ra, rowoff + 32u * kk, 0, 0);
+  }
   stage(la, lb, lds_a, lds_b, tid);
   __syncthreads();
   // 64-row windows: waves 0-3 compute (2x2); 128-row windows: all eight
@@ -226,14 +249,26 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
 
   const int ksteps = s.kp / 16;
   const int nw = wn * (TNW * 32);
+  if constexpr (AD) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk >= ksteps) break;
+      u32x4 fb[TNW];
+#pragma unroll
+      for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, s.pb, s.b_kc, nw + 32 * j, kk, lane);
+#pragma unroll
+      for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fad[kk], fb[j], acc[0][j]);
+    }
+  } else {
 #pragma unroll 2
-  for (int kk = 0; kk < ksteps; ++kk) {
-    const u32x4 fa = read_frag(lds_a, s.pa, s.a_kc, wm * 32, kk, lane);
-    u32x4 fb[TNW];
+    for (int kk = 0; kk < ksteps; ++kk) {
+      const u32x4 fa = read_frag(lds_a, s.pa, s.a_kc, wm * 32, kk, lane);
+      u32x4 fb[TNW];
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, s.pb, s.b_kc, nw + 32 * j, kk, lane);
+      for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, s.pb, s.b_kc, nw + 32 * j, kk, lane);
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
+      for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
+    }
   }
   store_outputs<1, TNW>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
 }
@@ -241,11 +276,20 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
 template <int DT>
 int32_t launch_dt(const SmallArgs &s, size_t lds, hipStream_t st) {
   const dim3 grid((unsigned)(s.g.batch * s.g.tiles_m * s.g.tiles_n)), block(kStageThreads);
-  switch (s.nt / 64) {
-    case 1: hipLaunchKernelGGL((gemm_small_kernel<DT, 1>), grid, block, lds, st, s); break;
-    case 2: hipLaunchKernelGGL((gemm_small_kernel<DT, 2>), grid, block, lds, st, s); break;
-    case 3: hipLaunchKernelGGL((gemm_small_kernel<DT, 3>), grid, block, lds, st, s); break;
-    default: hipLaunchKernelGGL((gemm_small_kernel<DT, 4>), grid, block, lds, st, s); break;
+  if (s.a_direct) {
+    switch (s.nt / 64) {
+      case 1: hipLaunchKernelGGL((gemm_small_kernel<DT, 1, true>), grid, block, lds, st, s); break;
+      case 2: hipLaunchKernelGGL((gemm_small_kernel<DT, 2, true>), grid, block, lds, st, s); break;
+      case 3: hipLaunchKernelGGL((gemm_small_kernel<DT, 3, true>), grid, block, lds, st, s); break;
+      default: hipLaunchKernelGGL((gemm_small_kernel<DT, 4, true>), grid, block, lds, st, s); break;
+    }
+  } else {
+    switch (s.nt / 64) {
+      case 1: hipLaunchKernelGGL((gemm_small_kernel<DT, 1, false>), grid, block, lds, st, s); break;
+      case 2: hipLaunchKernelGGL((gemm_small_kernel<DT, 2, false>), grid, block, lds, st, s); break;
+      case 3: hipLaunchKernelGGL((gemm_small_kernel<DT, 3, false>), grid, block, lds, st, s); break;
+      default: hipLaunchKernelGGL((gemm_small_kernel<DT, 4, false>), grid, block, lds, st, s); break;
+    }
   }
   return check_hip(hipGetLastError(), "gemm_small launch");
 }
@@ -306,6 +350,11 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
       s.bm = 2 * kBM;
     }
   }
+  // A read straight into MFMA fragments: K-contiguous, every row 16-byte
+  // aligned, whole k16 steps (no k past K to zero), at most four of them.
+  s.a_direct = akc && (reinterpret_cast<uintptr_t>(a_in.A) & 15u) == 0 &&
+               a_in.sa_outer % 8 == 0 && a_in.sab % 8 == 0 && a_in.K % 16 == 0 && a_in.K <= 64;
+  if (s.a_direct) p.lds -= (size_t)p.a_lines * p.pa;
   s.a_kc = akc;
   s.b_kc = bkc;
   s.pa = p.pa;

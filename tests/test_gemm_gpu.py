@@ -486,6 +486,28 @@ def test_gemm_small_epilogues(cuda, epi, odt, shape):
         assert_close_lp(got, want, f"small {shape} {odt} epilogue {epi}")
 
 
+@pytest.mark.parametrize("dt", [S.F16, S.BF16])
+@pytest.mark.parametrize("shape", [(2, 197, 197, 64), (5, 100, 131, 32), (1, 37, 301, 16),
+                                   (3, 260, 77, 48), (2, 129, 255, 64)])
+def test_gemm_small_direct_a_exact(cuda, dt, shape):
+    """The small-K kernel with A read straight into MFMA fragments (K-
+    contiguous A with 16-byte aligned rows, K a multiple of 16 up to 64; B
+    with unaligned N-contiguous rows is staged): 64- and 128-row windows,
+    M off the 32-row blocks, N past one 256-column tile.  Integer-valued
+    inputs make every product and sum exact, so the output must equal the
+    oracle's exactly."""
+    import torch
+    batch, M, N, K = shape
+    g = np.random.default_rng(71)
+    a = g.integers(-4, 5, (batch, M, K)).astype(np.float32)
+    b = g.integers(-4, 5, (batch, K, N)).astype(np.float32)
+    A = to_dev(S.round_to(a, dt), dt, cuda)
+    B = to_dev(S.round_to(b, dt), dt, cuda)
+    got = nh.gemm(A, B).cpu().numpy()
+    want = ref.gemm(S.round_to(a, dt), S.round_to(b, dt), adt=dt, bdt=dt)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("cfg", ["c4a", "c4b"])
 def test_c4_fp16_unaligned_full(cuda, cfg):
     """Config 4: fp16 batch GEMM with non-tile-aligned shapes (edge tiles)."""
