@@ -171,8 +171,12 @@ __device__ __forceinline__ void round_tile_of(int id, const GemmArgs &a, int &b,
 // top-left output is (mw, nw) in batch bidx.  Accumulator element v of lane
 // l sits at row 8*(v/4) + 4*(l/32) + v%4, column l%32 of its tile; a store
 // instruction writes 32 consecutive columns of two rows.  Bounds-checked
-// (edge tiles), specialised on output dtype and epilogue.
-template <int TM, int TN, int ODT, int EPI>
+// (edge tiles), specialised on output dtype and epilogue.  NT: f32 stores
+// with the nontemporal hint, for callers whose store instructions write
+// whole 128-byte lines (with partial lines the hint costs time).  It is a
+// template parameter: behind a runtime branch the compiler merges the two
+// stores into one and drops the hint.
+template <int TM, int TN, int ODT, int EPI, bool NT = false>
 __device__ __forceinline__ void store_outputs_t(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
                                                 int bidx, int mw, int nw, int lane) {
   constexpr bool kBias = (EPI == NOVA_HIP_EPI_BIAS || EPI == NOVA_HIP_EPI_BIAS_GELU);
@@ -195,7 +199,10 @@ __device__ __forceinline__ void store_outputs_t(const f32x16 (&acc)[TM][TN], con
         if constexpr (kGelu) x = gelu_tanh(x);
         if (n_ok && m < a.M) {
           T *dst = Cb + (int64_t)m * a.scm + n;
-          if constexpr (ODT == NOVA_HIP_DT_F32) *dst = x;
+          if constexpr (ODT == NOVA_HIP_DT_F32) {
+            if constexpr (NT) __builtin_nontemporal_store(x, dst);
+            else *dst = x;
+          }
           else if constexpr (ODT == NOVA_HIP_DT_BF16) *dst = to_bf16(x);
           else *dst = to_f16(x);
         }
@@ -243,7 +250,7 @@ __device__ __forceinline__ void store_outputs_any(const f32x16 (&acc)[TM][TN], c
 
 // Runtime (output dtype, epilogue) -> one specialisation of store_outputs_t
 // (grids of up to 4 tiles per wave).
-template <int TM, int TN>
+template <int TM, int TN, bool NT = false>
 __device__ __forceinline__ void store_outputs(const f32x16 (&acc)[TM][TN], const GemmArgs &a,
                                               int bidx, int mw, int nw, int lane) {
   if constexpr (TM * TN > 4) {
@@ -253,7 +260,7 @@ __device__ __forceinline__ void store_outputs(const f32x16 (&acc)[TM][TN], const
   switch (a.out_dt * 4 + a.epi) {
 #define NOVA_EPI_CASE(O, E) \
   case O * 4 + E:           \
-    store_outputs_t<TM, TN, O, E>(acc, a, bidx, mw, nw, lane); \
+    store_outputs_t<TM, TN, O, E, NT>(acc, a, bidx, mw, nw, lane); \
     break;
     NOVA_EPI_CASE(0, 0) NOVA_EPI_CASE(0, 1) NOVA_EPI_CASE(0, 2) NOVA_EPI_CASE(0, 3)
     NOVA_EPI_CASE(1, 0) NOVA_EPI_CASE(1, 1) NOVA_EPI_CASE(1, 2) NOVA_EPI_CASE(1, 3)

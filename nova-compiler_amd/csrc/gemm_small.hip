@@ -50,6 +50,7 @@ struct SmallArgs {
   int kp;          // K rounded up to 16
   int nt;          // output columns per workgroup
   int a_direct;    // A fragments loaded from memory, A not staged
+  int nt_store;    // f32 output in whole 128-byte lines: nontemporal stores
 };
 
 // Staging geometry of one operand for one workgroup.
@@ -178,7 +179,7 @@ __device__ __forceinline__ u32x4 read_frag(const char *lds, int pitch, bool kc, 
   return u32x4{l2[0], l2[1], h2[0], h2[1]};
 }
 
-template <int DT, int TNW, bool AD>
+template <int DT, int TNW, bool AD, bool NT>
 __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmArgs &a = s.g;
@@ -270,26 +271,27 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
       for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
     }
   }
-  store_outputs<1, TNW>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
+  store_outputs<1, TNW, NT>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
 }
 
 template <int DT>
 int32_t launch_dt(const SmallArgs &s, size_t lds, hipStream_t st) {
   const dim3 grid((unsigned)(s.g.batch * s.g.tiles_m * s.g.tiles_n)), block(kStageThreads);
-  if (s.a_direct) {
-    switch (s.nt / 64) {
-      case 1: hipLaunchKernelGGL((gemm_small_kernel<DT, 1, true>), grid, block, lds, st, s); break;
-      case 2: hipLaunchKernelGGL((gemm_small_kernel<DT, 2, true>), grid, block, lds, st, s); break;
-      case 3: hipLaunchKernelGGL((gemm_small_kernel<DT, 3, true>), grid, block, lds, st, s); break;
-      default: hipLaunchKernelGGL((gemm_small_kernel<DT, 4, true>), grid, block, lds, st, s); break;
-    }
-  } else {
-    switch (s.nt / 64) {
-      case 1: hipLaunchKernelGGL((gemm_small_kernel<DT, 1, false>), grid, block, lds, st, s); break;
-      case 2: hipLaunchKernelGGL((gemm_small_kernel<DT, 2, false>), grid, block, lds, st, s); break;
-      case 3: hipLaunchKernelGGL((gemm_small_kernel<DT, 3, false>), grid, block, lds, st, s); break;
-      default: hipLaunchKernelGGL((gemm_small_kernel<DT, 4, false>), grid, block, lds, st, s); break;
-    }
+  switch ((s.a_direct ? 8 : 0) + (s.nt_store ? 4 : 0) + s.nt / 64 - 1) {
+#define NOVA_SMALL(AD, NT, T)                                                        \
+  case (AD ? 8 : 0) + (NT ? 4 : 0) + T - 1:                                         \
+    hipLaunchKernelGGL((gemm_small_kernel<DT, T, AD, NT>), grid, block, lds, st, s); \
+    break;
+    NOVA_SMALL(false, false, 1) NOVA_SMALL(false, false, 2)
+    NOVA_SMALL(false, false, 3) NOVA_SMALL(false, false, 4)
+    NOVA_SMALL(false, true, 1) NOVA_SMALL(false, true, 2)
+    NOVA_SMALL(false, true, 3) NOVA_SMALL(false, true, 4)
+    NOVA_SMALL(true, false, 1) NOVA_SMALL(true, false, 2)
+    NOVA_SMALL(true, false, 3) NOVA_SMALL(true, false, 4)
+    NOVA_SMALL(true, true, 1) NOVA_SMALL(true, true, 2)
+    NOVA_SMALL(true, true, 3) NOVA_SMALL(true, true, 4)
+#undef NOVA_SMALL
+    default: break;
   }
   return check_hip(hipGetLastError(), "gemm_small launch");
 }
@@ -355,6 +357,13 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
   s.a_direct = akc && (reinterpret_cast<uintptr_t>(a_in.A) & 15u) == 0 &&
                a_in.sa_outer % 8 == 0 && a_in.sab % 8 == 0 && a_in.K % 16 == 0 && a_in.K <= 64;
   if (s.a_direct) p.lds -= (size_t)p.a_lines * p.pa;
+  // Each store instruction writes 32 consecutive f32 of two rows: whole
+  // 128-byte lines when the rows and the slices are line-aligned and N is a
+  // multiple of 32.  Those go out with the nontemporal hint (config 4b's
+  // [96, 197, 64] output: 9.54 -> 9.08 us); partial lines (config 4a's
+  // 788-byte rows) would take longer with it (9.7 -> 12.8 us).
+  s.nt_store = a_in.out_dt == NOVA_HIP_DT_F32 && (reinterpret_cast<uintptr_t>(a_in.C) & 127u) == 0 &&
+               a_in.scm % 32 == 0 && a_in.scb % 32 == 0 && a_in.N % 32 == 0;
   s.a_kc = akc;
   s.b_kc = bkc;
   s.pa = p.pa;
