@@ -335,7 +335,9 @@ int32_t launch_gemm_f32_mfma(const GemmProblem &p, hipStream_t s) {
     const int64_t stages = (p.K + kBK - 1) / kBK;
     const double out_bytes = (double)p.batch * p.M * p.N * 4.0;
     double best = 0.0;
-    for (int sp = 1; sp <= 8 && (sp == 1 || p.K / sp >= 1024); ++sp) {
+    // The partials take splits x the output of workspace: at most 1 GiB.
+    for (int sp = 1; sp <= 8 && (sp == 1 || (p.K / sp >= 1024 && sp * out_bytes <= 1073741824.0));
+         ++sp) {
       const int64_t rounds = (tiles * sp + slots - 1) / slots;
       const double us = (double)(rounds * ((stages + sp - 1) / sp)) * 3.0 +
                         (sp > 1 ? (sp + 1) * out_bytes / 5e12 * 1e6 : 0.0);
