@@ -327,6 +327,29 @@ def test_f32_gemm_gpt_step_input_gradient_shape(cuda):
     assert np.array_equal(got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("shape,layout", [((8192, 384, 50304), "NT"), ((384, 1536, 8192), "TN"),
+                                          ((1536, 384, 8192), "TN")],
+                         ids=["lm_head_grad_input", "mlp_grad_weight_384x1536", "mlp_grad_weight_1536x384"])
+def test_f32_gemm_gpt_step_shapes_full_k(cuda, shape, layout):
+    """The GPT step's long-K exact f32 GEMMs at their full shapes (the
+    LM-head input gradient, K = 50304, on the 64x96 form; the MLP weight
+    gradients, K = 8192, on the deep-stage 64x64 form), in the step's
+    operand layouts, bit-exact against the oracle's sequential sum on
+    16,384 sampled outputs and the corners."""
+    import torch
+    M, N, K = shape
+    g = np.random.default_rng(63)
+    a = g.uniform(-1, 1, (1, M, K)).astype(np.float32)
+    b = g.uniform(-1, 1, (1, K, N)).astype(np.float32)
+    A = view_as(a[0], layout[0], cuda, S.F32)
+    B = view_as(b[0], layout[1], cuda, S.F32)
+    got = nh.gemm(A, B).reshape(1, M, N)
+    idx = sample_idx(1, M, N, 16384, 64)
+    it = torch.from_numpy(idx).to(cuda)
+    want = ref.gemm_sampled(a, b, idx)
+    assert np.array_equal(got[it[:, 0], it[:, 1], it[:, 2]].cpu().numpy(), want)
+
+
 def test_wrapper_kat_on_gpu(cuda):
     """test/wrapper.c:94-100 through the linear entry point, at full size."""
     import torch
