@@ -675,6 +675,16 @@ std::vector<int64_t> dense_strides(const std::vector<int64_t> &shape) {
 
 bool is_dense(const View &v) { return v.strides == dense_strides(v.shape); }
 
+// Dims [0, n - R) of v fold into dim n - R of a rank-R descriptor: each
+// folded dim's stride is the next one's stride times its size (dims of size
+// one are free).
+bool leading_dims_fold(const View &v, int R) {
+  const int n = (int)v.shape.size();
+  for (int j = n - R - 1; j >= 0; --j)
+    if (v.shape[j] > 1 && v.strides[j] != v.strides[j + 1] * v.shape[j + 1]) return false;
+  return true;
+}
+
 struct Plan {
   std::vector<Buffer> bufs;
   std::vector<Step> steps;
@@ -1302,6 +1312,27 @@ struct Planner {
         return fail(NOVA_HIP_EINVAL, "line %d: op '%s' is not part of this path's op surface",
                     op.line, n.c_str());
       }
+    }
+    // The launches pass rank-R descriptors (GEMM 3, row ops 2, binary ops
+    // 4) and fold any leading dims into the first kept one; that is only the
+    // same addressing when the folded dims are contiguous over it.  A view
+    // whose leading dims are permuted (a nova.transpose of batch axes) is
+    // refused here rather than addressed wrongly.
+    for (const Step &st : plan.steps) {
+      int R = 0;
+      size_t nin = st.in.size();
+      if (st.kind == "gemm") R = 3, nin = 2;
+      else if (st.kind == "binary") R = 4;
+      else if (st.kind == "layer_norm" || st.kind == "sce" || st.kind == "sce_fwd_bwd" ||
+               st.kind == "sce_bwd" || st.kind == "ln_bwd" || st.kind == "lin_bwd" ||
+               st.kind == "mm_bwd" || st.kind == "gather")
+        R = 2, nin = st.kind == "ln_bwd" ? 2 : st.kind == "lin_bwd" || st.kind == "mm_bwd" ? 3 : 1;
+      for (size_t i = 0; R > 0 && i < nin && i < st.in.size(); ++i)
+        if (!leading_dims_fold(st.in[i], R))
+          return fail(NOVA_HIP_ESTRIDE,
+                      "%s: operand %zu has leading dims that are not contiguous (a transpose "
+                      "of batch axes is not on this path)",
+                      st.text.c_str(), i);
     }
     for (const std::string &r : f.rets) {
       auto it = env.find(r);

@@ -54,6 +54,21 @@ def test_f32_programs_bit_exact(cuda):
     assert np.array_equal(y, ref.gemm(x, w, bias=b, epilogue=ref.EPI_BIAS)[0])
 
 
+def test_rank4_matmul_programs_bit_exact(cuda):
+    """nova.matmul above rank 3, and with a rank-2 operand broadcast over
+    two batch dims: f32 bit-exact against the oracle on the collapsed batch."""
+    p = prog("matmul_rank4.mlir")
+    A = S.uniform((2, 3, 8, 16), 79)
+    B = S.uniform((2, 3, 16, 5), 79, offset=A.size)
+    (C,) = p.run("mm4", A, B)
+    want = ref.gemm(A.reshape(6, 8, 16), B.reshape(6, 16, 5)).reshape(2, 3, 8, 5)
+    assert np.array_equal(C, want)
+    W = S.uniform((16, 5), 80)
+    (C2,) = p.run("mm4_bcast", A, W)
+    want2 = ref.gemm(A.reshape(6, 8, 16), np.broadcast_to(W, (6, 16, 5)).copy()).reshape(2, 3, 8, 5)
+    assert np.array_equal(C2, want2)
+
+
 def test_layer_norm_programs(cuda):
     p = prog("reductions.mlir")
     x = S.normal((64, 1024), 74)

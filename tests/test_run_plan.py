@@ -279,3 +279,15 @@ def test_f32_gemm_mode_marks_every_f32_product():
     assert "f32=mfma" not in p.plan("gpt_step")
     with pytest.raises(nova_run.NovaRunError, match="mode"):
         p.set_f32_gemm(7)
+
+
+def test_rank4_matmul_plans_and_batch_transpose_is_refused():
+    """nova.matmul above rank 3 folds its batch dims into one launch; a
+    transpose of batch axes leaves leading dims the launch cannot fold and
+    is refused at plan time instead of being addressed wrongly."""
+    p = prog("matmul_rank4.mlir")
+    for f in ("mm4", "mm4_bcast"):
+        assert p.plan(f).count("_mlir_ciface_nova_hip_gemm") == 1
+        assert p.results(f) == [(0, (2, 3, 8, 5))]
+    with pytest.raises(nova_run.NovaRunError, match="leading dims that are not contiguous"):
+        p.plan("mm4_batch_transposed")
