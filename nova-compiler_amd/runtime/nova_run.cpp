@@ -1313,26 +1313,34 @@ struct Planner {
                     op.line, n.c_str());
       }
     }
-    // The launches pass rank-R descriptors (GEMM 3, row ops 2, binary ops
-    // 4) and fold any leading dims into the first kept one; that is only the
-    // same addressing when the folded dims are contiguous over it.  A view
+    // The launches pass rank-R descriptors (GEMM 3, row ops 2, labels and
+    // vectors 1, binary ops 4) and fold any leading dims into the first kept
+    // one; that is only the same addressing when the folded dims are
+    // contiguous over it.  Operands read as flat arrays must be dense.  A view
     // whose leading dims are permuted (a nova.transpose of batch axes) is
     // refused here rather than addressed wrongly.
     for (const Step &st : plan.steps) {
-      int R = 0;
-      size_t nin = st.in.size();
-      if (st.kind == "gemm") R = 3, nin = 2;
-      else if (st.kind == "binary") R = 4;
-      else if (st.kind == "layer_norm" || st.kind == "sce" || st.kind == "sce_fwd_bwd" ||
-               st.kind == "sce_bwd" || st.kind == "ln_bwd" || st.kind == "lin_bwd" ||
-               st.kind == "mm_bwd" || st.kind == "gather")
-        R = 2, nin = st.kind == "ln_bwd" ? 2 : st.kind == "lin_bwd" || st.kind == "mm_bwd" ? 3 : 1;
-      for (size_t i = 0; R > 0 && i < nin && i < st.in.size(); ++i)
-        if (!leading_dims_fold(st.in[i], R))
+      std::vector<int> ranks;  // per input: R, or 0 for "dense"
+      if (st.kind == "gemm") ranks = {3, 3, 1};
+      else if (st.kind == "binary") ranks = {4, 4};
+      else if (st.kind == "layer_norm") ranks = {2, 1, 1};
+      else if (st.kind == "sce" || st.kind == "sce_fwd_bwd" || st.kind == "sce_bwd") ranks = {2, 1};
+      else if (st.kind == "ln_bwd") ranks = {2, 2, 1, 0, 0};
+      else if (st.kind == "lin_bwd" || st.kind == "mm_bwd") ranks = {2, 2, 2};
+      else if (st.kind == "gather") ranks = {2, 0};
+      else if (st.kind == "scatter" || st.kind == "gelu" || st.kind == "gelu_bwd" ||
+               st.kind == "reduce_sum" || st.kind == "idx32")
+        ranks = {0, 0};
+      for (size_t i = 0; i < ranks.size() && i < st.in.size(); ++i) {
+        const View &v = st.in[i];
+        const bool ok = ranks[i] > 0 ? leading_dims_fold(v, ranks[i]) : is_dense(v);
+        if (!ok)
           return fail(NOVA_HIP_ESTRIDE,
-                      "%s: operand %zu has leading dims that are not contiguous (a transpose "
-                      "of batch axes is not on this path)",
-                      st.text.c_str(), i);
+                      "%s: operand %zu is a view whose %s (a transpose of batch axes is not on "
+                      "this path)",
+                      st.text.c_str(), i,
+                      ranks[i] > 0 ? "leading dims are not contiguous" : "elements are not dense");
+      }
     }
     for (const std::string &r : f.rets) {
       auto it = env.find(r);

@@ -284,10 +284,13 @@ def test_f32_gemm_mode_marks_every_f32_product():
 def test_rank4_matmul_plans_and_batch_transpose_is_refused():
     """nova.matmul above rank 3 folds its batch dims into one launch; a
     transpose of batch axes leaves leading dims the launch cannot fold and
-    is refused at plan time instead of being addressed wrongly."""
+    is refused at plan time instead of being addressed wrongly, as are SCE
+    labels given as a transposed view."""
     p = prog("matmul_rank4.mlir")
     for f in ("mm4", "mm4_bcast"):
         assert p.plan(f).count("_mlir_ciface_nova_hip_gemm") == 1
         assert p.results(f) == [(0, (2, 3, 8, 5))]
-    with pytest.raises(nova_run.NovaRunError, match="leading dims that are not contiguous"):
+    with pytest.raises(nova_run.NovaRunError, match="leading dims are not contiguous"):
         p.plan("mm4_batch_transposed")
+    with pytest.raises(nova_run.NovaRunError, match="operand 1 is a view whose leading dims"):
+        p.plan("sce_labels_transposed")
