@@ -55,3 +55,35 @@ def test_sce_noalloc_at_the_row_limit(cuda):
     t = S.labels(9, 100, 65, offset=900)
     sm1, l1, sm2, l2 = _pair(x, t, cuda)
     assert torch.equal(l1, l2) and torch.equal(sm1, sm2)
+
+
+def test_sce_noalloc_under_hip_graph_capture(cuda):
+    """The callers this entry point is for: captured in a HIP graph (which
+    the allocating entry point's first call could not be) and replayed
+    three times, with new logits written eagerly between the replays; every
+    replay's loss equals the allocating entry point's on the same logits."""
+    import torch
+    rows, C = 256, 3000
+    X = torch.empty((rows, C), device=cuda)
+    T = torch.from_numpy(S.labels(rows, C, 66)).to(cuda)
+    loss = torch.empty(1, device=cuda)
+    X.copy_(torch.from_numpy(S.normal((rows, C), 66, 0, 2)))
+    nh.sce(X, T, loss=loss, noalloc=True)  # set-up call outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            nh.sce(X, T, loss=loss, noalloc=True)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        X.copy_(torch.from_numpy(S.normal((rows, C), 67 + i, 0, 2)))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = loss.clone()
+        _, want = nh.sce(X, T)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), i
