@@ -33,7 +33,7 @@ using namespace gemm;
 
 constexpr int kBM = 64;
 constexpr int kMaxNT = 256;
-constexpr int kLdsBytes = 64 * 1024;  // staging budget per workgroup
+constexpr int kLdsBytes = 80 * 1024;  // staging budget per workgroup (two fit a CU)
 // Staging runs on eight waves, the MFMAs and the epilogue on the first four
 // (2x2 grid): staging is the long, latency-bound part.
 constexpr int kStageThreads = 512;
@@ -51,6 +51,7 @@ struct SmallArgs {
   int nt;          // output columns per workgroup
   int a_direct;    // A fragments loaded from memory, A not staged
   int nt_store;    // f32 output in whole 128-byte lines: nontemporal stores
+  int buf_store;   // f32 output whose batch slice fits 31-bit byte offsets: buffer stores
 };
 
 // Staging geometry of one operand for one workgroup.
@@ -179,6 +180,39 @@ __device__ __forceinline__ u32x4 read_frag(const char *lds, int pitch, bool kc, 
   return u32x4{l2[0], l2[1], h2[0], h2[1]};
 }
 
+// f32 epilogue through buffer stores: one resource per batch slice whose
+// range ends at its last element, a per-lane 32-bit offset (a column past N
+// gets one past every range) plus the row's uniform offset, so rows past M
+// and columns past N are dropped by the range check, with one add per store
+// instead of 64-bit address arithmetic (config 4b: 9.10 -> 8.74 us).
+template <int TNW, bool NT>
+__device__ __forceinline__ void store_f32_buf(const f32x16 (&acc)[1][TNW], const GemmArgs &a,
+                                              int bidx, int mw, int nw, int lane) {
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
+  float *Cb = static_cast<float *>(a.C) + (int64_t)bidx * a.scb;
+  const int range = (int)(((int64_t)(a.M - 1) * a.scm + a.N) * 4);
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(Cb, (short)0, range, 0x00020000);
+  const int lrow = lane & 31, lh = lane >> 5;
+  const uint32_t rstep = (uint32_t)a.scm * 4u;
+#pragma unroll
+  for (int j = 0; j < TNW; ++j) {
+    const int n = nw + j * 32 + lrow;
+    const uint32_t base = n < a.N ? (uint32_t)((mw + 4 * lh) * a.scm + n) * 4u : kOOB;
+    const float bv = (has_bias && n < a.N) ? bias_at(a.bias, a.bias_dt, n) : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      float x = acc[0][j][v];
+      if (has_bias) x = x + bv;
+      if (has_gelu) x = gelu_tanh(x);
+      const uint32_t off = base + (uint32_t)(8 * (v >> 2) + (v & 3)) * rstep;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rc, off, 0,
+                                            NT ? 2 : 0);  // 2: nontemporal
+    }
+  }
+}
+
 template <int DT, int TNW, bool AD, bool NT>
 __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -271,7 +305,10 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
       for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
     }
   }
-  store_outputs<1, TNW, NT>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
+  if (s.buf_store)
+    store_f32_buf<TNW, NT>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
+  else
+    store_outputs<1, TNW, NT>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
 }
 
 template <int DT>
@@ -297,9 +334,11 @@ int32_t launch_dt(const SmallArgs &s, size_t lds, hipStream_t st) {
 }
 
 // Staging geometry chosen on the host: output columns per workgroup, K
-// rounded up to whole k16 steps, and each operand's LDS line pitch (its
-// padded width plus 16 bytes, which spreads the rows of a fragment read
-// over the banks).
+// rounded up to whole k16 steps, and each operand's LDS line pitch: a [row][k]
+// line's padded width plus 16 bytes, which spreads the rows of a 16-byte
+// fragment read over the banks; a [k][row] line's plus 64 bytes, so that the
+// four k-lines a 16-lane group of ds_read_b64_tr_b16 reads (64 bytes each
+// per half wave) fall on disjoint banks (config 4a: 9.69 -> 9.53 us).
 struct SmallPlan {
   int nt, kp, pa, pb, a_lines, b_lines;
   size_t lds;
@@ -309,9 +348,9 @@ SmallPlan plan_small(int64_t N, int64_t K, bool akc, bool bkc, int bm = kBM) {
   SmallPlan p;
   p.nt = N >= kMaxNT ? kMaxNT : (int)(((N + 63) / 64) * 64);
   p.kp = (int)(((K + 15) / 16) * 16);
-  p.pa = (akc ? p.kp : bm) * 2 + 16;
+  p.pa = akc ? p.kp * 2 + 16 : bm * 2 + 64;
   p.a_lines = akc ? bm : p.kp;
-  p.pb = (bkc ? p.kp : p.nt) * 2 + 16;
+  p.pb = bkc ? p.kp * 2 + 16 : p.nt * 2 + 64;
   p.b_lines = bkc ? p.nt : p.kp;
   p.lds = (size_t)p.a_lines * p.pa + (size_t)p.b_lines * p.pb;
   return p;
@@ -324,7 +363,7 @@ bool gemm_small_applicable(const gemm::GemmArgs &a, bool akc, bool bkc) {
   // Resources reach up to 30 bytes past a slice (both ends rounded to 16).
   if (a.a_bytes > 0x7fffff00u || a.b_bytes > 0x7fffff00u) return false;
   // The whole K range of a 64-row A window and an NT-column B window must
-  // fit the staging budget.
+  // fit the staging budget (80 KB: two workgroups per CU).
   const SmallPlan p = plan_small(a.N, a.K, akc, bkc);
   return p.lds <= (size_t)kLdsBytes;
 }
@@ -339,8 +378,8 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
   // budget and cut the workgroups a CU must run: each wave's share of the
   // work is the same, so the time follows the most loaded CU.  Config 4a:
   // 192 workgroups instead of 384 on 256 CUs, 11.40 -> 10.35 us, the same
-  // bits (in-process A/B).  Config 4b's A window does not fit (85 KB; with
-  // the larger LDS it measured 9.70 against 9.54 us).
+  // bits (in-process A/B).  Config 4b's 128-row A window does not fit (95 KB;
+  // with that much LDS it had measured 9.70 against 9.54 us).
   {
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const int64_t tn = (a_in.N + p.nt - 1) / p.nt;
@@ -364,6 +403,8 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
   // 788-byte rows) would take longer with it (9.7 -> 12.8 us).
   s.nt_store = a_in.out_dt == NOVA_HIP_DT_F32 && (reinterpret_cast<uintptr_t>(a_in.C) & 127u) == 0 &&
                a_in.scm % 32 == 0 && a_in.scb % 32 == 0 && a_in.N % 32 == 0;
+  s.buf_store = a_in.out_dt == NOVA_HIP_DT_F32 &&
+                ((int64_t)(a_in.M - 1) * a_in.scm + a_in.N) * 4 <= 0x7fffffff;
   s.a_kc = akc;
   s.b_kc = bkc;
   s.pa = p.pa;
