@@ -23,8 +23,8 @@
 //   * 64x64 output tile per 256-thread workgroup, 4x4 outputs per thread,
 //     K staged through LDS 16 at a time, element loads: any strides, every
 //     dtype;
-//   * f32 with 16-byte aligned operand rows: 128x128, 64x128, 64x96 and
-//     64x64 tiles (8x8, 4x8, 4x6 and 4x4 outputs per thread), 16-byte global
+//   * f32 with 16-byte aligned operand rows: 128x128, 64x128, 64x96, 64x64
+//     and 64x32 tiles (8x8, 4x8, 4x6, 4x4 and 4x2 outputs per thread), 16-byte global
 //     loads along each operand's unit-stride dim, LDS stages [k][m] / [k][n]
 //     read with 16-byte reads; the tile is chosen per problem so that the
 //     CUs stay busy.
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void gemm_exact_vec_kernel(F32Args a, uint32_t
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   static_assert(RM == 4 || RM == 8, "rows per thread");
-  static_assert(CN == 4 || CN == 6 || CN == 8, "columns per thread");
+  static_assert(CN == 2 || CN == 4 || CN == 6 || CN == 8, "columns per thread");
   constexpr int TM = kVt * RM, TN = kVt * CN;
   constexpr int A4 = TM * KS / 4, B4 = TN * KS / 4;  // float4 per stage
   constexpr int EA = (A4 + 255) / 256, EB = (B4 + 255) / 256;
@@ -312,6 +312,7 @@ __global__ __launch_bounds__(256) void gemm_exact_vec_kernel(F32Args a, uint32_t
     }
   };
   auto col = [&](int j) __attribute__((always_inline)) {
+    if (CN == 2) return tx * 2 + j;
     return j < 4 ? tx * 4 + j : 4 * kVt + tx * (CN - 4) + (j - 4);
   };
   const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
@@ -330,9 +331,15 @@ __global__ __launch_bounds__(256) void gemm_exact_vec_kernel(F32Args a, uint32_t
     for (int g = 0; g < RM / 4; ++g)
       av[g] = *reinterpret_cast<const f32x4 *>(&sa[buf][kk][g * 4 * kVt + ty * 4]);
     float bv[CN];
-    const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&sb[buf][kk][tx * 4]);
+    if constexpr (CN == 2) {
+      const f32x2 b0 = *reinterpret_cast<const f32x2 *>(&sb[buf][kk][tx * 2]);
+      bv[0] = b0[0];
+      bv[1] = b0[1];
+    } else {
+      const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&sb[buf][kk][tx * 4]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bv[j] = b0[j];
+      for (int j = 0; j < 4; ++j) bv[j] = b0[j];
+    }
     if constexpr (CN == 8) {
       const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&sb[buf][kk][4 * kVt + tx * 4]);
 #pragma unroll
@@ -386,12 +393,15 @@ __global__ __launch_bounds__(256) void gemm_exact_vec_kernel(F32Args a, uint32_t
 // The vector forms: rows and columns per thread, k per stage, and the
 // relative rate of one CU running two or more of its workgroups (measured on
 // the GPT step's shapes: 55, 52, 51 and ~44 TFLOP/s when every CU holds
-// several tiles).
+// several tiles; the 64x32 form's 0.6 keeps it to problems of few tiles,
+// where its twice as many waves hide latency that the others cannot).
 struct VecForm {
   int rm, cn, ks;
   double rate;
 };
-constexpr VecForm kVecForms[] = {{8, 8, 16, 1.0}, {4, 8, 16, 0.95}, {4, 6, 32, 0.93}, {4, 4, 64, 0.8}};
+constexpr VecForm kVecForms[] = {{8, 8, 16, 1.0}, {4, 8, 16, 0.95}, {4, 6, 32, 0.93},
+                                 {4, 4, 64, 0.8}, {4, 2, 64, 0.6}};
+constexpr int kNumVecForms = sizeof(kVecForms) / sizeof(kVecForms[0]);
 
 template <int RM, int CN, int KS>
 void launch_vec(const F32Args &a, bool akc, bool bkc, uint32_t ab, uint32_t bb, unsigned grid,
@@ -445,10 +455,12 @@ int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s) {
   // outer and batch strides multiples of 4, 32-bit buffer offsets).  The
   // form is the one of least estimated time: the tiles run in waves of two
   // per CU, each wave taking the tile's area over the form's rate.  The
-  // deep-stage 64x64 form wins where there are few tiles and long K (one
-  // workgroup per CU, whose loads a 16-k stage cannot hide); the 64x96 form
-  // gives the LM-head input gradient [8192, 50304] x [50304, 384] exactly
-  // two tiles per CU (6.9 ms against 10.0 ms for the scalar 64x64 form).
+  // deep-stage 64x32 form wins where there are few tiles and long K (the
+  // GPT step's MLP weight gradients [384, 8192] x [8192, 1536]: 288 tiles,
+  // 0.59 -> 0.37 ms against the 64x64 form, whose one wave per SIMD cannot
+  // hide its loads); the 64x96 form gives the LM-head input gradient
+  // [8192, 50304] x [50304, 384] exactly two tiles per CU (6.9 ms against
+  // 10.0 ms for the scalar 64x64 form).
   if (p.in_dt == NOVA_HIP_DT_F32) {
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const int64_t a_ext = p.a_kcontig ? (p.M - 1) * p.sa_outer + p.K : (p.K - 1) * p.sa_outer + p.M;
@@ -459,7 +471,7 @@ int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s) {
       int best = -1;
       double best_cost = 0.0;
       int64_t best_tiles = 0;
-      for (int f = 0; f < 4; ++f) {
+      for (int f = 0; f < kNumVecForms; ++f) {
         const VecForm &v = kVecForms[f];
         const int64_t tm = 16 * v.rm, tn = 16 * v.cn;
         const int64_t tiles = p.batch * ((p.M + tm - 1) / tm) * ((p.N + tn - 1) / tn);
@@ -483,7 +495,8 @@ int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s) {
           case 0: launch_vec<8, 8, 16>(a, akc, bkc, ab, bb, grid, s); break;
           case 1: launch_vec<4, 8, 16>(a, akc, bkc, ab, bb, grid, s); break;
           case 2: launch_vec<4, 6, 32>(a, akc, bkc, ab, bb, grid, s); break;
-          default: launch_vec<4, 4, 64>(a, akc, bkc, ab, bb, grid, s); break;
+          case 3: launch_vec<4, 4, 64>(a, akc, bkc, ab, bb, grid, s); break;
+          default: launch_vec<4, 2, 64>(a, akc, bkc, ab, bb, grid, s); break;
         }
         return check_hip(hipGetLastError(), "gemm_exact launch");
       }

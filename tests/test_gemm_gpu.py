@@ -221,7 +221,7 @@ def test_f32_gemm_layouts_bias_gelu_bit_exact(cuda):
 
 # The exact f32 GEMM's vector forms (16-byte aligned rows): rows x columns
 # per thread and the relative rate the library's choice weighs them by.
-VEC_FORMS = [(8, 8, 1.0), (4, 8, 0.95), (4, 6, 0.93), (4, 4, 0.8)]
+VEC_FORMS = [(8, 8, 1.0), (4, 8, 0.95), (4, 6, 0.93), (4, 4, 0.8), (4, 2, 0.6)]
 
 
 def vec_form(batch, M, N, cus):
@@ -238,9 +238,10 @@ def vec_form(batch, M, N, cus):
 
 
 # One problem per form (on a 256-CU part), M and N off the tile edges, K
-# ending in a partial stage (stages of 16, 16, 32 and 64 k).
+# ending in a partial stage (stages of 16, 16, 32, 64 and 64 k).
 VEC_CASES = [(0, (1, 2044, 4092, 37)), (1, (1, 2044, 2044, 70)), (2, (1, 1020, 3070, 101)),
-             (3, (2, 500, 777, 130))]
+             (3, (1, 1000, 1100, 130)), (4, (2, 500, 777, 130))]
+VEC_IDS = ["128x128", "64x128", "64x96", "64x64", "64x32"]
 
 
 def _vec_case(cuda, form, shape):
@@ -253,10 +254,10 @@ def _vec_case(cuda, form, shape):
 
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
 @pytest.mark.parametrize("bias_dt", [None, S.F32, S.BF16])
-@pytest.mark.parametrize("form,shape", VEC_CASES, ids=["128x128", "64x128", "64x96", "64x64"])
+@pytest.mark.parametrize("form,shape", VEC_CASES, ids=VEC_IDS)
 def test_f32_gemm_vector_forms_bit_exact(cuda, layout, bias_dt, form, shape):
-    """The exact f32 GEMM's vector forms (aligned rows; 128x128, 64x128, 64x96
-    and 64x64 tiles) against the oracle's sequential arithmetic, bit for bit,
+    """The exact f32 GEMM's vector forms (aligned rows; 128x128, 64x128, 64x96,
+    64x64 and 64x32 tiles) against the oracle's sequential arithmetic, bit for bit,
     on 65,536 sampled outputs and the corners, in all four layouts, with no
     bias, an f32 bias and a bf16 bias."""
     import torch
@@ -281,7 +282,7 @@ def test_f32_gemm_vector_forms_bit_exact(cuda, layout, bias_dt, form, shape):
     assert np.array_equal(gs, want), (layout, float(np.abs(gs - want).max()))
 
 
-@pytest.mark.parametrize("form,shape", VEC_CASES, ids=["128x128", "64x128", "64x96", "64x64"])
+@pytest.mark.parametrize("form,shape", VEC_CASES, ids=VEC_IDS)
 def test_f32_gemm_vector_forms_padded_rows_and_gelu(cuda, form, shape):
     """The vector forms with K = 101 and A's rows padded to 104 floats (the
     last 16-byte load of a row reaches past K), with a bias and GELU
@@ -333,7 +334,7 @@ def test_f32_gemm_gpt_step_input_gradient_shape(cuda):
 def test_f32_gemm_gpt_step_shapes_full_k(cuda, shape, layout):
     """The GPT step's long-K exact f32 GEMMs at their full shapes (the
     LM-head input gradient, K = 50304, on the 64x96 form; the MLP weight
-    gradients, K = 8192, on the deep-stage 64x64 form), in the step's
+    gradients, K = 8192, on the deep-stage 64x32 form), in the step's
     operand layouts, bit-exact against the oracle's sequential sum on
     16,384 sampled outputs and the corners."""
     import torch
