@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void gemm_pers_kernel(GemmArgs a) {
   constexpr int kSteps = BK / 16;
   constexpr int kFrags = TM + TN;
   static_assert(kSpread == 2 && kPerStep == kLoads && kPerStep * 2 == TM * TN,
-                "one DMA load per MFMA: A's in the last k16 step, B's in the first");
+                "one DMA load per MFMA: A's in the last k16 step, B's in the first two");
   u32x4 fa[2][TM], fb[2][TN];
 
   // (Every lambda here must inline: a call would force acc into memory.)
@@ -241,13 +241,18 @@ __global__ __launch_bounds__(kThreads) void gemm_pers_kernel(GemmArgs a) {
     const int nxt = cur ^ 1;
     NOVA_WAIT_LGKMCNT0();
     __builtin_amdgcn_sched_barrier(0);
+    // The next K step's B loads go out half in k16 step 0 and half in k16
+    // step 1, beside that step's fragment reads: all eight in step 0 made
+    // a burst that ran 0.6-3.4% slower depending on the box (C2, in-process
+    // A/B, same bits); in step 2 they no longer land in time (3% slower).
+    constexpr int kHalf = kPerStep / 2;
 #pragma unroll
     for (int m = 0; m < TM * TN; ++m) {
       mfma_one(m, 0);
       if (m < kFrags) read_one(m, 1, A, B, 1);
-      if (KIND == 1 && m < kPerStep)
+      if (KIND == 1 && m < kHalf)
         dma(kPerStep + m, ring_a[nxt], ring_b[nxt], tc, kt + 1, true);
-      if (KIND == 2 && m < kPerStep) dma(kPerStep + m, ring_a[nxt], ring_b[nxt], tn, 0, tn_live);
+      if (KIND == 2 && m < kHalf) dma(kPerStep + m, ring_a[nxt], ring_b[nxt], tn, 0, tn_live);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -258,6 +263,10 @@ __global__ __launch_bounds__(kThreads) void gemm_pers_kernel(GemmArgs a) {
       for (int m = 0; m < TM * TN; ++m) {
         mfma_one(m, s & 1);
         if (m < kFrags) read_one(m, (s + 1) & 1, A, B, s + 1);
+        if (s == 1 && KIND == 1 && m < kPerStep - kHalf)
+          dma(kPerStep + kHalf + m, ring_a[nxt], ring_b[nxt], tc, kt + 1, true);
+        if (s == 1 && KIND == 2 && m < kPerStep - kHalf)
+          dma(kPerStep + kHalf + m, ring_a[nxt], ring_b[nxt], tn, 0, tn_live);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
