@@ -22,7 +22,11 @@
 // memory before the B staging starts (config 4a: 10.4 -> 9.7 us, same bits).
 // Eight waves stage.  In a 64-row window four of them, in a 2x2 grid, then
 // each own 32 rows x NT/2 columns as NT/64 tiles of v_mfma_f32_32x32x16; in
-// a 128-row window all eight do, in a 4x2 grid.  The epilogue writes
+// a 128-row window all eight do, in a 4x2 grid.  The MFMA loops are
+// specialised per operand layout and read the next fragments from LDS while
+// the current ones multiply; with A read directly and an f32 output each
+// 32-column block is stored before the next block multiplies (configs 4a /
+// 4b: 9.66 -> 8.94 / 8.75 -> 8.19 us, the same bits).  The epilogue writes
 // bounds-checked coalesced stores.
 #include "gemm_common.h"
 
@@ -64,6 +68,7 @@ struct Lines {
   int len;                      // valid elements per line
   int ncpl;                     // 16-byte LDS chunks written per line
   int pitch;                    // LDS bytes per line
+  bool aligned;                 // every line starts 16-byte aligned: one load per chunk
 };
 
 __device__ __forceinline__ Lines make_lines(const uint16_t *slice, uint32_t slice_bytes,
@@ -86,13 +91,17 @@ __device__ __forceinline__ Lines make_lines(const uint16_t *slice, uint32_t slic
   l.len = len;
   l.ncpl = ncpl;
   l.pitch = pitch;
+  l.aligned = ((l.c0 | l.step) & 15u) == 0;
   return l;
 }
 
 // Normalised chunk q (line i = q / ncpl, chunk c = q % ncpl): the two aligned
-// global chunks holding elements 8c .. 8c+7 of line i.  Chunks with no valid
-// element load from beyond the resource's range: zeros, no memory access,
-// and no branch to split the batch of loads.
+// global chunks holding elements 8c .. 8c+7 of line i, or only the first
+// when every line is 16-byte aligned (config 4b's B: 8.17 -> 7.92 us).
+// Chunks with no valid element load from beyond the resource's range: zeros,
+// no memory access, and no branch to split the batch of loads.  (Loading
+// each aligned chunk once and taking its neighbour from the next lane with a
+// shuffle measured slower: 9.60 / 8.86 against 8.94 / 8.11 us on 4a / 4b.)
 struct Raw {
   u32x4 lo, hi;
 };
@@ -102,7 +111,10 @@ __device__ __forceinline__ Raw chunk_load(const Lines &l, int q, int nq) {
   const uint32_t off = ((l.c0 + (uint32_t)i * l.step) & ~15u) + 16u * c;
   Raw r;
   r.lo = __builtin_amdgcn_raw_buffer_load_b128(l.rsrc, live ? off : kOOB, 0, 0);
-  r.hi = __builtin_amdgcn_raw_buffer_load_b128(l.rsrc, live ? off + 16u : kOOB, 0, 0);
+  if (l.aligned)
+    r.hi = u32x4{0u, 0u, 0u, 0u};  // the shift is zero: unused
+  else
+    r.hi = __builtin_amdgcn_raw_buffer_load_b128(l.rsrc, live ? off + 16u : kOOB, 0, 0);
   return r;
 }
 
@@ -180,14 +192,15 @@ __device__ __forceinline__ u32x4 read_frag(const char *lds, int pitch, bool kc, 
   return u32x4{l2[0], l2[1], h2[0], h2[1]};
 }
 
-// f32 epilogue through buffer stores: one resource per batch slice whose
-// range ends at its last element, a per-lane 32-bit offset (a column past N
-// gets one past every range) plus the row's uniform offset, so rows past M
-// and columns past N are dropped by the range check, with one add per store
-// instead of 64-bit address arithmetic (config 4b: 9.10 -> 8.74 us).
-template <int TNW, bool NT>
-__device__ __forceinline__ void store_f32_buf(const f32x16 (&acc)[1][TNW], const GemmArgs &a,
-                                              int bidx, int mw, int nw, int lane) {
+// f32 epilogue through buffer stores, one 32-column block (columns n0j ..
+// n0j + 31 of rows mw ..): one resource per batch slice whose range ends at
+// its last element, a per-lane 32-bit offset (a column past N gets one past
+// every range) plus the row's uniform offset, so rows past M and columns
+// past N are dropped by the range check, with one add per store instead of
+// 64-bit address arithmetic (config 4b: 9.10 -> 8.74 us).
+template <bool NT>
+__device__ __forceinline__ void store_f32_blk(const f32x16 &acc, const GemmArgs &a, int bidx,
+                                              int mw, int n0j, int lane) {
   const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
   const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
   float *Cb = static_cast<float *>(a.C) + (int64_t)bidx * a.scb;
@@ -196,20 +209,96 @@ __device__ __forceinline__ void store_f32_buf(const f32x16 (&acc)[1][TNW], const
       __builtin_amdgcn_make_buffer_rsrc(Cb, (short)0, range, 0x00020000);
   const int lrow = lane & 31, lh = lane >> 5;
   const uint32_t rstep = (uint32_t)a.scm * 4u;
+  const int n = n0j + lrow;
+  const uint32_t base = n < a.N ? (uint32_t)((mw + 4 * lh) * a.scm + n) * 4u : kOOB;
+  const float bv = (has_bias && n < a.N) ? bias_at(a.bias, a.bias_dt, n) : 0.0f;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    float x = acc[v];
+    if (has_bias) x = x + bv;
+    if (has_gelu) x = gelu_tanh(x);
+    const uint32_t off = base + (uint32_t)(8 * (v >> 2) + (v & 3)) * rstep;
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rc, off, 0,
+                                          NT ? 2 : 0);  // 2: nontemporal
+  }
+}
+
+template <int TNW, bool NT>
+__device__ __forceinline__ void store_f32_buf(const f32x16 (&acc)[1][TNW], const GemmArgs &a,
+                                              int bidx, int mw, int nw, int lane) {
+#pragma unroll
+  for (int j = 0; j < TNW; ++j) store_f32_blk<NT>(acc[0][j], a, bidx, mw, nw + 32 * j, lane);
+}
+
+// MFMA phase of a window whose A is staged: the fragments of k16 step kk+1
+// are read from LDS while step kk multiplies.  The layouts are template
+// parameters, so the loop has no branches around its LDS reads (with the
+// layouts as runtime values every step waited for its own reads).
+template <int DT, int TNW, bool AKC, bool BKC>
+__device__ __forceinline__ void mfma_staged(f32x16 (&acc)[1][TNW], const char *lds_a, int pa,
+                                            const char *lds_b, int pb, int row0, int nw,
+                                            int ksteps, int lane) {
+  u32x4 fa = read_frag(lds_a, pa, AKC, row0, 0, lane);
+  u32x4 fb[TNW];
+#pragma unroll
+  for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, pb, BKC, nw + 32 * j, 0, lane);
+#pragma unroll 2
+  for (int kk = 0; kk < ksteps; ++kk) {
+    // The last step reads its own fragments again: in bounds, unused.
+    const int kn = kk + 1 < ksteps ? kk + 1 : kk;
+    const u32x4 na = read_frag(lds_a, pa, AKC, row0, kn, lane);
+    u32x4 nb[TNW];
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) nb[j] = read_frag(lds_b, pb, BKC, nw + 32 * j, kn, lane);
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
+    fa = na;
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) fb[j] = nb[j];
+  }
+}
+
+// MFMA phase of a window whose A fragments were loaded from memory (at most
+// four k16 steps): every B fragment of the step read before its MFMAs.
+template <int DT, int TNW, bool BKC>
+__device__ __forceinline__ void mfma_direct(f32x16 (&acc)[1][TNW], const u32x4 (&fad)[4],
+                                            const char *lds_b, int pb, int nw, int ksteps,
+                                            int lane) {
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    if (kk >= ksteps) break;
+    u32x4 fb[TNW];
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, pb, BKC, nw + 32 * j, kk, lane);
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fad[kk], fb[j], acc[0][j]);
+  }
+}
+
+// The same with the f32 buffer-store epilogue folded in, one 32-column block
+// at a time: the next block's B fragments are read while this block
+// multiplies, and this block's stores go out before the next block's MFMAs.
+template <int DT, int TNW, bool BKC, bool NT>
+__device__ __forceinline__ void mfma_direct_store(f32x16 (&acc)[1][TNW], const u32x4 (&fad)[4],
+                                                  const char *lds_b, int pb, int nw, int ksteps,
+                                                  const GemmArgs &a, int bidx, int mw, int n0,
+                                                  int lane) {
+  u32x4 fb[2][4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+    if (kk < ksteps) fb[0][kk] = read_frag(lds_b, pb, BKC, nw, kk, lane);
 #pragma unroll
   for (int j = 0; j < TNW; ++j) {
-    const int n = nw + j * 32 + lrow;
-    const uint32_t base = n < a.N ? (uint32_t)((mw + 4 * lh) * a.scm + n) * 4u : kOOB;
-    const float bv = (has_bias && n < a.N) ? bias_at(a.bias, a.bias_dt, n) : 0.0f;
+    if (j + 1 < TNW) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      float x = acc[0][j][v];
-      if (has_bias) x = x + bv;
-      if (has_gelu) x = gelu_tanh(x);
-      const uint32_t off = base + (uint32_t)(8 * (v >> 2) + (v & 3)) * rstep;
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rc, off, 0,
-                                            NT ? 2 : 0);  // 2: nontemporal
+      for (int kk = 0; kk < 4; ++kk)
+        if (kk < ksteps)
+          fb[(j + 1) & 1][kk] = read_frag(lds_b, pb, BKC, nw + 32 * (j + 1), kk, lane);
     }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      if (kk < ksteps) acc[0][j] = mfma_32x32x16<DT>(fad[kk], fb[j & 1][kk], acc[0][j]);
+    store_f32_blk<NT>(acc[0][j], a, bidx, mw, n0 + nw + 32 * j, lane);
   }
 }
 
@@ -285,25 +374,30 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
   const int ksteps = s.kp / 16;
   const int nw = wn * (TNW * 32);
   if constexpr (AD) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      if (kk >= ksteps) break;
-      u32x4 fb[TNW];
-#pragma unroll
-      for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, s.pb, s.b_kc, nw + 32 * j, kk, lane);
-#pragma unroll
-      for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fad[kk], fb[j], acc[0][j]);
+    if (s.buf_store) {
+      if (s.b_kc)
+        mfma_direct_store<DT, TNW, true, NT>(acc, fad, lds_b, s.pb, nw, ksteps, a, bidx,
+                                             m0 + wm * 32, n0, lane);
+      else
+        mfma_direct_store<DT, TNW, false, NT>(acc, fad, lds_b, s.pb, nw, ksteps, a, bidx,
+                                              m0 + wm * 32, n0, lane);
+      return;
     }
+    if (s.b_kc)
+      mfma_direct<DT, TNW, true>(acc, fad, lds_b, s.pb, nw, ksteps, lane);
+    else
+      mfma_direct<DT, TNW, false>(acc, fad, lds_b, s.pb, nw, ksteps, lane);
+  } else if (s.a_kc) {
+    if (s.b_kc)
+      mfma_staged<DT, TNW, true, true>(acc, lds_a, s.pa, lds_b, s.pb, wm * 32, nw, ksteps, lane);
+    else
+      mfma_staged<DT, TNW, true, false>(acc, lds_a, s.pa, lds_b, s.pb, wm * 32, nw, ksteps, lane);
   } else {
-#pragma unroll 2
-    for (int kk = 0; kk < ksteps; ++kk) {
-      const u32x4 fa = read_frag(lds_a, s.pa, s.a_kc, wm * 32, kk, lane);
-      u32x4 fb[TNW];
-#pragma unroll
-      for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, s.pb, s.b_kc, nw + 32 * j, kk, lane);
-#pragma unroll
-      for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
-    }
+    if (s.b_kc)
+      mfma_staged<DT, TNW, false, true>(acc, lds_a, s.pa, lds_b, s.pb, wm * 32, nw, ksteps, lane);
+    else
+      mfma_staged<DT, TNW, false, false>(acc, lds_a, s.pa, lds_b, s.pb, wm * 32, nw, ksteps,
+                                         lane);
   }
   if (s.buf_store)
     store_f32_buf<TNW, NT>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
