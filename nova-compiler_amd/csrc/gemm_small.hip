@@ -37,7 +37,8 @@ using namespace gemm;
 
 constexpr int kBM = 64;
 constexpr int kMaxNT = 256;
-constexpr int kLdsBytes = 80 * 1024;  // staging budget per workgroup (two fit a CU)
+constexpr int kLdsBytes = 80 * 1024;    // staging budget per workgroup (two fit a CU)
+constexpr int kCuLdsBytes = 160 * 1024;  // a CU's LDS, for a workgroup alone on its CU
 // Staging runs on eight waves, the MFMAs and the epilogue on the first four
 // (2x2 grid): staging is the long, latency-bound part.
 constexpr int kStageThreads = 512;
@@ -472,15 +473,17 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
   // budget and cut the workgroups a CU must run: each wave's share of the
   // work is the same, so the time follows the most loaded CU.  Config 4a:
   // 192 workgroups instead of 384 on 256 CUs, 11.40 -> 10.35 us, the same
-  // bits (in-process A/B).  Config 4b's 128-row A window does not fit (95 KB;
-  // with that much LDS it had measured 9.70 against 9.54 us).
+  // bits (in-process A/B).  When there are no more such workgroups than CUs,
+  // each has a CU to itself and may use its whole LDS: config 4b's 128-row
+  // A window (95 KB) then runs 7.73 against 7.91 us in 64-row windows.
   {
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const int64_t tn = (a_in.N + p.nt - 1) / p.nt;
     const int64_t t64 = (int64_t)a_in.batch * ((a_in.M + kBM - 1) / kBM) * tn;
     const int64_t t128 = (int64_t)a_in.batch * ((a_in.M + 2 * kBM - 1) / (2 * kBM)) * tn;
     const SmallPlan p2 = plan_small(a_in.N, a_in.K, akc, bkc, 2 * kBM);
-    if (p2.lds <= (size_t)kLdsBytes && (t128 + cus - 1) / cus < (t64 + cus - 1) / cus) {
+    const size_t budget = t128 <= cus ? (size_t)kCuLdsBytes : (size_t)kLdsBytes;
+    if (p2.lds <= budget && (t128 + cus - 1) / cus < (t64 + cus - 1) / cus) {
       p = p2;
       s.bm = 2 * kBM;
     }

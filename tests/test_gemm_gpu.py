@@ -534,6 +534,24 @@ def test_gemm_small_direct_a_exact(cuda, dt, shape):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("dt", [S.F16, S.BF16])
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("shape", [(100, 150, 50, 40), (96, 197, 64, 197)])
+def test_gemm_small_128_row_windows_exact(cuda, dt, layout, shape):
+    """The small-K kernel in 128-row windows with A staged: more 64-row tiles
+    than CUs, so the 128-row form (eight computing waves) is chosen, and at
+    K = 197 its staging (up to ~106 KB with A transposed) only fits because
+    each workgroup has a CU to itself.  Integer-valued inputs make every
+    product and sum exact, so every layout must equal the oracle exactly."""
+    batch, M, N, K = shape
+    g = np.random.default_rng(73)
+    a = S.round_to(g.integers(-4, 5, (batch, M, K)).astype(np.float32), dt)
+    b = S.round_to(g.integers(-4, 5, (batch, K, N)).astype(np.float32), dt)
+    got = nh.gemm(view_as(a, layout[0], cuda, dt), view_as(b, layout[1], cuda, dt)).cpu().numpy()
+    want = ref.gemm(a, b, adt=dt, bdt=dt)
+    assert np.array_equal(got, want), f"{shape} {layout} dt={dt}"
+
+
 @pytest.mark.parametrize("cfg", ["c4a", "c4b"])
 def test_c4_fp16_unaligned_full(cuda, cfg):
     """Config 4: fp16 batch GEMM with non-tile-aligned shapes (edge tiles)."""
