@@ -15,8 +15,8 @@
 // a sum rounded first to f32 (24 bits) then to a p-bit type is the
 // correctly rounded p-bit sum whenever 24 >= 2p + 2 (p = 8 for bf16, 11 for
 // f16), so this is the narrow type's own IEEE arithmetic.  The reference's GPU path
-// would have used tf32 mma.sync for f32 (SURVEY of
-// NovaGPUNestedLayoutDistributionPatterns.cpp:2460); this kernel does not,
+// would have used tf32 mma.sync for f32
+// (NovaGPUNestedLayoutDistributionPatterns.cpp:2460); this kernel does not,
 // because tf32 breaks 1e-4 parity.
 //
 // Two families, with the same per-output arithmetic (so the same bits):
