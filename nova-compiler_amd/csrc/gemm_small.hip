@@ -28,6 +28,8 @@
 // 32-column block is stored before the next block multiplies (configs 4a /
 // 4b: 9.66 -> 8.94 / 8.75 -> 8.19 us, the same bits).  The epilogue writes
 // bounds-checked coalesced stores.
+#include <algorithm>
+
 #include "gemm_common.h"
 
 namespace nova_hip {
@@ -482,7 +484,8 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
     const int64_t t64 = (int64_t)a_in.batch * ((a_in.M + kBM - 1) / kBM) * tn;
     const int64_t t128 = (int64_t)a_in.batch * ((a_in.M + 2 * kBM - 1) / (2 * kBM)) * tn;
     const SmallPlan p2 = plan_small(a_in.N, a_in.K, akc, bkc, 2 * kBM);
-    const size_t budget = t128 <= cus ? (size_t)kCuLdsBytes : (size_t)kLdsBytes;
+    const size_t cu_lds = (size_t)std::min(kCuLdsBytes, device_lds_per_block());
+    const size_t budget = t128 <= cus ? std::max(cu_lds, (size_t)kLdsBytes) : (size_t)kLdsBytes;
     if (p2.lds <= budget && (t128 + cus - 1) / cus < (t64 + cus - 1) / cus) {
       p = p2;
       s.bm = 2 * kBM;

@@ -39,20 +39,31 @@ void clear_error() { t_err[0] = 0; }
 
 hipStream_t current_stream() { return t_stream; }
 
-int device_cu_count() {
-  constexpr int kMaxDevices = 64;
-  static std::atomic<int> cache[kMaxDevices];  // 0: not queried yet
+namespace {
+// A device attribute of the current device, queried once per device.
+int cached_attribute(std::atomic<int> *cache, int n, hipDeviceAttribute_t attr) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < kMaxDevices) {
-    const int c = cache[dev].load(std::memory_order_relaxed);
+  if (dev < n) {
+    const int c = cache[dev].load(std::memory_order_relaxed);  // 0: not queried yet
     if (c) return c > 0 ? c : 0;
   }
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 0;
-  if (dev < kMaxDevices) cache[dev].store(cus > 0 ? cus : -1, std::memory_order_relaxed);
-  return cus > 0 ? cus : 0;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, attr, dev) != hipSuccess) v = 0;
+  if (dev < n) cache[dev].store(v > 0 ? v : -1, std::memory_order_relaxed);
+  return v > 0 ? v : 0;
+}
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+int device_cu_count() {
+  static std::atomic<int> cache[kMaxDevices];
+  return cached_attribute(cache, kMaxDevices, hipDeviceAttributeMultiprocessorCount);
+}
+
+int device_lds_per_block() {
+  static std::atomic<int> cache[kMaxDevices];
+  return cached_attribute(cache, kMaxDevices, hipDeviceAttributeMaxSharedMemoryPerBlock);
 }
 
 int32_t check_hip(hipError_t e, const char *what) {

@@ -18,6 +18,8 @@ hipStream_t current_stream();
 // Compute units of the current device (cached per device), or 0 if the
 // query fails.
 int device_cu_count();
+// LDS bytes one workgroup may use on the current device (0 if unknown).
+int device_lds_per_block();
 // Convert a HIP status into NOVA_HIP_EDEVICE with text, or success.
 int32_t check_hip(hipError_t e, const char *what);
 
