@@ -105,6 +105,47 @@ def test_sce_repeat_calls_identical(cuda):
     assert_close_f32(l3.cpu().numpy(), ref17, "second, smaller call")
 
 
+def _chunk_mean_f32(v):
+    """The mean in the order of lowerFullReduceMeanToSCF
+    (NovaToLinalg.cpp:1974-2126): 64 contiguous chunks of ceil(R/64) rows,
+    each summed sequentially in f32, the chunk sums sequentially, then / R."""
+    R = len(v)
+    per = (R + 63) // 64
+    total = np.float32(0)
+    for c in range(64):
+        p = np.float32(0)
+        for r in range(c * per, min(c * per + per, R)):
+            p = np.float32(p + v[r])
+        total = np.float32(total + p)
+    return np.float32(total / np.float32(R))
+
+
+@pytest.mark.parametrize("rows,C", [(5, 2052), (1000, 2052), (4173, 2052), (64, 32000)])
+def test_sce_mean_is_the_chunked_order_of_its_row_losses(cuda, rows, C):
+    """Each row's loss, taken from a one-row call (whose mean is the row loss
+    itself), summed on the host in the reference's 64-chunk order, gives the
+    batched call's loss bit for bit: the device mean keeps that order
+    exactly, for chunks of one row, 16 and 66 rows (more than one wave's
+    worth) and 64 chunks of one row each.  The fused forward+backward gives
+    the same loss bits."""
+    import torch
+    x = S.normal((rows, C), 47, 0, 2)
+    t = S.labels(rows, C, 47, offset=rows * C)
+    X, T = dev(x, cuda), dev(t, cuda)
+    single = np.empty(rows, np.float32)
+    for r in range(rows):
+        _, lr = nh.sce(X[r:r + 1], T[r:r + 1])
+        single[r] = lr.cpu().numpy()[0]
+    _, loss = nh.sce(X, T)
+    want = _chunk_mean_f32(single)
+    got = loss.cpu().numpy()[0]
+    assert got.view(np.uint32) == want.view(np.uint32), (got, want)
+    lf, _ = nh.sce_fwd_bwd(X, T)
+    assert torch.equal(lf, loss)
+    _, loss_ref, _ = ref.sce(x, t)
+    assert_close_f32(loss.cpu().numpy(), loss_ref, f"sce {rows}x{C}")
+
+
 def test_sce_strided_rows(cuda):
     wide = S.normal((40, 600), 43, 0, 2)
     t = S.labels(40, 500, 43, offset=2 * 40 * 600)
