@@ -1,0 +1,303 @@
+/* nova_forms.h -- the op forms the libnova_hip path lowers.
+ *
+ * One table, consulted by both carriers of the Nova -> libnova_hip rewrite:
+ * the MLIR-free planner (libnova_run, nova-compiler_amd/runtime/nova_run.cpp)
+ * and the nova-hip-lower MLIR pass (nova-compiler_amd/mlir/
+ * NovaHipLowering.cpp).  Each asks nova_forms::check() about every op it
+ * would rewrite and declines exactly the forms it rejects, with the reason it
+ * gives, so the two accept the same programs.  tests/test_forms.py drives
+ * the planner through every row of kRankForms and every dtype rule below.
+ *
+ * Header-only C++17: no MLIR, HIP or torch types.
+ *
+ * What a row means: operand i of the op may have rank min_rank[i] ..
+ * max_rank[i]; leading dims of a GEMM or row operand fold into its batch or
+ * row dim.  The shape, broadcast and element-type rules of each op follow
+ * the reference's lowering patterns (file:line per rule in check()).
+ */
+#ifndef NOVA_FORMS_H
+#define NOVA_FORMS_H
+
+#include <stdint.h>
+#include <string.h>
+
+#include "nova_hip.h"
+
+namespace nova_forms {
+
+constexpr int kMaxOperands = 5;
+constexpr int kMaxRank = 8;
+
+struct RankForm {
+  const char *op;
+  int nops;
+  int min_rank[kMaxOperands];
+  int max_rank[kMaxOperands];
+};
+
+// clang-format off
+inline constexpr RankForm kRankForms[] = {
+  // lhs [..., M, K], rhs [..., K, N]                     NovaToLinalg.cpp:874-1051
+  {"nova.matmul",              2, {2, 2},             {kMaxRank, kMaxRank}},
+  // ins (A, B) and the zero-filled outs                  (linalg named ops)
+  {"linalg.matmul",            3, {2, 2, 2},          {2, 2, 2}},
+  {"linalg.batch_matmul",      3, {3, 3, 3},          {3, 3, 3}},
+  // input [..., M, K], weight [K, N], bias [N]          NovaToLinalgGeneric.cpp:1623-1822
+  {"nova.linear",              3, {2, 2, 1},          {kMaxRank, 2, 1}},
+  // input [..., D], gamma [D], beta [D]                  NovaToLinalgGeneric.cpp:1997-2126
+  {"nova.layer_norm",          3, {2, 1, 1},          {kMaxRank, 1, 1}},
+  // logits [..., C], targets [...]                       NovaToLinalgGeneric.cpp:801-1010
+  {"nova.sce",                 2, {2, 1},             {kMaxRank, kMaxRank - 1}},
+  // softmax [..., C], targets [...]                      NovaToLinalgGeneric.cpp:1012-1137
+  {"nova.sce_backward",        2, {2, 1},             {kMaxRank, kMaxRank - 1}},
+  // grad_y [..., D], x [..., D], gamma [D], mean_sum [...], var_sum [...]
+  //                                                      NovaToLinalgGeneric.cpp:2128-2371
+  {"nova.layer_norm_backward", 5, {2, 2, 1, 1, 1},    {kMaxRank, kMaxRank, 1, kMaxRank - 1, kMaxRank - 1}},
+  // grad_out [..., M, N], input [..., M, K], weight [K, N]
+  //                                                      NovaToLinalgGeneric.cpp:1824-1996
+  {"nova.linear_backward",     3, {2, 2, 2},          {kMaxRank, kMaxRank, 2}},
+  // grad [M, N], a [M, K], b [K, N]: the pattern reads shape[0] / shape[1]
+  //                                                      NovaToLinalgGeneric.cpp:160-239
+  {"nova.matmul_backward",     3, {2, 2, 2},          {2, 2, 2}},
+  // program glue (elementwise f32, numpy broadcasting up to rank 4)
+  {"nova.add",                 2, {0, 0},             {4, 4}},
+  {"nova.sub",                 2, {0, 0},             {4, 4}},
+  {"nova.mul",                 2, {0, 0},             {4, 4}},
+  {"nova.div",                 2, {0, 0},             {4, 4}},
+  {"nova.gelu",                1, {0},                {kMaxRank}},
+  {"nova.gelu_backward",       2, {0, 0},             {kMaxRank, kMaxRank}},
+  // table [V, D] along axis 0, indices [...]             NovaToLinalgGeneric.cpp:2372-2471
+  {"nova.gather",              2, {2, 0},             {2, kMaxRank}},
+  // input [V, D] along axis 0, indices [...], src [..., D]  NovaToLinalg.cpp:1086-1290
+  {"nova.scatter_add",         3, {2, 0, 1},          {2, kMaxRank, kMaxRank}},
+  {"nova.reduce<sum>",         1, {1},                {kMaxRank}},
+  {"nova.constant",            0, {},                 {}},
+};
+// clang-format on
+
+inline const RankForm *rank_form(const char *op) {
+  for (const RankForm &f : kRankForms)
+    if (strcmp(f.op, op) == 0) return &f;
+  return nullptr;
+}
+
+// An operand as the carrier sees it.
+struct Operand {
+  int stored = -1;   // element type in memory (NOVA_HIP_DT_*; -1 for any other)
+  int logical = -1;  // element type the op reads: f32 through a widening nova.cast
+  int rank = 0;
+  const int64_t *shape = nullptr;
+};
+
+// Attributes some forms depend on.
+struct Attrs {
+  int axis = 0;            // nova.gather / nova.scatter_add axis (normalised)
+  int dim = -1;            // nova.sce_backward class dim (normalised; -1 = last)
+  bool splat_f32 = true;   // nova.constant: a splat dense<value> of f32
+  bool ignore_nan = false; // nova.reduce
+  bool adjacent = true;    // nova.reduce: the reduced dims are adjacent
+};
+
+inline bool is_float(int dt) {
+  return dt == NOVA_HIP_DT_F32 || dt == NOVA_HIP_DT_BF16 || dt == NOVA_HIP_DT_F16;
+}
+inline bool is_index(int dt) {
+  return dt == NOVA_HIP_DT_I32 || dt == NOVA_HIP_DT_I64 || dt == NOVA_HIP_DT_I16;
+}
+
+// Batch dims of an operand of rank r in a product whose result has batch
+// rank nb: either all equal to the result's, or all 1 (a rank-2 operand
+// included), which the GEMM entry point broadcasts with batch stride 0.
+// A partial broadcast (some batch dims 1, others not) is declined: the
+// reference materialises it (broadcastTensor, NovaToLinalg.cpp:904-925),
+// the entry point addresses one batch stride.
+inline bool batch_ok(const Operand &o, const int64_t *res_batch, int nb) {
+  const int ob = o.rank - 2;
+  bool all_one = true, all_eq = ob == nb;
+  for (int i = 0; i < ob; ++i) {
+    all_one = all_one && o.shape[i] == 1;
+    all_eq = all_eq && o.shape[i] == res_batch[i];
+  }
+  return all_one || all_eq;
+}
+
+// Element types of a GEMM (nova.matmul, nova.linear, linalg.(batch_)matmul):
+// both operands stored as one 16- or 32-bit float type; the result is f32
+// (accumulated in f32: f32 operands, or 16-bit data read through a widening
+// nova.cast / into f32 linalg outs), or a 16-bit type equal to the stored
+// and logical operand type (accumulated in that type, as a linalg.matmul
+// with narrow outs does, NovaToLinalg.cpp:1027-1049).  A bf16 x bf16
+// nova.matmul infers an f16 result (NovaOps.cpp:1198), a bf16 -> f16
+// accumulation whose arithmetic is not pinned here: declined.
+inline const char *gemm_dtypes(const Operand &a, const Operand &b, int out, const Operand *bias) {
+  if (a.stored != b.stored) return "GEMM operands are stored as different element types";
+  if (!is_float(a.stored)) return "GEMM operands must be f32, bf16 or f16";
+  if (a.stored == NOVA_HIP_DT_F32 && out != NOVA_HIP_DT_F32) return "f32 operands give f32 results only";
+  const bool narrow = out != NOVA_HIP_DT_F32;
+  if (narrow && !is_float(out)) return "GEMM result must be f32, bf16 or f16";
+  if (narrow && (a.logical != a.stored || b.logical != b.stored || a.stored != out))
+    return "a 16-bit GEMM result accumulates in its own type; only operands of that same type "
+           "(not cast) are on this path (spell the f32-accumulate form: nova.cast the operands "
+           "to f32, or f32 linalg outs)";
+  if (bias) {
+    if (!is_float(bias->stored)) return "bias must be f32, bf16 or f16";
+    if (narrow && (bias->stored != out || bias->logical != bias->stored))
+      return "a 16-bit accumulator needs a bias of its own type";
+  }
+  return nullptr;
+}
+
+// nullptr when the op is on the path with these operands and result element
+// types; otherwise the reason (a static string).
+inline const char *check(const char *op, int nops, const Operand *in, int nres,
+                         const int *res_dt, const Attrs &at = Attrs()) {
+  const RankForm *f = rank_form(op);
+  if (!f) return "not part of this path's op surface";
+  if (nops != f->nops) return "wrong number of operands";
+  for (int i = 0; i < nops; ++i) {
+    if (in[i].rank < f->min_rank[i] || in[i].rank > f->max_rank[i])
+      return "operand rank outside the form (see nova_forms.h)";
+  }
+  auto last = [&](int i, int k) { return in[i].shape[in[i].rank - 1 - k]; };
+  auto same_lead = [&](int i, int j, int keep_i, int keep_j) {
+    // shape[:-keep_i] of operand i equals shape[:-keep_j] of operand j
+    if (in[i].rank - keep_i != in[j].rank - keep_j) return false;
+    for (int d = 0; d < in[i].rank - keep_i; ++d)
+      if (in[i].shape[d] != in[j].shape[d]) return false;
+    return true;
+  };
+  const int out = nres > 0 ? res_dt[0] : -1;
+
+  if (!strcmp(op, "nova.matmul") || !strcmp(op, "linalg.matmul") ||
+      !strcmp(op, "linalg.batch_matmul")) {
+    if (last(0, 0) != last(1, 1)) return "contraction dims differ";
+    // Result batch: the broadcast of both operands' batch dims.
+    const int nb = (in[0].rank > in[1].rank ? in[0].rank : in[1].rank) - 2;
+    int64_t rb[kMaxRank] = {};
+    for (int d = 0; d < nb; ++d) {
+      const int i0 = d - (nb - (in[0].rank - 2)), i1 = d - (nb - (in[1].rank - 2));
+      const int64_t x = i0 >= 0 ? in[0].shape[i0] : 1, y = i1 >= 0 ? in[1].shape[i1] : 1;
+      if (x != y && x != 1 && y != 1) return "batch dims do not broadcast";
+      rb[d] = x == 1 ? y : x;
+    }
+    if (!batch_ok(in[0], rb, nb) || !batch_ok(in[1], rb, nb))
+      return "an operand's batch dims are partly broadcast (only batch dims equal to the "
+             "result's, or all 1, are on this path)";
+    if (!strcmp(op, "linalg.batch_matmul") && (in[0].shape[0] != in[2].shape[0] ||
+                                               in[1].shape[0] != in[2].shape[0]))
+      return "linalg.batch_matmul batch sizes differ";
+    return gemm_dtypes(in[0], in[1], out, nullptr);
+  }
+  if (!strcmp(op, "nova.linear")) {
+    if (last(0, 0) != in[1].shape[0]) return "input and weight contraction dims differ";
+    if (in[2].shape[0] != in[1].shape[1]) return "bias size is not the weight's columns";
+    return gemm_dtypes(in[0], in[1], out, &in[2]);
+  }
+  if (!strcmp(op, "nova.linear_backward") || !strcmp(op, "nova.matmul_backward")) {
+    // grad_out [..., M, N], input [..., M, K], weight [K, N]
+    if (!same_lead(0, 1, 1, 1)) return "grad_out and input leading dims differ";
+    if (last(1, 0) != in[2].shape[0] || last(0, 0) != in[2].shape[1])
+      return "weight is not [K, N] of input [..., K] and grad_out [..., N]";
+    if (in[0].stored != in[1].stored || in[1].stored != in[2].stored)
+      return "backward GEMM operands must share a stored element type";
+    if (!is_float(in[1].stored)) return "backward GEMM operands must be f32, bf16 or f16";
+    // The reference accumulates in the result type (linalg.generic over
+    // zero-filled outs); the entry points accumulate in f32: f32 results only
+    // (f32 operands, or 16-bit data read through a widening nova.cast).
+    for (int r = 0; r < nres; ++r)
+      if (res_dt[r] != NOVA_HIP_DT_F32)
+        return "backward GEMMs with 16-bit results (a 16-bit accumulator) are not on this path";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.layer_norm")) {
+    if (in[1].shape[0] != last(0, 0) || in[2].shape[0] != last(0, 0))
+      return "gamma / beta are not [D]";
+    for (int i = 0; i < 3; ++i)
+      if (in[i].stored != NOVA_HIP_DT_F32 || in[i].logical != NOVA_HIP_DT_F32)
+        return "layer_norm operands must be stored f32";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.layer_norm_backward")) {
+    if (!same_lead(0, 1, 0, 0)) return "grad_y and x shapes differ";
+    if (in[2].shape[0] != last(1, 0)) return "gamma is not [D]";
+    for (int i = 3; i < 5; ++i) {
+      int64_t n = 1, r = 1;
+      for (int d = 0; d < in[i].rank; ++d) n *= in[i].shape[d];
+      for (int d = 0; d + 1 < in[1].rank; ++d) r *= in[1].shape[d];
+      if (n != r) return "saved statistics are not one per row";
+    }
+    for (int i = 0; i < 5; ++i)
+      if (in[i].stored != NOVA_HIP_DT_F32 || in[i].logical != NOVA_HIP_DT_F32)
+        return "layer_norm_backward operands must be stored f32";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.sce") || !strcmp(op, "nova.sce_backward")) {
+    if (!same_lead(0, 1, 1, 0)) return "targets are not one per row of the logits";
+    if (in[0].stored != NOVA_HIP_DT_F32 || in[0].logical != NOVA_HIP_DT_F32)
+      return "logits / softmax must be stored f32";
+    if (!is_index(in[1].stored)) return "targets must be i16, i32 or i64";
+    if (!strcmp(op, "nova.sce_backward") && at.dim != -1 && at.dim != in[0].rank - 1)
+      return "sce_backward over a dim other than the last";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.add") || !strcmp(op, "nova.sub") || !strcmp(op, "nova.mul") ||
+      !strcmp(op, "nova.div")) {
+    const int n = in[0].rank > in[1].rank ? in[0].rank : in[1].rank;
+    for (int d = 0; d < n; ++d) {
+      const int i0 = d - (n - in[0].rank), i1 = d - (n - in[1].rank);
+      const int64_t x = i0 >= 0 ? in[0].shape[i0] : 1, y = i1 >= 0 ? in[1].shape[i1] : 1;
+      if (x != y && x != 1 && y != 1) return "shapes do not broadcast";
+    }
+    for (int i = 0; i < 2; ++i)
+      if (in[i].stored != NOVA_HIP_DT_F32 || in[i].logical != NOVA_HIP_DT_F32)
+        return "elementwise operands must be stored f32";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.gelu") || !strcmp(op, "nova.gelu_backward")) {
+    for (int i = 0; i < nops; ++i)
+      if (in[i].stored != NOVA_HIP_DT_F32 || in[i].logical != NOVA_HIP_DT_F32)
+        return "gelu operands must be stored f32";
+    if (nops == 2) {
+      int64_t a = 1, b = 1;
+      for (int d = 0; d < in[0].rank; ++d) a *= in[0].shape[d];
+      for (int d = 0; d < in[1].rank; ++d) b *= in[1].shape[d];
+      if (a != b) return "gelu_backward operand sizes differ";
+    }
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.gather")) {
+    if (at.axis != 0) return "gather along axis 0 only";
+    if (in[0].stored != NOVA_HIP_DT_F32 || in[0].logical != NOVA_HIP_DT_F32)
+      return "gather table must be stored f32";
+    if (!is_index(in[1].stored)) return "gather indices must be i16, i32 or i64";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.scatter_add")) {
+    if (at.axis != 0) return "scatter_add along axis 0 only";
+    if (in[0].stored != NOVA_HIP_DT_F32 || in[2].stored != NOVA_HIP_DT_F32 ||
+        in[0].logical != NOVA_HIP_DT_F32 || in[2].logical != NOVA_HIP_DT_F32)
+      return "scatter_add input and src must be stored f32";
+    if (!is_index(in[1].stored)) return "scatter_add indices must be i16, i32 or i64";
+    int64_t ni = 1, ns = 1;
+    for (int d = 0; d < in[1].rank; ++d) ni *= in[1].shape[d];
+    for (int d = 0; d < in[2].rank; ++d) ns *= in[2].shape[d];
+    if (ns != ni * in[0].shape[1]) return "scatter_add src is not [indices, D]";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.reduce<sum>")) {
+    if (at.ignore_nan) return "reduce ignore_nan is not on this path";
+    if (!at.adjacent) return "reduce over non-adjacent dims";
+    if (in[0].stored != NOVA_HIP_DT_F32 || in[0].logical != NOVA_HIP_DT_F32)
+      return "reduce input must be stored f32";
+    return nullptr;
+  }
+  if (!strcmp(op, "nova.constant")) {
+    if (!at.splat_f32) return "nova.constant other than an f32 splat dense<value>";
+    return nullptr;
+  }
+  return "not part of this path's op surface";
+}
+
+}  // namespace nova_forms
+
+#endif  // NOVA_FORMS_H

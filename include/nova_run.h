@@ -73,7 +73,12 @@ int32_t nova_run_execute(const NovaRunProgram *p, const char *func, const void *
  * launches are queued on the calling thread's libnova_hip stream and the
  * call returns without synchronising (nova_hip_synchronize waits).
  * Intermediates live in device buffers the program keeps and reuses on the
- * next execution, as for nova_run_execute. */
+ * next execution, as for nova_run_execute.  Executions of one function share
+ * those buffers, so each waits on the device (hipStreamWaitEvent, not on
+ * the host) for the previous one to finish, whatever stream that ran on:
+ * executions on several streams are ordered, never concurrent.  A plan
+ * whose buffer sizes changed frees the old buffers only after the previous
+ * execution has completed. */
 int32_t nova_run_execute_device(const NovaRunProgram *p, const char *func,
                                 void *const *dev_args, void *const *dev_results);
 

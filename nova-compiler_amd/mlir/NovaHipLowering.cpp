@@ -1,13 +1,21 @@
-//===- NovaHipLowering.cpp - Nova hot ops -> calls into libnova_hip -------===//
+//===- NovaHipLowering.cpp - Nova ops -> calls into libnova_hip -----------===//
 //
-// The lowering that takes Nova's GPU matmul / reduction ops off the
-// IREE-derived LLVMGPU sequence (lib/Transforms/LLVMGPU/Passes.cpp:115-372:
-// TileAndDistribute, PromoteMatmulOperands, PadOperands, vector
-// distribution, multibuffering) and calls the hand-written gfx950 kernels of
-// libnova_hip instead.  It runs on the Nova ops themselves, ahead of
-// Nova -> Linalg (Passes.cpp:88-90), so the ops it rewrites never reach that
-// sequence; every other op, and every form below it declines, keeps the
-// existing path.
+// UNCOMPILED PROTOTYPE.  This image has no MLIR, so this file has never been
+// built; its tested counterpart is the MLIR-free planner
+// (runtime/nova_run.cpp), which carries the same rewrite and which every GPU
+// test runs.  Both decide which op forms they lower from one table,
+// include/nova_forms.h (nova_forms::check), so they accept and decline the
+// same forms.
+//
+// The lowering takes Nova's GPU matmul / reduction ops (and the program glue
+// around them) off the IREE-derived LLVMGPU sequence
+// (lib/Transforms/LLVMGPU/Passes.cpp:115-372: TileAndDistribute,
+// PromoteMatmulOperands, PadOperands, vector distribution, multibuffering)
+// and calls the hand-written gfx950 kernels of libnova_hip instead.  It runs
+// on the Nova ops themselves, ahead of Nova -> Linalg (Passes.cpp:88-90), so
+// the ops it rewrites never reach that sequence.  A form the table declines
+// keeps the existing path; with strict=true the pass instead fails on it
+// (that path emits NVPTX, which cannot run on AMD).
 //
 // Each rewritten op becomes, in tensor form:
 //   %b_i  = bufferization.to_buffer %operand_i read_only   (a view: see below)
@@ -19,30 +27,36 @@
 // LLVM lowering calls _mlir_ciface_nova_hip_<op>(StridedMemRefType<T,R>*...),
 // the entry points include/nova_hip.h declares.  Every buffer is passed as a
 // memref with dynamic sizes, strides and offset: the descriptor layout of
-// the C interface, whatever the static type.  One-shot bufferization later
-// resolves the to_buffer / to_tensor pairs.
+// the C interface, whatever the static type.  The memref.alloc results are
+// what the reference pipeline's ConvertMemRefToGpu turns into device
+// allocations (ConvertMemRefToGpu.cpp:37-63).
 //
-// The op forms and folds are those of the MLIR-free planner that carries the
-// same rewrite in this repository (runtime/nova_run.cpp), one pattern each:
+// Every lowering first reads its operands, its folds and the table's verdict,
+// and checks that each callee it needs can be declared with the type it
+// needs; only then does it create ops.  A declined op leaves the IR as it was.
+//
+// Views and folds (the planner's, one each):
 //   * nova.transpose of the last two dims feeding a GEMM operand is a
 //     memref.transpose view (strided), not a copy;
-//   * a widening nova.cast (bf16 / f16 -> f32) feeding a GEMM operand is
-//     dropped: the kernel reads the narrow data and accumulates in f32;
+//   * a widening nova.cast (bf16 / f16 -> f32) feeding a GEMM operand or
+//     bias is dropped: the kernel reads the narrow data and accumulates in
+//     f32;
 //   * nova.linear / nova.matmul followed by a nova.gelu that is the result's
 //     only use, and then a narrowing nova.cast that is the only use, fold
 //     into the GEMM's epilogue (bias -> GELU -> round to bf16 / f16);
-//   * bf16 / f16 GEMMs whose result keeps the narrow type accumulate in it
-//     (NOVA_HIP_GEMM_ACC_OUT), as linalg.matmul with narrow outs does; a
-//     bf16 x bf16 nova.matmul (f16 result, NovaOps.cpp:1198) is declined;
+//   * leading dims fold into the batch (GEMMs) or row dim (row ops) through
+//     collapse_shape views of the dense buffers: rank > 3 nova.matmul as
+//     NovaToLinalg.cpp:904-988 collapses them, rank-3 nova.linear_backward
+//     (the reference GPT step's own form, ltest/test.mlir:40, 42) as
+//     [B*M, .];
 //   * nova.sce whose softmax feeds only a nova.sce_backward over the same
 //     targets is one fused call, and the softmax is never materialised;
-//   * non-i32 targets are widened by nova_hip_index_to_i32 first.
+//   * non-i32 targets / indices are widened by nova_hip_index_to_i32_* first.
 // f32 GEMMs run the exact kernel (bit-identical to the CPU pipeline) unless
 // the pass option f32-gemm=mfma selects the f32 matrix cores.
 //
 // Built only where MLIR is available (CMakeLists.txt next to this file,
-// find_package(MLIR)): this repository's image has none, so the planner is
-// the tested carrier of the rewrite.
+// find_package(MLIR)).
 //===----------------------------------------------------------------------===//
 
 #include "Compiler/Dialect/nova/NovaDialect.h"
@@ -53,6 +67,7 @@
 #include "mlir/Dialect/ControlFlow/IR/ControlFlowOps.h"
 #include "mlir/Dialect/Func/IR/FuncOps.h"
 #include "mlir/Dialect/LLVMIR/LLVMDialect.h"
+#include "mlir/Dialect/Linalg/IR/Linalg.h"
 #include "mlir/Dialect/MemRef/IR/MemRef.h"
 #include "mlir/IR/AffineMap.h"
 #include "mlir/IR/BuiltinOps.h"
@@ -62,6 +77,7 @@
 #include "llvm/ADT/SmallPtrSet.h"
 #include "llvm/ADT/TypeSwitch.h"
 
+#include "nova_forms.h"
 #include "nova_hip.h"
 
 using namespace mlir;
@@ -90,9 +106,9 @@ MemRefType abiType(Type elem, int64_t rank) {
                          StridedLayoutAttr::get(elem.getContext(), kDyn, strides));
 }
 
-bool staticRanked(Value v) {
+RankedTensorType staticTensor(Value v) {
   auto t = dyn_cast<RankedTensorType>(v.getType());
-  return t && t.hasStaticShape();
+  return t && t.hasStaticShape() ? t : RankedTensorType();
 }
 
 Value singleUse(Value v) { return v.hasOneUse() ? v : Value(); }
@@ -105,16 +121,16 @@ struct GemmOperand {
   Type stored;  // element type of the data read
 };
 
+bool widening(CastOp c) {
+  Type from = getElementTypeOrSelf(c.getInput().getType());
+  return getElementTypeOrSelf(c.getType()).isF32() && (from.isBF16() || from.isF16());
+}
+
 GemmOperand traceOperand(Value v) {
   GemmOperand o;
   o.tensor = v;
-  // f32 view of narrow data: nova.cast bf16 / f16 -> f32 (exact widening).
-  if (auto c = v.getDefiningOp<CastOp>()) {
-    Type from = getElementTypeOrSelf(c.getInput().getType());
-    Type to = getElementTypeOrSelf(c.getType());
-    if (to.isF32() && (from.isBF16() || from.isF16())) o.tensor = c.getInput();
-  }
-  // nova.transpose of the last two dims, before or after the cast.
+  if (auto c = v.getDefiningOp<CastOp>())
+    if (widening(c)) o.tensor = c.getInput();
   if (auto t = o.tensor.getDefiningOp<TransposeOp>()) {
     auto ty = cast<RankedTensorType>(t.getInput().getType());
     const int64_t r = ty.getRank();
@@ -124,56 +140,108 @@ GemmOperand traceOperand(Value v) {
     if (r >= 2 && ((a1 == r - 1 && a2 == r - 2) || (a1 == r - 2 && a2 == r - 1))) {
       o.tensor = t.getInput();
       o.transposed = true;
-      if (auto c = o.tensor.getDefiningOp<CastOp>()) {
-        Type from = getElementTypeOrSelf(c.getInput().getType());
-        if (getElementTypeOrSelf(c.getType()).isF32() && (from.isBF16() || from.isF16()))
-          o.tensor = c.getInput();
-      }
+      if (auto c = o.tensor.getDefiningOp<CastOp>())
+        if (widening(c)) o.tensor = c.getInput();
     }
   }
   o.stored = getElementTypeOrSelf(o.tensor.getType());
   return o;
 }
 
+// The operands of one op as nova_forms sees them.
+struct Form {
+  SmallVector<nova_forms::Operand, 5> ops;
+  SmallVector<SmallVector<int64_t, 8>, 5> shapes;
+  bool ok = true;  // every operand a static ranked tensor
+  // `v` is the value the op reads (its shape and logical type); `stored` the
+  // element type of the data behind it (through folded casts).
+  void add(Value v, Type stored) {
+    auto t = staticTensor(v);
+    if (!t) {
+      ok = false;
+      return;
+    }
+    shapes.emplace_back(t.getShape().begin(), t.getShape().end());
+    nova_forms::Operand o;
+    o.stored = dtypeCode(stored);
+    o.logical = dtypeCode(t.getElementType());
+    o.rank = (int)t.getRank();
+    ops.push_back(o);
+  }
+  void add(Value v) { add(v, getElementTypeOrSelf(v.getType())); }
+};
+
 class Lowerer {
  public:
   Lowerer(ModuleOp m, bool f32Mfma) : module(m), rewriter(m.getContext()), f32Mfma(f32Mfma) {}
 
-  // Buffer of a tensor value, as the ABI memref type: optionally the
-  // transposed view of its last two dims, and a rank-2 value optionally as
-  // [1, M, N] (a batch of one, which the GEMM entry points broadcast).
-  Value abiBuffer(Location loc, Value tensor, bool transposed = false, bool rank3 = false) {
+  // Ops the table declined (for strict mode), with the reason.
+  SmallVector<std::pair<Operation *, std::string>> declinedOps;
+
+  // Asks the form table about `op` (named `name` there).  True, and the op
+  // recorded with the reason, when the op is not on this path.
+  bool declined(Operation *op, const char *name, Form &f, const nova_forms::Attrs &at = {}) {
+    if (!f.ok) {
+      declinedOps.push_back({op, "operands are not statically shaped ranked tensors"});
+      return true;
+    }
+    for (size_t i = 0; i < f.ops.size(); ++i) f.ops[i].shape = f.shapes[i].data();
+    SmallVector<int> res;
+    for (Type t : op->getResultTypes()) res.push_back(dtypeCode(getElementTypeOrSelf(t)));
+    const char *why = nova_forms::check(name, (int)f.ops.size(), f.ops.data(), (int)res.size(),
+                                        res.data(), at);
+    if (why) declinedOps.push_back({op, why});
+    return why != nullptr;
+  }
+
+  // ---- building blocks (called only after every check has passed) --------
+
+  // Dense buffer of a tensor value.
+  Value dense(Location loc, Value tensor) {
     auto tt = cast<RankedTensorType>(tensor.getType());
-    auto mt = MemRefType::get(tt.getShape(), tt.getElementType());
-    Value b = rewriter.create<bufferization::ToBufferOp>(loc, mt, tensor, /*readOnly=*/true);
+    return rewriter.create<bufferization::ToBufferOp>(
+        loc, MemRefType::get(tt.getShape(), tt.getElementType()), tensor, /*readOnly=*/true);
+  }
+
+  // A view of the dense buffer `b` (identity layout) with another static
+  // shape of the same element count, row-major.
+  Value reshaped(Location loc, Value b, ArrayRef<int64_t> shape) {
+    auto mt = cast<MemRefType>(b.getType());
+    SmallVector<int64_t> strides(shape.size(), 1);
+    for (int64_t i = (int64_t)shape.size() - 2; i >= 0; --i) strides[i] = strides[i + 1] * shape[i + 1];
+    auto layout = StridedLayoutAttr::get(rewriter.getContext(), 0, strides);
+    auto t = MemRefType::get(shape, mt.getElementType(), layout);
+    SmallVector<OpFoldResult> sz, st;
+    for (int64_t d : shape) sz.push_back(rewriter.getIndexAttr(d));
+    for (int64_t d : strides) st.push_back(rewriter.getIndexAttr(d));
+    return rewriter.create<memref::ReinterpretCastOp>(loc, t, b, rewriter.getIndexAttr(0), sz, st);
+  }
+
+  Value toAbi(Location loc, Value b) {
+    auto mt = cast<MemRefType>(b.getType());
+    return rewriter.create<memref::CastOp>(loc, abiType(mt.getElementType(), mt.getRank()), b);
+  }
+
+  // A GEMM operand as a rank-3 ABI buffer: leading dims collapsed into one
+  // batch dim (a rank-2 operand is a batch of one), then, if transposed, the
+  // view with the last two dims swapped.
+  Value gemmOperand(Location loc, const GemmOperand &o) {
+    auto tt = cast<RankedTensorType>(o.tensor.getType());
+    auto s = tt.getShape();
     const int64_t r = tt.getRank();
-    if (transposed) {
-      SmallVector<unsigned> perm;
-      for (int64_t i = 0; i < r; ++i) perm.push_back((unsigned)i);
-      std::swap(perm[r - 1], perm[r - 2]);
-      auto map = AffineMap::getPermutationMap(perm, rewriter.getContext());
+    int64_t batch = 1;
+    for (int64_t i = 0; i + 2 < r; ++i) batch *= s[i];
+    Value b = reshaped(loc, dense(loc, o.tensor), {batch, s[r - 2], s[r - 1]});
+    if (o.transposed) {
+      auto map = AffineMap::getPermutationMap(ArrayRef<unsigned>{0, 2, 1}, rewriter.getContext());
       b = rewriter.create<memref::TransposeOp>(loc, b, AffineMapAttr::get(map));
     }
-    int64_t rank = r;
-    if (rank3 && r == 2) b = batchOfOne(loc, b), rank = 3;
-    return rewriter.create<memref::CastOp>(loc, abiType(tt.getElementType(), rank), b);
+    return toAbi(loc, b);
   }
 
-  // [M, N] (any strided layout) -> [1, M, N].
-  Value batchOfOne(Location loc, Value b) {
-    auto mt = cast<MemRefType>(b.getType());
-    SmallVector<ReassociationIndices> re = {{0, 1}, {2}};
-    SmallVector<int64_t> shape = {1, mt.getShape()[0], mt.getShape()[1]};
-    FailureOr<MemRefType> et = memref::ExpandShapeOp::computeExpandedType(mt, shape, re);
-    return rewriter.create<memref::ExpandShapeOp>(loc, *et, b, re);
-  }
-
-  // A fresh result buffer of tensor type `t`; `abi` receives its ABI view.
-  Value allocResult(Location loc, RankedTensorType t, Value &abi) {
-    Value m = rewriter.create<memref::AllocOp>(
-        loc, MemRefType::get(t.getShape(), t.getElementType()));
-    abi = rewriter.create<memref::CastOp>(loc, abiType(t.getElementType(), t.getRank()), m);
-    return m;
+  // A fresh result buffer of tensor type `t`.
+  Value alloc(Location loc, RankedTensorType t) {
+    return rewriter.create<memref::AllocOp>(loc, MemRefType::get(t.getShape(), t.getElementType()));
   }
 
   Value asTensor(Location loc, Value buffer, Type tensorType) {
@@ -185,12 +253,21 @@ class Lowerer {
     return rewriter.create<arith::ConstantOp>(loc, rewriter.getI32IntegerAttr((int32_t)v));
   }
 
-  // The private, C-interface declaration of @name, created on first use.
-  // Null when the module already declares @name with another type (one
-  // module calls each generic entry point with one operand type only).
+  // ---- callees -------------------------------------------------------------
+
+  FunctionType sig(ArrayRef<Type> args) {
+    return rewriter.getFunctionType(args, {rewriter.getI32Type()});
+  }
+
+  // Whether @name can be called with `type`: not yet declared, or declared
+  // with that type (one module declares each entry point once).
+  bool declarable(StringRef name, FunctionType type) {
+    if (auto f = module.lookupSymbol<func::FuncOp>(name)) return f.getFunctionType() == type;
+    return !module.lookupSymbol(name);
+  }
+
   func::FuncOp declare(StringRef name, FunctionType type) {
-    if (auto f = module.lookupSymbol<func::FuncOp>(name))
-      return f.getFunctionType() == type ? f : func::FuncOp();
+    if (auto f = module.lookupSymbol<func::FuncOp>(name)) return f;
     OpBuilder::InsertionGuard guard(rewriter);
     rewriter.setInsertionPointToStart(module.getBody());
     auto f = rewriter.create<func::FuncOp>(module.getLoc(), name, type);
@@ -200,66 +277,121 @@ class Lowerer {
   }
 
   // func.call @name(args) -> i32, then an assertion that it returned 0.
-  LogicalResult call(Location loc, StringRef name, ValueRange args) {
+  void call(Location loc, StringRef name, ValueRange args) {
     SmallVector<Type> types;
     for (Value a : args) types.push_back(a.getType());
-    auto f = declare(name, rewriter.getFunctionType(types, {rewriter.getI32Type()}));
-    if (!f) return failure();
-    auto c = rewriter.create<func::CallOp>(loc, f, args);
+    auto c = rewriter.create<func::CallOp>(loc, declare(name, sig(types)), args);
     Value ok = rewriter.create<arith::CmpIOp>(loc, arith::CmpIPredicate::eq, c.getResult(0),
                                               i32Const(loc, NOVA_HIP_SUCCESS));
     rewriter.create<cf::AssertOp>(loc, ok, ("libnova_hip " + name + " failed").str());
-    return success();
   }
 
-  // Labels as an i32 buffer (non-i32 integer targets widened on the GPU).
-  Value labelsI32(Location loc, Value targets) {
-    auto tt = cast<RankedTensorType>(targets.getType());
+  Type f32() { return rewriter.getF32Type(); }
+  Type i32() { return rewriter.getI32Type(); }
+
+  // Index / label widening: the callee it needs (empty for i32) and its type.
+  std::string widenName(int dt) {
+    return dt == NOVA_HIP_DT_I16 ? "nova_hip_index_to_i32_i16"
+           : dt == NOVA_HIP_DT_I64 ? "nova_hip_index_to_i32_i64" : "";
+  }
+  bool widenDeclarable(Value idx) {
+    Type el = getElementTypeOrSelf(idx.getType());
+    const std::string n = widenName(dtypeCode(el));
+    return n.empty() || declarable(n, sig({abiType(el, 1), abiType(i32(), 1), i32()}));
+  }
+  // Indices as a flat i32 ABI buffer (non-i32 types widened on the GPU).
+  Value indicesI32(Location loc, Value idx) {
+    auto tt = cast<RankedTensorType>(idx.getType());
+    const int64_t n = tt.getNumElements();
+    Value flat = toAbi(loc, reshaped(loc, dense(loc, idx), {n}));
     const int dt = dtypeCode(tt.getElementType());
-    auto flat = [&](Value t) {
-      auto ty = cast<RankedTensorType>(t.getType());
-      Value b = abiBuffer(loc, t);
-      if (ty.getRank() == 1) return b;
-      // [d0, ..., dn] -> [d0 * ... * dn], a view of the dense buffer.
-      SmallVector<ReassociationIndices> all(1);
-      for (int64_t i = 0; i < ty.getRank(); ++i) all[0].push_back(i);
-      Value dense = rewriter.create<bufferization::ToBufferOp>(
-          loc, MemRefType::get(ty.getShape(), ty.getElementType()), t, true);
-      Value c = rewriter.create<memref::CollapseShapeOp>(loc, dense, all);
-      return rewriter.create<memref::CastOp>(loc, abiType(ty.getElementType(), 1), c)
-          .getResult();
-    };
-    if (dt == NOVA_HIP_DT_I32) return flat(targets);
-    if (dt != NOVA_HIP_DT_I16 && dt != NOVA_HIP_DT_I64) return Value();
-    auto wide = RankedTensorType::get({tt.getNumElements()}, rewriter.getI32Type());
-    Value abi;
-    allocResult(loc, wide, abi);
-    if (failed(call(loc, dt == NOVA_HIP_DT_I16 ? "nova_hip_index_to_i32_i16"
-                                                : "nova_hip_index_to_i32_i64",
-                    {flat(targets), abi, i32Const(loc, dt)})))
-      return Value();
-    return abi;
+    if (dt == NOVA_HIP_DT_I32) return flat;
+    Value wide = toAbi(loc, alloc(loc, RankedTensorType::get({n}, i32())));
+    call(loc, widenName(dt), {flat, wide, i32Const(loc, dt)});
+    return wide;
   }
 
-  // nova.linear / nova.matmul (rank 2 or 3) and their epilogue folds.
-  LogicalResult lowerGemm(Operation *op, Value lhs, Value rhs, Value bias) {
+  // Row-major [R, D] view of a tensor's dense buffer (leading dims folded).
+  Value rows2d(Location loc, Value t) {
+    auto tt = cast<RankedTensorType>(t.getType());
+    const int64_t D = tt.getShape().back();
+    return toAbi(loc, reshaped(loc, dense(loc, t), {tt.getNumElements() / D, D}));
+  }
+  Value flat1d(Location loc, Value t) {
+    auto tt = cast<RankedTensorType>(t.getType());
+    return toAbi(loc, reshaped(loc, dense(loc, t), {tt.getNumElements()}));
+  }
+
+  // Replace `result` by the buffer `buf` of the same element count, viewed
+  // with the result's shape.
+  void replaceWith(Location loc, Value result, Value buf) {
+    auto rt = cast<RankedTensorType>(result.getType());
+    auto bt = cast<MemRefType>(buf.getType());
+    Value b = buf;
+    if (bt.getShape() != rt.getShape()) {
+      // dense [..] -> dense [rt shape]: a fresh identity-layout view
+      SmallVector<ReassociationIndices> all(1);
+      for (int64_t i = 0; i < bt.getRank(); ++i) all[0].push_back(i);
+      Value flat = bt.getRank() == 1 ? buf : rewriter.create<memref::CollapseShapeOp>(loc, buf, all);
+      SmallVector<ReassociationIndices> back(1);
+      for (int64_t i = 0; i < rt.getRank(); ++i) back[0].push_back(i);
+      if (rt.getRank() == 0) {
+        b = rewriter.create<memref::CollapseShapeOp>(loc, flat, SmallVector<ReassociationIndices>{});
+      } else {
+        b = rewriter.create<memref::ExpandShapeOp>(
+            loc, MemRefType::get(rt.getShape(), rt.getElementType()), flat, back);
+      }
+    }
+    rewriter.replaceAllUsesWith(result, asTensor(loc, b, rt));
+  }
+
+  // ---- GEMMs -----------------------------------------------------------------
+
+  // Entry-point name suffix of a dtype combination.  A module declares each
+  // function once, with one type, but the generic entry points take operands
+  // of any dtype; nova_hip.h therefore exports one alias per (input,
+  // output[, bias]) dtype combination, which these names select.
+  static std::string typeSuffix(int in, int out, int bias) {
+    static const char *n[] = {"f32", "bf16", "f16"};
+    std::string s = std::string(n[in]) + "_" + n[out];
+    if (bias >= 0) s += std::string("_b") + n[bias];
+    return s;
+  }
+
+  // nova.linear / nova.matmul / linalg.(batch_)matmul and their epilogue folds.
+  LogicalResult lowerGemm(Operation *op, const char *form_name, Value lhs, Value rhs, Value bias,
+                          Value outs) {
     Location loc = op->getLoc();
     Value result = op->getResult(0);
-    auto rt = cast<RankedTensorType>(result.getType());
-    if (!staticRanked(lhs) || !staticRanked(rhs) || !rt.hasStaticShape() || rt.getRank() > 3 ||
-        rt.getRank() < 2)
-      return failure();
+    auto rt = staticTensor(result);
     GemmOperand a = traceOperand(lhs), b = traceOperand(rhs);
-    if (a.stored != b.stored) return failure();
+    GemmOperand bo;
+    if (bias) bo = traceOperand(bias);
+    Form f;
+    f.add(lhs, a.stored);
+    f.add(rhs, b.stored);
+    if (bias) f.add(bias, bo.stored);
+    if (outs) f.add(outs);
+    if (!rt || declined(op, form_name, f)) return failure();
+    if (bias && bo.transposed) return failure();  // a 1-D bias has no transpose
+    // linalg outs must be a zero fill (the product overwrites them).
+    if (outs) {
+      auto fill = outs.getDefiningOp<linalg::FillOp>();
+      if (!fill) return failure();
+      auto c = fill.getInputs()[0].getDefiningOp<arith::ConstantOp>();
+      auto fa = c ? dyn_cast<FloatAttr>(c.getValue()) : FloatAttr();
+      if (!fa || !fa.getValue().isZero()) return failure();
+      if (auto mm = dyn_cast<linalg::MatmulOp>(op))
+        if (mm.getIndexingMapsArray() != linalg::MatmulOp::getDefaultIndexingMaps(op->getContext()))
+          return failure();
+      if (auto bm = dyn_cast<linalg::BatchMatmulOp>(op))
+        if (bm.getIndexingMapsArray() !=
+            linalg::BatchMatmulOp::getDefaultIndexingMaps(op->getContext()))
+          return failure();
+    }
     const int in = dtypeCode(a.stored);
     int out = dtypeCode(rt.getElementType());
-    if (in < 0 || in > NOVA_HIP_DT_F16 || out < 0 || out > NOVA_HIP_DT_F16) return failure();
-    // Narrow result: linalg.matmul with narrow outs accumulates in it; only
-    // the same-dtype form is on this path.
     const bool narrow = out != NOVA_HIP_DT_F32;
-    if (narrow && (in != out || getElementTypeOrSelf(lhs.getType()) != a.stored ||
-                   getElementTypeOrSelf(rhs.getType()) != b.stored))
-      return failure();
     int epi = bias ? NOVA_HIP_EPI_BIAS : NOVA_HIP_EPI_NONE;
     Operation *last = op;
     SmallVector<Operation *> folded;
@@ -283,71 +415,118 @@ class Lowerer {
         }
       }
     }
-    int biasDt = 0;
-    GemmOperand bo;
-    if (bias) {
-      if (!staticRanked(bias)) return failure();
-      bo = traceOperand(bias);
-      biasDt = dtypeCode(bo.stored);
-      if (biasDt < 0 || biasDt > NOVA_HIP_DT_F16 || (narrow && biasDt != in)) return failure();
-    }
-    rewriter.setInsertionPoint(last);
+    const int biasDt = bias ? dtypeCode(bo.stored) : NOVA_HIP_DT_F32;
     auto outTy = cast<RankedTensorType>(last->getResult(0).getType());
-    // Every GEMM goes through the 3-D entry point; a rank-2 operand or
-    // result is a batch of one.
-    Value A = abiBuffer(loc, a.tensor, a.transposed, /*rank3=*/true);
-    Value B = abiBuffer(loc, b.tensor, b.transposed, /*rank3=*/true);
-    Value cBuf = rewriter.create<memref::AllocOp>(
-        loc, MemRefType::get(outTy.getShape(), outTy.getElementType()));
-    Value C = cBuf;
-    if (outTy.getRank() == 2) C = batchOfOne(loc, C);
-    C = rewriter.create<memref::CastOp>(loc, abiType(outTy.getElementType(), 3), C);
-    Value biasAbi;
-    if (bias) {
-      biasAbi = abiBuffer(loc, bo.tensor);
-    } else {
-      // The entry point takes a bias descriptor always; an empty one when
-      // the epilogue has none.
-      Value z;
-      allocResult(loc, RankedTensorType::get({0}, rewriter.getF32Type()), z);
-      biasAbi = z;
-    }
-    int32_t flags = NOVA_HIP_GEMM_FLAGS(in, out, epi, biasDt);
+    const std::string name = "nova_hip_gemm_" + typeSuffix(in, out, biasDt);
+    FunctionType ft = sig({abiType(a.stored, 3), abiType(b.stored, 3),
+                           abiType(outTy.getElementType(), 3),
+                           abiType(bias ? bo.stored : f32(), 1), i32()});
+    if (!declarable(name, ft)) return failure();
+
+    // Every check has passed: build.
+    rewriter.setInsertionPoint(last);
+    Value A = gemmOperand(loc, a), B = gemmOperand(loc, b);
+    Value cBuf = alloc(loc, outTy);
+    auto cs = outTy.getShape();
+    const int64_t r = outTy.getRank();
+    int64_t batch = 1;
+    for (int64_t i = 0; i + 2 < r; ++i) batch *= cs[i];
+    Value C = toAbi(loc, reshaped(loc, cBuf, {batch, cs[r - 2], cs[r - 1]}));
+    // The entry point takes a bias descriptor always; an empty one when the
+    // epilogue has none.
+    Value biasAbi = bias ? flat1d(loc, bo.tensor)
+                         : toAbi(loc, alloc(loc, RankedTensorType::get({0}, f32())));
+    int32_t flags = NOVA_HIP_GEMM_FLAGS(in, out, epi, bias ? biasDt : 0);
     if (narrow) flags |= NOVA_HIP_GEMM_ACC_OUT;
     if (in == NOVA_HIP_DT_F32 && f32Mfma) flags |= NOVA_HIP_GEMM_F32_MFMA;
-    const std::string name = "nova_hip_gemm_" + typeSuffix(in, out, bias ? biasDt : NOVA_HIP_DT_F32);
-    if (failed(call(loc, name, {A, B, C, biasAbi, i32Const(loc, flags)}))) return failure();
+    call(loc, name, {A, B, C, biasAbi, i32Const(loc, flags)});
     rewriter.replaceAllUsesWith(last->getResult(0), asTensor(loc, cBuf, outTy));
-    for (auto it = folded.rbegin(); it != folded.rend(); ++it) rewriter.eraseOp(*it);
+    for (auto it = folded.rbegin(); it != folded.rend(); ++it) {
+      erasedOps.insert(*it);
+      rewriter.eraseOp(*it);
+    }
     rewriter.eraseOp(op);
     return success();
   }
+
+  // nova.linear_backward / nova.matmul_backward: GEMMs over views, leading
+  // dims of grad_out and input folded into rows.
+  template <typename OpTy>
+  LogicalResult lowerGemmBackward(OpTy op, const char *form_name, Value go, Value x, Value w,
+                                  bool linear) {
+    Location loc = op.getLoc();
+    GemmOperand g = traceOperand(go), xi = traceOperand(x), wi = traceOperand(w);
+    Form f;
+    f.add(go, g.stored);
+    f.add(x, xi.stored);
+    f.add(w, wi.stored);
+    if (declined(op, form_name, f)) return failure();
+    if (g.transposed || xi.transposed || wi.transposed) return failure();
+    const int in = dtypeCode(xi.stored);
+    const int out = NOVA_HIP_DT_F32;  // the table admits f32 results only
+    const std::string name =
+        std::string(linear ? "nova_hip_linear_backward_" : "nova_hip_matmul_backward_") +
+        typeSuffix(in, out, -1);
+    SmallVector<Type> argTypes = {abiType(xi.stored, 2), abiType(xi.stored, 2),
+                                  abiType(xi.stored, 2), abiType(f32(), 2), abiType(f32(), 2)};
+    if (linear) argTypes.push_back(abiType(f32(), 1));
+    argTypes.push_back(i32());
+    if (!declarable(name, sig(argTypes))) return failure();
+
+    rewriter.setInsertionPoint(op);
+    SmallVector<Value> bufs, outs;
+    for (Value r : op->getResults()) {
+      Value buf = alloc(loc, cast<RankedTensorType>(r.getType()));
+      bufs.push_back(buf);
+      outs.push_back(toAbi(loc, buf));
+    }
+    // grad_input [..., M, K] is written as [rows, K]: its buffer viewed 2-D.
+    {
+      auto t = cast<RankedTensorType>(op->getResult(0).getType());
+      const int64_t K = t.getShape().back();
+      outs[0] = toAbi(loc, reshaped(loc, bufs[0], {t.getNumElements() / K, K}));
+    }
+    int32_t flags = NOVA_HIP_GEMM_FLAGS(in, out, NOVA_HIP_EPI_NONE, 0);
+    if (in == NOVA_HIP_DT_F32 && f32Mfma) flags |= NOVA_HIP_GEMM_F32_MFMA;
+    SmallVector<Value> args = {rows2d(loc, g.tensor), rows2d(loc, xi.tensor),
+                               toAbi(loc, dense(loc, wi.tensor))};
+    args.append(outs.begin(), outs.end());
+    args.push_back(i32Const(loc, flags));
+    call(loc, name, args);
+    for (auto [r, b] : llvm::zip(op->getResults(), bufs))
+      rewriter.replaceAllUsesWith(r, asTensor(loc, b, r.getType()));
+    rewriter.eraseOp(op);
+    return success();
+  }
+
+  // ---- row reductions ---------------------------------------------------------
 
   // nova.layer_norm -> (y, mean_sum, rstd); eps is the op's 1e-5
   // (NovaToLinalgGeneric.cpp:2025).
   LogicalResult lowerLayerNorm(LayerNormOp op) {
     Location loc = op.getLoc();
-    auto xt = dyn_cast<RankedTensorType>(op.getInput().getType());
-    if (!xt || !xt.hasStaticShape() || xt.getRank() < 2 || !xt.getElementType().isF32())
+    Form f;
+    f.add(op.getInput());
+    f.add(op.getGamma());
+    f.add(op.getBeta());
+    if (declined(op, "nova.layer_norm", f)) return failure();
+    const std::string name = "nova_hip_layer_norm_f32";
+    if (!declarable(name, sig({abiType(f32(), 2), abiType(f32(), 1), abiType(f32(), 1),
+                               abiType(f32(), 2), abiType(f32(), 1), abiType(f32(), 1), f32()})))
       return failure();
-    rewriter.setInsertionPoint(op);
+    auto xt = cast<RankedTensorType>(op.getInput().getType());
     const int64_t D = xt.getShape().back(), R = xt.getNumElements() / D;
-    // Rows flattened: [..., D] -> [R, D]; the stats [R].
-    Value x = flat2d(loc, op.getInput(), R, D);
-    Value yAbi, sAbi, rAbi;
-    auto y2 = RankedTensorType::get({R, D}, rewriter.getF32Type());
-    auto r1 = RankedTensorType::get({R}, rewriter.getF32Type());
-    Value yBuf = allocResult(loc, y2, yAbi);
-    Value sBuf = allocResult(loc, r1, sAbi);
-    Value rBuf = allocResult(loc, r1, rAbi);
+    rewriter.setInsertionPoint(op);
+    Value yBuf = alloc(loc, RankedTensorType::get({R, D}, f32()));
+    Value sBuf = alloc(loc, RankedTensorType::get({R}, f32()));
+    Value rBuf = alloc(loc, RankedTensorType::get({R}, f32()));
     Value eps = rewriter.create<arith::ConstantOp>(loc, rewriter.getF32FloatAttr(1.0e-5f));
-    if (failed(call(loc, "nova_hip_layer_norm_f32",
-                    {x, abiBuffer(loc, op.getGamma()), abiBuffer(loc, op.getBeta()), yAbi, sAbi,
-                     rAbi, eps})))
-      return failure();
-    replaceReshaped(loc, op.getOutput(), yBuf);
-    replaceReshaped(loc, op.getMeanSum(), sBuf);
-    replaceReshaped(loc, op.getVarSum(), rBuf);
+    call(loc, name,
+         {rows2d(loc, op.getInput()), flat1d(loc, op.getGamma()), flat1d(loc, op.getBeta()),
+          toAbi(loc, yBuf), toAbi(loc, sBuf), toAbi(loc, rBuf), eps});
+    replaceWith(loc, op.getOutput(), yBuf);
+    replaceWith(loc, op.getMeanSum(), sBuf);
+    replaceWith(loc, op.getVarSum(), rBuf);
     rewriter.eraseOp(op);
     return success();
   }
@@ -355,42 +534,45 @@ class Lowerer {
   // nova.sce (+ the nova.sce_backward of its softmax, fused).
   LogicalResult lowerSce(SceOp op) {
     Location loc = op.getLoc();
-    auto lt = dyn_cast<RankedTensorType>(op.getLogits().getType());
-    if (!lt || !lt.hasStaticShape() || !lt.getElementType().isF32() || !staticRanked(op.getTargets()))
-      return failure();
-    const int64_t C = lt.getShape().back(), R = lt.getNumElements() / C;
+    Form f;
+    f.add(op.getLogits());
+    f.add(op.getTargets());
+    if (declined(op, "nova.sce", f)) return failure();
+    auto lt = cast<RankedTensorType>(op.getLogits().getType());
     SceBackwardOp bw;
     if (Value u = singleUse(op.getSoftmax()))
       if (auto b = dyn_cast<SceBackwardOp>(*u.getUsers().begin()))
         if (b.getTargets() == op.getTargets() &&
             (b.getDim() == -1 || b.getDim() == lt.getRank() - 1))
           bw = b;
+    const bool smDead = op.getSoftmax().use_empty();
+    const std::string name = bw ? "nova_hip_sce_fwd_bwd_f32"
+                             : smDead ? "nova_hip_sce_loss_f32" : "nova_hip_sce_f32";
+    SmallVector<Type> argTypes = {abiType(f32(), 2), abiType(i32(), 1), abiType(f32(), 1)};
+    if (!smDead || bw) argTypes.push_back(abiType(f32(), 2));
+    if (!declarable(name, sig(argTypes)) || !widenDeclarable(op.getTargets())) return failure();
+
+    const int64_t C = lt.getShape().back(), R = lt.getNumElements() / C;
     rewriter.setInsertionPoint(bw ? bw.getOperation() : op.getOperation());
-    Value x = flat2d(loc, op.getLogits(), R, C);
-    Value t = labelsI32(loc, op.getTargets());
-    if (!t) return failure();
-    Value lossAbi;
-    Value lossBuf = allocResult(loc, RankedTensorType::get({1}, rewriter.getF32Type()), lossAbi);
-    auto full = RankedTensorType::get({R, C}, rewriter.getF32Type());
+    Value x = rows2d(loc, op.getLogits());
+    Value t = indicesI32(loc, op.getTargets());
+    Value lossBuf = alloc(loc, RankedTensorType::get({1}, f32()));
+    auto full = RankedTensorType::get({R, C}, f32());
     if (bw) {
-      Value gAbi;
-      Value gBuf = allocResult(loc, full, gAbi);
-      if (failed(call(loc, "nova_hip_sce_fwd_bwd_f32", {x, t, lossAbi, gAbi}))) return failure();
-      replaceReshaped(loc, bw.getGradLogits(), gBuf);
+      Value gBuf = alloc(loc, full);
+      call(loc, name, {x, t, toAbi(loc, lossBuf), toAbi(loc, gBuf)});
+      replaceWith(loc, bw.getGradLogits(), gBuf);
       erasedOps.insert(bw);
       rewriter.eraseOp(bw);
+    } else if (smDead) {
+      // The op is Pure and its softmax dead: the loss alone.
+      call(loc, name, {x, t, toAbi(loc, lossBuf)});
     } else {
-      if (op.getSoftmax().use_empty()) {
-        // The op is Pure and its softmax dead: the loss alone.
-        if (failed(call(loc, "nova_hip_sce_loss_f32", {x, t, lossAbi}))) return failure();
-      } else {
-        Value smAbi;
-        Value smBuf = allocResult(loc, full, smAbi);
-        if (failed(call(loc, "nova_hip_sce_f32", {x, t, lossAbi, smAbi}))) return failure();
-        replaceReshaped(loc, op.getSoftmax(), smBuf);
-      }
+      Value smBuf = alloc(loc, full);
+      call(loc, name, {x, t, toAbi(loc, lossBuf), toAbi(loc, smBuf)});
+      replaceWith(loc, op.getSoftmax(), smBuf);
     }
-    replaceReshaped(loc, op.getResult(), lossBuf);
+    replaceWith(loc, op.getResult(), lossBuf);
     rewriter.eraseOp(op);
     return success();
   }
@@ -398,19 +580,27 @@ class Lowerer {
   // nova.sce_backward on its own.
   LogicalResult lowerSceBackward(SceBackwardOp op) {
     Location loc = op.getLoc();
-    auto st = dyn_cast<RankedTensorType>(op.getSoftmax().getType());
-    if (!st || !st.hasStaticShape() || !st.getElementType().isF32() ||
-        (op.getDim() != -1 && op.getDim() != st.getRank() - 1))
+    Form f;
+    f.add(op.getSoftmax());
+    f.add(op.getTargets());
+    nova_forms::Attrs at;
+    if (auto st = staticTensor(op.getSoftmax())) {
+      int64_t d = op.getDim();
+      if (d < 0) d += st.getRank();
+      at.dim = d == st.getRank() - 1 ? -1 : (int)d;
+    }
+    if (declined(op, "nova.sce_backward", f, at)) return failure();
+    const std::string name = "nova_hip_sce_backward_f32";
+    if (!declarable(name, sig({abiType(f32(), 2), abiType(i32(), 1), abiType(f32(), 2)})) ||
+        !widenDeclarable(op.getTargets()))
       return failure();
-    rewriter.setInsertionPoint(op);
+    auto st = cast<RankedTensorType>(op.getSoftmax().getType());
     const int64_t C = st.getShape().back(), R = st.getNumElements() / C;
-    Value t = labelsI32(loc, op.getTargets());
-    if (!t) return failure();
-    Value gAbi;
-    Value gBuf = allocResult(loc, RankedTensorType::get({R, C}, rewriter.getF32Type()), gAbi);
-    if (failed(call(loc, "nova_hip_sce_backward_f32", {flat2d(loc, op.getSoftmax(), R, C), t, gAbi})))
-      return failure();
-    replaceReshaped(loc, op.getGradLogits(), gBuf);
+    rewriter.setInsertionPoint(op);
+    Value t = indicesI32(loc, op.getTargets());
+    Value gBuf = alloc(loc, RankedTensorType::get({R, C}, f32()));
+    call(loc, name, {rows2d(loc, op.getSoftmax()), t, toAbi(loc, gBuf)});
+    replaceWith(loc, op.getGradLogits(), gBuf);
     rewriter.eraseOp(op);
     return success();
   }
@@ -418,57 +608,204 @@ class Lowerer {
   // nova.layer_norm_backward with the forward's saved stats.
   LogicalResult lowerLayerNormBackward(LayerNormBackwardOp op) {
     Location loc = op.getLoc();
-    auto xt = dyn_cast<RankedTensorType>(op.getX().getType());
-    if (!xt || !xt.hasStaticShape() || !xt.getElementType().isF32()) return failure();
-    rewriter.setInsertionPoint(op);
-    const int64_t D = xt.getShape().back(), R = xt.getNumElements() / D;
-    auto d1 = RankedTensorType::get({D}, rewriter.getF32Type());
-    Value dxAbi, dgAbi, dbAbi;
-    Value dxBuf = allocResult(loc, RankedTensorType::get({R, D}, rewriter.getF32Type()), dxAbi);
-    Value dgBuf = allocResult(loc, d1, dgAbi);
-    Value dbBuf = allocResult(loc, d1, dbAbi);
-    if (failed(call(loc, "nova_hip_layer_norm_backward_f32",
-                    {flat2d(loc, op.getGradY(), R, D), flat2d(loc, op.getX(), R, D),
-                     abiBuffer(loc, op.getGamma()), flat1d(loc, op.getMeanSum(), R),
-                     flat1d(loc, op.getVarSum(), R), dxAbi, dgAbi, dbAbi})))
+    Form f;
+    for (Value v : {op.getGradY(), op.getX(), op.getGamma(), op.getMeanSum(), op.getVarSum()})
+      f.add(v);
+    if (declined(op, "nova.layer_norm_backward", f)) return failure();
+    const std::string name = "nova_hip_layer_norm_backward_f32";
+    if (!declarable(name, sig({abiType(f32(), 2), abiType(f32(), 2), abiType(f32(), 1),
+                               abiType(f32(), 1), abiType(f32(), 1), abiType(f32(), 2),
+                               abiType(f32(), 1), abiType(f32(), 1)})))
       return failure();
-    replaceReshaped(loc, op.getGradX(), dxBuf);
-    replaceReshaped(loc, op.getGradGamma(), dgBuf);
-    replaceReshaped(loc, op.getGradBeta(), dbBuf);
+    auto xt = cast<RankedTensorType>(op.getX().getType());
+    const int64_t D = xt.getShape().back(), R = xt.getNumElements() / D;
+    rewriter.setInsertionPoint(op);
+    Value dxBuf = alloc(loc, RankedTensorType::get({R, D}, f32()));
+    Value dgBuf = alloc(loc, RankedTensorType::get({D}, f32()));
+    Value dbBuf = alloc(loc, RankedTensorType::get({D}, f32()));
+    call(loc, name,
+         {rows2d(loc, op.getGradY()), rows2d(loc, op.getX()), flat1d(loc, op.getGamma()),
+          flat1d(loc, op.getMeanSum()), flat1d(loc, op.getVarSum()), toAbi(loc, dxBuf),
+          toAbi(loc, dgBuf), toAbi(loc, dbBuf)});
+    replaceWith(loc, op.getGradX(), dxBuf);
+    replaceWith(loc, op.getGradGamma(), dgBuf);
+    replaceWith(loc, op.getGradBeta(), dbBuf);
     rewriter.eraseOp(op);
     return success();
   }
 
-  // nova.linear_backward / nova.matmul_backward (rank 2): GEMMs over views.
-  template <typename OpTy>
-  LogicalResult lowerGemmBackward(OpTy op, Value go, Value x, Value w, bool linear) {
+  // ---- program glue -------------------------------------------------------------
+
+  // nova.add / sub / mul / div: operands and result as 4-D views (leading
+  // unit dims), size-1 dims broadcast by the entry point.
+  LogicalResult lowerBinary(Operation *op, const char *form_name, int code) {
+    Location loc = op->getLoc();
+    Value a = op->getOperand(0), b = op->getOperand(1), r = op->getResult(0);
+    Form f;
+    f.add(a);
+    f.add(b);
+    auto rt = staticTensor(r);
+    if (!rt || declined(op, form_name, f)) return failure();
+    const std::string name = "nova_hip_binary_f32";
+    if (!declarable(name, sig({abiType(f32(), 4), abiType(f32(), 4), abiType(f32(), 4), i32()})))
+      return failure();
+    auto four = [&](Value buf, ArrayRef<int64_t> s) {
+      SmallVector<int64_t> s4(4 - s.size(), 1);
+      s4.append(s.begin(), s.end());
+      return toAbi(loc, reshaped(loc, buf, s4));
+    };
+    rewriter.setInsertionPoint(op);
+    Value cBuf = alloc(loc, rt);
+    call(loc, name,
+         {four(dense(loc, a), cast<RankedTensorType>(a.getType()).getShape()),
+          four(dense(loc, b), cast<RankedTensorType>(b.getType()).getShape()),
+          four(cBuf, rt.getShape()), i32Const(loc, code)});
+    rewriter.replaceAllUsesWith(r, asTensor(loc, cBuf, rt));
+    rewriter.eraseOp(op);
+    return success();
+  }
+
+  // nova.gelu that did not fold into a GEMM epilogue, and nova.gelu_backward:
+  // flat [n] streams.
+  LogicalResult lowerGelu(Operation *op, bool backward) {
+    Location loc = op->getLoc();
+    Form f;
+    for (Value v : op->getOperands()) f.add(v);
+    auto rt = staticTensor(op->getResult(0));
+    if (!rt || declined(op, backward ? "nova.gelu_backward" : "nova.gelu", f)) return failure();
+    const std::string name = backward ? "nova_hip_gelu_backward_f32" : "nova_hip_gelu_f32";
+    SmallVector<Type> argTypes(backward ? 3 : 2, abiType(f32(), 1));
+    if (!declarable(name, sig(argTypes))) return failure();
+    rewriter.setInsertionPoint(op);
+    Value outBuf = alloc(loc, rt);
+    SmallVector<Value> args;
+    for (Value v : op->getOperands()) args.push_back(flat1d(loc, v));
+    args.push_back(toAbi(loc, reshaped(loc, outBuf, {rt.getNumElements()})));
+    call(loc, name, args);
+    rewriter.replaceAllUsesWith(op->getResult(0), asTensor(loc, outBuf, rt));
+    rewriter.eraseOp(op);
+    return success();
+  }
+
+  // A splat f32 nova.constant: a fill.
+  LogicalResult lowerConstant(ConstantOp op) {
     Location loc = op.getLoc();
-    for (Value v : {go, x, w})
-      if (!staticRanked(v) || cast<RankedTensorType>(v.getType()).getRank() != 2) return failure();
-    const Type el = getElementTypeOrSelf(x.getType());
-    const int in = dtypeCode(el);
-    if (in < 0 || in > NOVA_HIP_DT_F16 || getElementTypeOrSelf(go.getType()) != el ||
-        getElementTypeOrSelf(w.getType()) != el)
+    auto rt = staticTensor(op.getResult());
+    auto attr = dyn_cast<DenseElementsAttr>(op.getValue());
+    nova_forms::Attrs at;
+    at.splat_f32 = rt && attr && attr.isSplat() && rt.getElementType().isF32();
+    Form f;
+    if (declined(op, "nova.constant", f, at)) return failure();
+    const std::string name = "nova_hip_fill_f32";
+    if (!declarable(name, sig({abiType(f32(), 1), f32()}))) return failure();
+    rewriter.setInsertionPoint(op);
+    Value buf = alloc(loc, rt);
+    Value v = rewriter.create<arith::ConstantOp>(loc, attr.getSplatValue<FloatAttr>());
+    call(loc, name, {toAbi(loc, reshaped(loc, buf, {rt.getNumElements()})), v});
+    rewriter.replaceAllUsesWith(op.getResult(), asTensor(loc, buf, rt));
+    rewriter.eraseOp(op);
+    return success();
+  }
+
+  // nova.gather along axis 0 (the embedding lookup): table [V, D], indices
+  // flattened and widened to i32, out [n, D] viewed as the result shape.
+  LogicalResult lowerGather(GatherOp op) {
+    Location loc = op.getLoc();
+    Form f;
+    f.add(op.getInput());
+    f.add(op.getIndices());
+    nova_forms::Attrs at;
+    at.axis = (int)op.getAxis();
+    if (auto t = staticTensor(op.getInput()))
+      if (at.axis < 0) at.axis += (int)t.getRank();
+    auto rt = staticTensor(op.getResult());
+    if (!rt || declined(op, "nova.gather", f, at)) return failure();
+    const std::string name = "nova_hip_gather_f32";
+    if (!declarable(name, sig({abiType(f32(), 2), abiType(i32(), 1), abiType(f32(), 2), i32()})) ||
+        !widenDeclarable(op.getIndices()))
       return failure();
     rewriter.setInsertionPoint(op);
-    SmallVector<Value> outs, bufs;
-    for (Value r : op->getResults()) {
-      Value abi;
-      bufs.push_back(allocResult(loc, cast<RankedTensorType>(r.getType()), abi));
-      outs.push_back(abi);
+    auto tt = cast<RankedTensorType>(op.getInput().getType());
+    const int64_t D = tt.getShape()[1];
+    Value idx = indicesI32(loc, op.getIndices());
+    Value outBuf = alloc(loc, rt);
+    call(loc, name,
+         {toAbi(loc, dense(loc, op.getInput())), idx,
+          toAbi(loc, reshaped(loc, outBuf, {rt.getNumElements() / D, D})),
+          i32Const(loc, NOVA_HIP_DT_I32)});
+    rewriter.replaceAllUsesWith(op.getResult(), asTensor(loc, outBuf, rt));
+    rewriter.eraseOp(op);
+    return success();
+  }
+
+  // nova.scatter_add along axis 0: the input copied into a fresh buffer, then
+  // the adds into it.
+  LogicalResult lowerScatterAdd(ScatterAddOp op) {
+    Location loc = op.getLoc();
+    Form f;
+    f.add(op.getInput());
+    f.add(op.getIndices());
+    f.add(op.getSrc());
+    nova_forms::Attrs at;
+    at.axis = (int)op.getAxis();
+    if (auto t = staticTensor(op.getInput()))
+      if (at.axis < 0) at.axis += (int)t.getRank();
+    auto rt = staticTensor(op.getResult());
+    if (!rt || declined(op, "nova.scatter_add", f, at)) return failure();
+    const std::string name = "nova_hip_scatter_add_f32";
+    if (!declarable(name, sig({abiType(f32(), 2), abiType(i32(), 1), abiType(f32(), 2), i32()})) ||
+        !widenDeclarable(op.getIndices()))
+      return failure();
+    rewriter.setInsertionPoint(op);
+    const int64_t D = rt.getShape()[1];
+    Value outBuf = alloc(loc, rt);
+    rewriter.create<memref::CopyOp>(loc, dense(loc, op.getInput()), outBuf);
+    Value idx = indicesI32(loc, op.getIndices());
+    auto srcT = cast<RankedTensorType>(op.getSrc().getType());
+    call(loc, name,
+         {toAbi(loc, outBuf), idx,
+          toAbi(loc, reshaped(loc, dense(loc, op.getSrc()), {srcT.getNumElements() / D, D})),
+          i32Const(loc, NOVA_HIP_DT_I32)});
+    rewriter.replaceAllUsesWith(op.getResult(), asTensor(loc, outBuf, rt));
+    rewriter.eraseOp(op);
+    return success();
+  }
+
+  // nova.reduce<sum> over adjacent dims: x viewed as [outer, n, inner].
+  LogicalResult lowerReduceSum(ReduceOp op) {
+    Location loc = op.getLoc();
+    auto xt = staticTensor(op.getInput());
+    auto rt = staticTensor(op.getResult());
+    Form f;
+    f.add(op.getInput());
+    nova_forms::Attrs at;
+    at.ignore_nan = op.getIgnoreNan();
+    SmallVector<int64_t> dims;
+    if (xt) {
+      if (auto d = op.getDimension())
+        for (Attribute a : *d) {
+          int64_t v = cast<IntegerAttr>(a).getInt();
+          dims.push_back(v < 0 ? v + xt.getRank() : v);
+        }
+      else
+        for (int64_t i = 0; i < xt.getRank(); ++i) dims.push_back(i);
+      llvm::sort(dims);
+      for (size_t i = 1; i < dims.size(); ++i) at.adjacent = at.adjacent && dims[i] == dims[i - 1] + 1;
     }
-    const int out = dtypeCode(getElementTypeOrSelf(op->getResult(0).getType()));
-    int32_t flags = NOVA_HIP_GEMM_FLAGS(in, out, NOVA_HIP_EPI_NONE, 0);
-    if (in == NOVA_HIP_DT_F32 && f32Mfma) flags |= NOVA_HIP_GEMM_F32_MFMA;
-    SmallVector<Value> args = {abiBuffer(loc, go), abiBuffer(loc, x), abiBuffer(loc, w)};
-    args.append(outs.begin(), outs.end());
-    args.push_back(i32Const(loc, flags));
-    const std::string name =
-        std::string(linear ? "nova_hip_linear_backward_" : "nova_hip_matmul_backward_") +
-        typeSuffix(in, out, -1);
-    if (failed(call(loc, name, args))) return failure();
-    for (auto [r, b] : llvm::zip(op->getResults(), bufs))
-      rewriter.replaceAllUsesWith(r, asTensor(loc, b, r.getType()));
+    const bool sum = op.getKind() == ReductionKind::SUM;
+    if (!rt || !sum || dims.empty() || declined(op, "nova.reduce<sum>", f, at)) return failure();
+    const std::string name = "nova_hip_reduce_sum_f32";
+    if (!declarable(name, sig({abiType(f32(), 3), abiType(f32(), 2)}))) return failure();
+    auto s = xt.getShape();
+    int64_t outer = 1, n = 1, inner = 1;
+    for (int64_t i = 0; i < xt.getRank(); ++i)
+      (i < dims.front() ? outer : i <= dims.back() ? n : inner) *= s[i];
+    rewriter.setInsertionPoint(op);
+    Value outBuf = alloc(loc, rt);
+    call(loc, name,
+         {toAbi(loc, reshaped(loc, dense(loc, op.getInput()), {outer, n, inner})),
+          toAbi(loc, reshaped(loc, outBuf, {outer, inner}))});
+    rewriter.replaceAllUsesWith(op.getResult(), asTensor(loc, outBuf, rt));
     rewriter.eraseOp(op);
     return success();
   }
@@ -477,88 +814,70 @@ class Lowerer {
     SmallVector<Operation *> work;
     module.walk([&](Operation *op) {
       if (isa<LinearOp, MatmulOp, LayerNormOp, SceOp, SceBackwardOp, LayerNormBackwardOp,
-              LinearBackwardOp, MatmulBackwardOp>(op))
+              LinearBackwardOp, MatmulBackwardOp, linalg::MatmulOp, linalg::BatchMatmulOp,
+              AddOp, SubOp, MulOp, DivOp, GeluOp, GeluBackwardOp, ConstantOp, GatherOp,
+              ScatterAddOp, ReduceOp>(op))
         work.push_back(op);
     });
     for (Operation *op : work) {
-      // (a sce_backward fused into its nova.sce is gone)
+      // (a sce_backward fused into its nova.sce is gone, and so is a gelu
+      // folded into its GEMM's epilogue)
       if (erasedOps.contains(op)) continue;
       (void)llvm::TypeSwitch<Operation *, LogicalResult>(op)
-          .Case([&](LinearOp o) { return lowerGemm(o, o.getInput(), o.getWeight(), o.getBias()); })
-          .Case([&](MatmulOp o) { return lowerGemm(o, o.getLhs(), o.getRhs(), Value()); })
+          .Case([&](LinearOp o) {
+            return lowerGemm(o, "nova.linear", o.getInput(), o.getWeight(), o.getBias(), Value());
+          })
+          .Case([&](MatmulOp o) {
+            return lowerGemm(o, "nova.matmul", o.getLhs(), o.getRhs(), Value(), Value());
+          })
+          .Case([&](linalg::MatmulOp o) {
+            return lowerGemm(o, "linalg.matmul", o.getDpsInputs()[0], o.getDpsInputs()[1], Value(),
+                             o.getDpsInits()[0]);
+          })
+          .Case([&](linalg::BatchMatmulOp o) {
+            return lowerGemm(o, "linalg.batch_matmul", o.getDpsInputs()[0], o.getDpsInputs()[1],
+                             Value(), o.getDpsInits()[0]);
+          })
           .Case([&](LayerNormOp o) { return lowerLayerNorm(o); })
           .Case([&](SceOp o) { return lowerSce(o); })
           .Case([&](SceBackwardOp o) { return lowerSceBackward(o); })
           .Case([&](LayerNormBackwardOp o) { return lowerLayerNormBackward(o); })
           .Case([&](LinearBackwardOp o) {
-            return lowerGemmBackward(o, o.getGradOut(), o.getInput(), o.getWeight(), true);
+            return lowerGemmBackward(o, "nova.linear_backward", o.getGradOut(), o.getInput(),
+                                     o.getWeight(), true);
           })
           .Case([&](MatmulBackwardOp o) {
-            return lowerGemmBackward(o, o.getGradOut(), o.getA(), o.getB(), false);
+            return lowerGemmBackward(o, "nova.matmul_backward", o.getGradOut(), o.getA(), o.getB(),
+                                     false);
           })
+          .Case([&](AddOp o) { return lowerBinary(o, "nova.add", NOVA_HIP_BIN_ADD); })
+          .Case([&](SubOp o) { return lowerBinary(o, "nova.sub", NOVA_HIP_BIN_SUB); })
+          .Case([&](MulOp o) { return lowerBinary(o, "nova.mul", NOVA_HIP_BIN_MUL); })
+          .Case([&](DivOp o) { return lowerBinary(o, "nova.div", NOVA_HIP_BIN_DIV); })
+          .Case([&](GeluOp o) { return lowerGelu(o, false); })
+          .Case([&](GeluBackwardOp o) { return lowerGelu(o, true); })
+          .Case([&](ConstantOp o) { return lowerConstant(o); })
+          .Case([&](GatherOp o) { return lowerGather(o); })
+          .Case([&](ScatterAddOp o) { return lowerScatterAdd(o); })
+          .Case([&](ReduceOp o) { return lowerReduceSum(o); })
           .Default([](Operation *) { return failure(); });
     }
   }
 
+  // Nova ops still in the module that would become kernels on the existing
+  // (NVPTX) path: every remaining op of the dialect with uses, except
+  // nova.reshape (a tensor view).
+  SmallVector<Operation *> leftovers() {
+    SmallVector<Operation *> left;
+    module.walk([&](Operation *op) {
+      if (op->getDialect() && op->getDialect()->getNamespace() == "nova" &&
+          !isa<ReshapeOp>(op) && !op->use_empty())
+        left.push_back(op);
+    });
+    return left;
+  }
+
  private:
-  // Entry-point name suffix of a dtype combination.  A module declares each
-  // function once, with one type, but the generic entry points take
-  // operands of any dtype; nova_hip.h therefore exports one alias per
-  // (input, output[, bias]) dtype combination, which these names select.
-  static std::string typeSuffix(int in, int out, int bias) {
-    static const char *n[] = {"f32", "bf16", "f16"};
-    std::string s = std::string(n[in]) + "_" + n[out];
-    if (bias >= 0) s += std::string("_b") + n[bias];
-    return s;
-  }
-
-  Value flat2d(Location loc, Value t, int64_t R, int64_t D) {
-    auto ty = cast<RankedTensorType>(t.getType());
-    if (ty.getRank() == 2) return abiBuffer(loc, t);
-    SmallVector<ReassociationIndices> re(2);
-    for (int64_t i = 0; i + 1 < ty.getRank(); ++i) re[0].push_back(i);
-    re[1].push_back(ty.getRank() - 1);
-    Value dense = rewriter.create<bufferization::ToBufferOp>(
-        loc, MemRefType::get(ty.getShape(), ty.getElementType()), t, true);
-    Value c = rewriter.create<memref::CollapseShapeOp>(loc, dense, re);
-    (void)R;
-    (void)D;
-    return rewriter.create<memref::CastOp>(loc, abiType(ty.getElementType(), 2), c);
-  }
-
-  Value flat1d(Location loc, Value t, int64_t R) {
-    auto ty = cast<RankedTensorType>(t.getType());
-    if (ty.getRank() == 1) return abiBuffer(loc, t);
-    SmallVector<ReassociationIndices> all(1);
-    for (int64_t i = 0; i < ty.getRank(); ++i) all[0].push_back(i);
-    Value dense = rewriter.create<bufferization::ToBufferOp>(
-        loc, MemRefType::get(ty.getShape(), ty.getElementType()), t, true);
-    Value c = rewriter.create<memref::CollapseShapeOp>(loc, dense, all);
-    (void)R;
-    return rewriter.create<memref::CastOp>(loc, abiType(ty.getElementType(), 1), c);
-  }
-
-  // Replace `result` by the flat buffer `buf` reshaped back to its type.
-  void replaceReshaped(Location loc, Value result, Value buf) {
-    auto rt = cast<RankedTensorType>(result.getType());
-    auto bt = cast<MemRefType>(buf.getType());
-    Value b = buf;
-    if (bt.getShape() != rt.getShape()) {
-      SmallVector<ReassociationIndices> re;
-      if (bt.getRank() == 1) {
-        re.emplace_back();
-        for (int64_t i = 0; i < rt.getRank(); ++i) re[0].push_back(i);
-      } else {  // [R, D] -> [..., D]
-        re.resize(2);
-        for (int64_t i = 0; i + 1 < rt.getRank(); ++i) re[0].push_back(i);
-        re[1].push_back(rt.getRank() - 1);
-      }
-      b = rewriter.create<memref::ExpandShapeOp>(
-          loc, MemRefType::get(rt.getShape(), rt.getElementType()), buf, re);
-    }
-    rewriter.replaceAllUsesWith(result, asTensor(loc, b, rt));
-  }
-
   ModuleOp module;
   IRRewriter rewriter;
   bool f32Mfma;
@@ -574,8 +893,8 @@ struct NovaHipLoweringPass
 
   StringRef getArgument() const final { return "nova-hip-lower"; }
   StringRef getDescription() const final {
-    return "Rewrite Nova's matmul / linear / layer_norm / sce ops (and their backward ops) "
-           "into calls to libnova_hip's gfx950 kernels";
+    return "Rewrite Nova's matmul / linear / layer_norm / sce ops, their backward ops and "
+           "the program glue into calls to libnova_hip's gfx950 kernels";
   }
   void getDependentDialects(DialectRegistry &registry) const override {
     registry.insert<arith::ArithDialect, bufferization::BufferizationDialect,
@@ -587,13 +906,33 @@ struct NovaHipLoweringPass
                               llvm::cl::desc("f32 GEMMs: 'exact' (bit-identical to the CPU "
                                              "pipeline) or 'mfma' (f32 matrix cores, 1e-4)"),
                               llvm::cl::init("exact")};
+  Option<bool> strict{*this, "strict",
+                      llvm::cl::desc("fail on any Nova op left for the NVPTX path (which "
+                                     "cannot run on AMD), with the form table's reason"),
+                      llvm::cl::init(false)};
 
   void runOnOperation() override {
     if (f32Gemm != "exact" && f32Gemm != "mfma") {
       getOperation().emitError() << "nova-hip-lower: f32-gemm must be 'exact' or 'mfma'";
       return signalPassFailure();
     }
-    Lowerer(getOperation(), f32Gemm == "mfma").run();
+    Lowerer l(getOperation(), f32Gemm == "mfma");
+    l.run();
+    if (!strict) return;
+    bool failed = false;
+    llvm::SmallPtrSet<Operation *, 16> reported;
+    for (auto &[op, why] : l.declinedOps) {
+      if (!op->getBlock() || !reported.insert(op).second) continue;
+      op->emitError() << "nova-hip-lower: not on the libnova_hip path: " << why;
+      failed = true;
+    }
+    for (Operation *op : l.leftovers()) {
+      if (reported.contains(op)) continue;
+      op->emitError() << "nova-hip-lower: not on the libnova_hip path: "
+                      << "not part of this path's op surface (or a view no lowered op folds)";
+      failed = true;
+    }
+    if (failed) signalPassFailure();
   }
 };
 

@@ -142,9 +142,21 @@ class Program:
                     or not t.is_cuda):
                 raise ValueError(f"argument needs a contiguous {DT_NAME[dt]} device tensor "
                                  f"of shape {shape}")
+        rspec = self.results(func)
         if results is None:
-            results = [torch.empty(shape, dtype=TORCH_DTYPE[dt], device=tensors[0].device)
-                       for dt, shape in self.results(func)]
+            dev = tensors[0].device if tensors else torch.device("cuda", torch.cuda.current_device())
+            results = [torch.empty(shape, dtype=TORCH_DTYPE[dt], device=dev) for dt, shape in rspec]
+        else:
+            # The kernels write each planned result's full byte size at its
+            # data pointer: the tensors must be exactly the planned results.
+            results = list(results)
+            if len(results) != len(rspec):
+                raise ValueError(f"@{func} has {len(rspec)} results, got {len(results)}")
+            for r, (dt, shape) in zip(results, rspec):
+                if (tuple(r.shape) != shape or r.dtype != TORCH_DTYPE[dt]
+                        or not r.is_contiguous() or not r.is_cuda):
+                    raise ValueError(f"result needs a contiguous {DT_NAME[dt]} device tensor "
+                                     f"of shape {shape}")
         nova_hip._bind_stream()
         pin = (ctypes.c_void_p * max(len(tensors), 1))(*[t.data_ptr() for t in tensors])
         pout = (ctypes.c_void_p * max(len(results), 1))(*[r.data_ptr() for r in results])

@@ -34,6 +34,7 @@
 #include <string>
 #include <vector>
 
+#include "../../include/nova_forms.h"
 #include "../../include/nova_hip.h"
 #include "../../include/nova_run.h"
 
@@ -434,6 +435,19 @@ int32_t infer(Op &op) {
                                 op.name.c_str(), n);
   };
   std::vector<Type> &R = op.result_types;
+  // Operand ranks outside the op's form (include/nova_forms.h) are declined
+  // before inference, with the table's reason.
+  if (const nova_forms::RankForm *rf = nova_forms::rank_form(op.name.c_str())) {
+    if ((int)T.size() == rf->nops)
+      for (int i = 0; i < rf->nops; ++i) {
+        const int r = (int)T[i].shape.size();
+        if (r < rf->min_rank[i] || r > rf->max_rank[i])
+          return fail(NOVA_HIP_EINVAL,
+                      "line %d: %s: operand rank outside the form (see nova_forms.h) (not on "
+                      "this path)",
+                      op.line, op.name.c_str());
+      }
+  }
   if (!R.empty() && op.name != "nova.cast") return NOVA_HIP_SUCCESS;
   int32_t rc;
   if (op.name == "nova.matmul") {
@@ -749,6 +763,32 @@ struct Planner {
                   op.line, what, op.name.c_str(), dt_name(v.dt));
     return NOVA_HIP_SUCCESS;
   }
+  // The op's form against the table both carriers of the rewrite consult
+  // (include/nova_forms.h): each operand's stored and logical element type
+  // and shape, the result element types, and the attributes the form
+  // depends on.
+  int32_t form(const Op &op, std::initializer_list<const View *> vs,
+               const nova_forms::Attrs &at = nova_forms::Attrs(), const char *name = nullptr) {
+    nova_forms::Operand o[nova_forms::kMaxOperands];
+    int n = 0;
+    for (const View *v : vs) {
+      if (n == nova_forms::kMaxOperands) break;
+      o[n].stored = v->dt;
+      o[n].logical = v->logical;
+      o[n].rank = (int)v->shape.size();
+      o[n].shape = v->shape.data();
+      ++n;
+    }
+    int rd[8];
+    int nr = 0;
+    for (const Type &t : op.result_types)
+      if (nr < 8) rd[nr++] = t.dt;
+    const char *why = nova_forms::check(name ? name : op.name.c_str(), n, o, nr, rd, at);
+    if (why)
+      return fail(NOVA_HIP_EINVAL, "line %d: %s: %s (not on this path)", op.line, op.name.c_str(),
+                  why);
+    return NOVA_HIP_SUCCESS;
+  }
   int32_t need_dense_f32(const Op &op, const View &v, const char *what) {
     int32_t rc = need_f32(op, v, what);
     if (rc) return rc;
@@ -949,6 +989,7 @@ struct Planner {
       } else if (n == "linalg.matmul" || n == "linalg.batch_matmul") {
         View a, b, c;
         if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = get(op, 2, c))) return rc;
+        if ((rc = form(op, {&a, &b, &c}))) return rc;
         if (!c.zero)
           return fail(NOVA_HIP_EINVAL,
                       "line %d: %s accumulating into a non-zero tensor is not on this path", op.line,
@@ -963,14 +1004,16 @@ struct Planner {
         if ((rc = emit_gemm(op, k, a, b, nullptr, c, folded))) return rc;
       } else if (n == "nova.matmul") {
         View a, b;
-        if ((rc = get(op, 0, a)) || (rc = get(op, 1, b))) return rc;
+        if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = form(op, {&a, &b}))) return rc;
         View out;
         out.shape = op.result_types[0].shape;
         out.dt = op.result_types[0].dt;
         if ((rc = emit_gemm(op, k, a, b, nullptr, out, folded))) return rc;
       } else if (n == "nova.linear") {
         View x, w, bias;
-        if ((rc = get(op, 0, x)) || (rc = get(op, 1, w)) || (rc = get(op, 2, bias))) return rc;
+        if ((rc = get(op, 0, x)) || (rc = get(op, 1, w)) || (rc = get(op, 2, bias)) ||
+            (rc = form(op, {&x, &w, &bias})))
+          return rc;
         View out;
         out.shape = op.result_types[0].shape;
         out.dt = op.result_types[0].dt;
@@ -978,7 +1021,8 @@ struct Planner {
       } else if (n == "nova.gelu") {
         // not folded: its input has other uses (e.g. a gelu_backward)
         View x;
-        if ((rc = get(op, 0, x)) || (rc = need_dense_f32(op, x, "input"))) return rc;
+        if ((rc = get(op, 0, x)) || (rc = form(op, {&x})) || (rc = need_dense_f32(op, x, "input")))
+          return rc;
         Step s;
         s.kind = "gelu";
         s.in = {x};
@@ -989,7 +1033,7 @@ struct Planner {
         plan.steps.push_back(s);
       } else if (n == "nova.gelu_backward") {
         View go, x;
-        if ((rc = get(op, 0, go)) || (rc = get(op, 1, x)) ||
+        if ((rc = get(op, 0, go)) || (rc = get(op, 1, x)) || (rc = form(op, {&go, &x})) ||
             (rc = need_dense_f32(op, go, "grad_out")) || (rc = need_dense_f32(op, x, "input")))
           return rc;
         if (numel_of(go.shape) != numel_of(x.shape))
@@ -1004,16 +1048,18 @@ struct Planner {
         plan.steps.push_back(s);
       } else if (n == "nova.mul" && (ones.count(op.operands[0]) || ones.count(op.operands[1]))) {
         const size_t keep = ones.count(op.operands[0]) ? 1 : 0;
-        View v;
-        if ((rc = get(op, keep, v))) return rc;
+        View v, one;
+        if ((rc = get(op, keep, v)) || (rc = get(op, 1 - keep, one)) ||
+            (rc = form(op, {keep ? &one : &v, keep ? &v : &one})))
+          return rc;
         v.producer = -1;
         env[op.results[0]] = v;
         plan.steps.push_back(Step{"view", {}, {}, 0, 0,
                                   "nova.mul by splat 1.0 -> view " + view_str(v)});
       } else if (n == "nova.add" || n == "nova.sub" || n == "nova.mul" || n == "nova.div") {
         View a, b;
-        if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = need_dense_f32(op, a, "lhs")) ||
-            (rc = need_dense_f32(op, b, "rhs")))
+        if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = form(op, {&a, &b})) ||
+            (rc = need_dense_f32(op, a, "lhs")) || (rc = need_dense_f32(op, b, "rhs")))
           return rc;
         if (op.result_types[0].shape.size() > 4)
           return fail(NOVA_HIP_ESHAPE, "line %d: %s above rank 4", op.line, n.c_str());
@@ -1037,6 +1083,7 @@ struct Planner {
         if (t.dt != DT_F32)
           return fail(NOVA_HIP_EDTYPE, "line %d: nova.constant of %s is not on this path", op.line,
                       dt_name(t.dt));
+        if ((rc = form(op, {}))) return rc;
         const float value = strtof(v.c_str() + 6, nullptr);
         // x * 1.0 == x for every f32 x: a splat 1.0 whose every use is a
         // nova.mul that leaves the other operand's shape unchanged needs
@@ -1079,7 +1126,11 @@ struct Planner {
         plan.steps.push_back(Step{"view", {}, {}, 0, 0, "nova.reshape -> view " + view_str(v)});
       } else if (n == "nova.gather") {
         View t, idx;
-        if ((rc = get(op, 0, t)) || (rc = get(op, 1, idx)) || (rc = need_dense_f32(op, t, "input")))
+        nova_forms::Attrs at;
+        at.axis = op.attrs.count("axis") ? atoi(op.attrs.at("axis").c_str()) : 0;
+        if (at.axis < 0) at.axis += (int)op.operand_types[0].shape.size();
+        if ((rc = get(op, 0, t)) || (rc = get(op, 1, idx)) || (rc = form(op, {&t, &idx}, at)) ||
+            (rc = need_dense_f32(op, t, "input")))
           return rc;
         if ((op.attrs.count("axis") && atoi(op.attrs.at("axis").c_str()) != 0) || t.shape.size() != 2)
           return fail(NOVA_HIP_EINVAL, "line %d: nova.gather of a 2-D table along axis 0 only",
@@ -1098,8 +1149,12 @@ struct Planner {
         plan.steps.push_back(s);
       } else if (n == "nova.scatter_add") {
         View base, idx, src;
+        nova_forms::Attrs at;
+        at.axis = op.attrs.count("axis") ? atoi(op.attrs.at("axis").c_str()) : 0;
+        if (at.axis < 0) at.axis += (int)op.operand_types[0].shape.size();
         if ((rc = get(op, 0, base)) || (rc = get(op, 1, idx)) || (rc = get(op, 2, src)) ||
-            (rc = need_dense_f32(op, base, "input")) || (rc = need_dense_f32(op, src, "src")))
+            (rc = form(op, {&base, &idx, &src}, at)) || (rc = need_dense_f32(op, base, "input")) ||
+            (rc = need_dense_f32(op, src, "src")))
           return rc;
         if ((op.attrs.count("axis") && atoi(op.attrs.at("axis").c_str()) != 0) ||
             base.shape.size() != 2)
@@ -1140,9 +1195,9 @@ struct Planner {
                       op.line);
         std::vector<int> dims = reduce_dims(op, (int)x.shape.size());
         std::sort(dims.begin(), dims.end());
-        for (size_t i = 1; i < dims.size(); ++i)
-          if (dims[i] != dims[i - 1] + 1)
-            return fail(NOVA_HIP_EINVAL, "line %d: nova.reduce over non-adjacent dims", op.line);
+        nova_forms::Attrs at;
+        for (size_t i = 1; i < dims.size(); ++i) at.adjacent = at.adjacent && dims[i] == dims[i - 1] + 1;
+        if ((rc = form(op, {&x}, at))) return rc;
         if (dims.empty() || dims[0] < 0 || dims.back() >= (int)x.shape.size())
           return fail(NOVA_HIP_EINVAL, "line %d: bad nova.reduce dimension", op.line);
         Step s;
@@ -1188,7 +1243,9 @@ struct Planner {
         }
       } else if (n == "nova.layer_norm") {
         View x, g, b;
-        if ((rc = get(op, 0, x)) || (rc = get(op, 1, g)) || (rc = get(op, 2, b))) return rc;
+        if ((rc = get(op, 0, x)) || (rc = get(op, 1, g)) || (rc = get(op, 2, b)) ||
+            (rc = form(op, {&x, &g, &b})))
+          return rc;
         if ((rc = need_f32(op, x, "input")) || (rc = need_f32(op, g, "gamma")) ||
             (rc = need_f32(op, b, "beta")))
           return rc;
@@ -1203,7 +1260,7 @@ struct Planner {
         plan.steps.push_back(s);
       } else if (n == "nova.sce") {
         View x, t;
-        if ((rc = get(op, 0, x)) || (rc = get(op, 1, t))) return rc;
+        if ((rc = get(op, 0, x)) || (rc = get(op, 1, t)) || (rc = form(op, {&x, &t}))) return rc;
         if ((rc = need_f32(op, x, "logits")) || (rc = as_i32(op, t))) return rc;
         // nova.sce whose softmax feeds only a nova.sce_backward over the same
         // labels: one fused launch writes the loss and the gradient, and the
@@ -1241,7 +1298,14 @@ struct Planner {
         plan.steps.push_back(s);
       } else if (n == "nova.sce_backward") {
         View sm, t;
-        if ((rc = get(op, 0, sm)) || (rc = get(op, 1, t))) return rc;
+        nova_forms::Attrs at;
+        if (op.attrs.count("dim")) {
+          at.dim = atoi(op.attrs.at("dim").c_str());
+          if (at.dim < 0) at.dim += (int)op.operand_types[0].shape.size();
+          if (at.dim == (int)op.operand_types[0].shape.size() - 1) at.dim = -1;
+        }
+        if ((rc = get(op, 0, sm)) || (rc = get(op, 1, t)) || (rc = form(op, {&sm, &t}, at)))
+          return rc;
         if ((rc = need_f32(op, sm, "softmax")) || (rc = as_i32(op, t))) return rc;
         if (op.attrs.count("dim")) {
           const int d = atoi(op.attrs.at("dim").c_str());
@@ -1260,7 +1324,7 @@ struct Planner {
       } else if (n == "nova.layer_norm_backward") {
         View gy, x, g, S, r;
         if ((rc = get(op, 0, gy)) || (rc = get(op, 1, x)) || (rc = get(op, 2, g)) ||
-            (rc = get(op, 3, S)) || (rc = get(op, 4, r)))
+            (rc = get(op, 3, S)) || (rc = get(op, 4, r)) || (rc = form(op, {&gy, &x, &g, &S, &r})))
           return rc;
         for (const View *v : {&gy, &x, &g, &S, &r})
           if ((rc = need_f32(op, *v, "operand"))) return rc;
@@ -1275,7 +1339,9 @@ struct Planner {
         plan.steps.push_back(s);
       } else if (n == "nova.linear_backward" || n == "nova.matmul_backward") {
         View go, x, w;
-        if ((rc = get(op, 0, go)) || (rc = get(op, 1, x)) || (rc = get(op, 2, w))) return rc;
+        if ((rc = get(op, 0, go)) || (rc = get(op, 1, x)) || (rc = get(op, 2, w)) ||
+            (rc = form(op, {&go, &x, &w})))
+          return rc;
         if (go.dt != x.dt || x.dt != w.dt)
           return fail(NOVA_HIP_EDTYPE, "line %d: %s operands must share a stored dtype", op.line,
                       n.c_str());
@@ -1575,6 +1641,12 @@ struct NovaRunProgram {
   // over and over); freed by nova_run_free.
   mutable std::mutex mu;
   mutable std::map<std::string, std::vector<std::pair<void *, int64_t>>> buffers;
+  // Per function: an event recorded on the stream of its last device
+  // execution, after that execution's last launch.  The next execution (on
+  // any stream) waits for it before touching the held buffers, so two
+  // executions of one program never run on those buffers at once; and the
+  // buffers are freed only once it has completed.
+  mutable std::map<std::string, hipEvent_t> done;
   int f32_gemm = NOVA_RUN_F32_GEMM_EXACT;  // nova_run_set_f32_gemm
   const Func *find(const char *name) const {
     for (const Func &f : funcs)
@@ -1582,6 +1654,11 @@ struct NovaRunProgram {
     return funcs.size() == 1 && !name ? &funcs[0] : nullptr;
   }
   void release() {
+    for (auto &kv : done) {
+      (void)hipEventSynchronize(kv.second);
+      (void)hipEventDestroy(kv.second);
+    }
+    done.clear();
     for (auto &kv : buffers)
       for (auto &b : kv.second)
         if (b.first) (void)hipFree(b.first);
@@ -1832,14 +1909,22 @@ int32_t nova_run_execute_device(const NovaRunProgram *p, const char *func,
   // The program's own buffers, kept from the last device execution of this
   // function while the plan's sizes match.
   std::vector<std::pair<void *, int64_t>> &held = p->buffers[f->name + "#device"];
+  hipEvent_t &done = p->done[f->name + "#device"];
+  if (!done && hipEventCreateWithFlags(&done, hipEventDisableTiming) != hipSuccess) {
+    done = nullptr;
+    return fail(NOVA_HIP_EDEVICE, "hipEventCreate failed");
+  }
   bool reuse = held.size() == nb;
   for (size_t b = 0; reuse && b < nb; ++b)
     reuse = held[b].second == (mine[b] ? pl.bufs[b].bytes : 0);
   if (!reuse) {
-    (void)hipStreamSynchronize(st);
+    // The last execution (whatever stream it ran on) may still use them.
+    (void)hipEventSynchronize(done);
     for (auto &h : held)
       if (h.first) (void)hipFree(h.first);
     held.assign(nb, {nullptr, 0});
+  } else if (hipStreamWaitEvent(st, done, 0) != hipSuccess) {
+    return fail(NOVA_HIP_EDEVICE, "hipStreamWaitEvent failed");
   }
   for (size_t b = 0; b < nb; ++b) {
     if (!mine[b]) continue;
@@ -1853,6 +1938,12 @@ int32_t nova_run_execute_device(const NovaRunProgram *p, const char *func,
     }
     ptr[b] = held[b].first;
   }
+  // Whatever happens below, the event marks the end of what was queued.
+  struct Mark {
+    hipEvent_t ev;
+    hipStream_t st;
+    ~Mark() { (void)hipEventRecord(ev, st); }
+  } mark{done, st};
   for (const Step &s : pl.steps) {
     if ((rc = run_step(s, ptr, st))) {
       const std::string why = nova_hip_last_error();

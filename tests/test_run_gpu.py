@@ -111,8 +111,9 @@ def test_backward_programs(cuda):
     bb = S.uniform((128, 96), 77, dtype=S.BF16, offset=g.size + a.size)
     ga, gbb = p.run("mm_bwd", g, a, bb)
     ga_ref, gb_ref2 = ref.matmul_backward(g, a, bb, dt=S.BF16)
-    assert_close_lp(S.widen(ga, S.BF16), ga_ref, "bf16 grad_a")
-    assert_close_lp(S.widen(gbb, S.BF16), gb_ref2, "bf16 grad_b")
+    assert ga.dtype == np.float32 and gbb.dtype == np.float32
+    assert_close_lp(ga, ga_ref, "bf16 grad_a")
+    assert_close_lp(gbb, gb_ref2, "bf16 grad_b")
 
 
 def test_memref_entry_fills_output_argument(cuda):
@@ -310,3 +311,45 @@ def test_f16_nova_matmul_accumulates_in_f16(cuda):
     B = S.uniform((3, 300, 40), 83, dtype=S.F16, offset=A.size)
     (C,) = p.run("h", A, B)
     assert np.array_equal(np.asarray(C).view(np.uint16), ref.gemm_acc_out(A, B, dt=S.F16))
+
+
+CHAIN = """func.func @chain(%x: tensor<1024x1024xf32>, %w1: tensor<1024x1024xf32>, %w2: tensor<1024x1024xf32>) -> tensor<1024x1024xf32> {
+  %t = nova.matmul %x, %w1 : tensor<1024x1024xf32>, tensor<1024x1024xf32>
+  %r = nova.matmul %t, %w2 : tensor<1024x1024xf32>, tensor<1024x1024xf32>
+  return %r : tensor<1024x1024xf32>
+}"""
+
+
+def test_device_executions_on_two_streams_are_ordered(cuda):
+    """Device executions of one program share its held intermediates (%t):
+    an execution queued on a second stream right after one on the first waits
+    for it on the device, so both give the single-stream bits."""
+    import torch
+    p = nova_run.Program(CHAIN)
+    ins = [torch.from_numpy(S.uniform((1024, 1024), 90 + i)).to(cuda) for i in range(4)]
+    want1 = p.run_device("chain", ins[0], ins[2], ins[3])[0].clone()
+    want2 = p.run_device("chain", ins[1], ins[2], ins[3])[0].clone()
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            o1 = p.run_device("chain", ins[0], ins[2], ins[3])[0]
+        with torch.cuda.stream(s2):
+            o2 = p.run_device("chain", ins[1], ins[2], ins[3])[0]
+        torch.cuda.synchronize()
+        assert torch.equal(o1, want1) and torch.equal(o2, want2)
+
+
+def test_device_execute_checks_given_results(cuda):
+    """Caller-supplied result tensors must be exactly the planned results
+    (shape, dtype, contiguity, device): the kernels write their full size."""
+    import torch
+    p = nova_run.Program(CHAIN)
+    x = torch.zeros(1024, 1024, device=cuda)
+    for bad in (torch.empty(1024, 1023, device=cuda), torch.empty(1024, 1024, device=cuda,
+                dtype=torch.float16), torch.empty(1024, 2048, device=cuda)[:, ::2],
+                torch.empty(1024, 1024)):
+        with pytest.raises(ValueError, match="result needs"):
+            p.run_device("chain", x, x, x, results=[bad])
+    with pytest.raises(ValueError, match="has 1 results"):
+        p.run_device("chain", x, x, x, results=[])
