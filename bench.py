@@ -32,6 +32,7 @@ sys.path.insert(0, os.path.join(REPO, "nova-compiler_amd"))
 PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU
 PEAK_HBM_GBS = 8000.0
 
+C1_FLOP = 2 * 256 ** 3                       # 33,554,432
 C2_FLOP = 2 * 8 * 4096 ** 3                  # 1,099,511,627,776
 C3_FLOP = 2 * 4096 * 4096 * 11008            # 369,367,187,456
 C4_FLOP = 2 * 96 * 197 * 197 * 64            # 476,884,992 (both shapes)
@@ -148,6 +149,25 @@ def bench_c2(args, torch, nh, S):
     del A, B, C
     tf = C2_FLOP / (ms * 1e-3) / 1e12
     return {"ms": ms, "tflops": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS, "finite": finite}
+
+
+def bench_c1(args, torch, nh, S):
+    """Config 1, the plumbing case: nova.matmul f32 256x256 . 256x256 on the
+    exact f32 kernel (bit-identical to the CPU pipeline)."""
+    inp = S.config_inputs("c1")
+    A, B = to_dev(inp["A"], S.F32, torch), to_dev(inp["B"], S.F32, torch)
+    C = torch.empty(256, 256, device="cuda")
+    d = [nh.ref(nh.memref_of(t)) for t in (A, B, C)]
+    f_ = nh.lib()._mlir_ciface_nova_hip_matmul_f32
+
+    def fn(_):
+        rc = f_(*d)
+        if rc:
+            nh.check(rc)
+
+    nh._bind_stream()
+    ms = time_launches(fn, args.steps * 4, args.warmup, torch)
+    return {"ms": ms, "tflops": C1_FLOP / (ms * 1e-3) / 1e12}
 
 
 def bench_c3(args, torch, nh, S):
@@ -460,6 +480,61 @@ def cpu_baseline(S):
             "host_cpus": os.cpu_count(), "host_cpu_model": cpu_model()}
 
 
+def cpu_baselines(S, only):
+    """The CPU oracle (one thread, the reference CPU pipeline's loop orders)
+    on configs 1, 3, 4 and 5: configs 1, 4a, 4b, LayerNorm and SCE in full;
+    config 3 on a slab of its first 8 rows (all 11008 outputs, K = 4096, bias
+    + GELU, bf16 out), extrapolated linearly.  Seconds per full config and
+    the rate in the config's unit."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import nova_cpu_ref as ref
+    out = {}
+
+    def timed(f):
+        t0 = time.perf_counter()
+        f()
+        return time.perf_counter() - t0
+
+    if "c1" in only:
+        inp = S.config_inputs("c1")
+        t = timed(lambda: ref.gemm(inp["A"], inp["B"]))
+        out["c1_matmul_f32_256"] = {"value": C1_FLOP / t / 1e9, "unit": "GFLOP/s", "cores": 1,
+                                    "kind": "port", "sample": "config 1 in full",
+                                    "seconds_full_config": t}
+    if "c3" in only:
+        inp = S.config_inputs("c3")
+        rows = 8
+        x = inp["x"][:rows]
+        t = timed(lambda: ref.gemm(x, inp["W"].T, adt=S.BF16, bdt=S.BF16, bias=inp["bias"],
+                                   biasdt=S.BF16, epilogue=ref.EPI_BIAS_GELU, cdt=S.BF16))
+        flop = 2.0 * rows * 4096 * 11008
+        out["c3_linear_bias_gelu_bf16"] = {
+            "value": flop / t / 1e9, "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"config 3 slab: rows 0-{rows - 1} of x, all 11008 outputs, K=4096, "
+                      f"bias+GELU, bf16 out ({flop:.3g} FLOP in {t:.2f} s); extrapolated linearly",
+            "seconds_full_config": t * 4096 / rows, "extrapolated": True}
+    if "c4" in only:
+        for name, key in (("c4a", "c4a_fp16_96x197x197x64"), ("c4b", "c4b_fp16_96x197x64x197")):
+            inp = S.config_inputs(name)
+            t = timed(lambda: ref.gemm(inp["A"], inp["B"], adt=S.F16, bdt=S.F16))
+            out[key] = {"value": C4_FLOP / t / 1e9, "unit": "GFLOP/s", "cores": 1,
+                        "kind": "port", "sample": f"config {name} in full",
+                        "seconds_full_config": t}
+    if "ln" in only:
+        inp = S.config_inputs("c5_ln")
+        t = timed(lambda: ref.layer_norm(inp["x"], inp["gamma"], inp["beta"]))
+        out["c5_layer_norm_f32_16384x4096"] = {
+            "value": LN_BYTES / t / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "config 5 LayerNorm in full", "seconds_full_config": t}
+    if "sce" in only:
+        inp = S.config_inputs("c5_sce")
+        t = timed(lambda: ref.sce(inp["logits"], inp["labels"]))
+        out["c5_sce_f32_4096x32000"] = {
+            "value": SCE_BYTES / t / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "config 5 SCE (mean loss) in full", "seconds_full_config": t}
+    return out
+
+
 def cpu_model():
     """The host CPU's model name, from /proc/cpuinfo."""
     try:
@@ -487,7 +562,7 @@ def main():
     torch.cuda.set_device(0)
     nh.lib()
     only = (set(args.only.split(",")) if args.only else
-            {"c2", "c3", "c4", "ln", "sce", "sce_bwd", "sce_fwd_bwd", "ln_bwd", "c3_bwd",
+            {"c1", "c2", "c3", "c4", "ln", "sce", "sce_bwd", "sce_fwd_bwd", "ln_bwd", "c3_bwd",
              "c2_vendor", "gpt_step"})
     cfg = {}
 
@@ -504,6 +579,8 @@ def main():
         return r
 
     c2 = stage("c2", lambda: bench_c2(args, torch, nh, S)) if "c2" in only else None
+    if "c1" in only:
+        cfg["c1_matmul_f32_256"] = stage("c1", lambda: bench_c1(args, torch, nh, S))
     if "c3" in only:
         cfg["c3_linear_bias_gelu_bf16"] = stage("c3", lambda: bench_c3(args, torch, nh, S))
     if "c4" in only:
@@ -534,6 +611,17 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = stage("cpu_baseline", lambda: cpu_baseline(S))
+        # The oracle on one core for each other config of BASELINE.json, in
+        # full where that takes seconds, config 3 on a slab (extrapolated),
+        # reported beside the config it belongs to.
+        per = stage("cpu_baselines", lambda: cpu_baselines(S, only))
+        for key, c in per.items():
+            if key in cfg and isinstance(cfg[key], dict):
+                cfg[key]["cpu_baseline"] = c
+                if "ms" in cfg[key] and c.get("seconds_full_config"):
+                    cfg[key]["gpu_over_cpu"] = c["seconds_full_config"] / (cfg[key]["ms"] * 1e-3)
+            else:
+                cfg[key] = {"cpu_baseline": c}
 
     # HBM bytes per config-2 launch: two rocprofv3 --pmc runs (FETCH_SIZE,
     # WRITE_SIZE) of `bench.py --only c2`, scaled by the copy calibration and

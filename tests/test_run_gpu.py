@@ -353,3 +353,83 @@ def test_device_execute_checks_given_results(cuda):
             p.run_device("chain", x, x, x, results=[bad])
     with pytest.raises(ValueError, match="has 1 results"):
         p.run_device("chain", x, x, x, results=[])
+
+
+# The shapes of the reference's own GEMM pipeline tests, as programs in this
+# path's op surface, against the oracle (f32: the exact kernel, so bit for
+# bit).  test/pipeline-tests/01_matmul_non_aligned.mlir (100x300 . 300x200),
+# 03_batch_matmul.mlir (4x64x256 . 4x256x64; 1x128x256 . 1x256x128 in its
+# second function), 04_matmul_bias_fusion.mlir (the 100x200 matmul plus a
+# [100, 200] bias added elementwise) and 13_matmul_bias_relu.mlir (128x256 .
+# 256x512 with a [512] bias, which FuseMatmulBias folds into the accumulator:
+# FuseMatmulBias.cpp:184-188).  Those files accumulate into a function
+# argument (outs = %C) or go on into linalg.generic / relu, forms outside
+# this path; the products and biases are the same.
+REF_SHAPES = """func.func @p01(%A: tensor<100x300xf32>, %B: tensor<300x200xf32>) -> tensor<100x200xf32> {
+  %r = nova.matmul %A, %B : tensor<100x300xf32>, tensor<300x200xf32>
+  return %r : tensor<100x200xf32>
+}
+func.func @p03(%A: tensor<4x64x256xf32>, %B: tensor<4x256x64xf32>) -> tensor<4x64x64xf32> {
+  %z = arith.constant 0.000000e+00 : f32
+  %e = tensor.empty() : tensor<4x64x64xf32>
+  %c = linalg.fill ins(%z : f32) outs(%e : tensor<4x64x64xf32>) -> tensor<4x64x64xf32>
+  %r = linalg.batch_matmul ins(%A, %B : tensor<4x64x256xf32>, tensor<4x256x64xf32>) outs(%c : tensor<4x64x64xf32>) -> tensor<4x64x64xf32>
+  return %r : tensor<4x64x64xf32>
+}
+func.func @p03b(%A: tensor<1x128x256xf32>, %B: tensor<1x256x128xf32>) -> tensor<1x128x128xf32> {
+  %r = nova.matmul %A, %B : tensor<1x128x256xf32>, tensor<1x256x128xf32>
+  return %r : tensor<1x128x128xf32>
+}
+func.func @p04(%A: tensor<100x300xf32>, %B: tensor<300x200xf32>, %bias: tensor<100x200xf32>) -> tensor<100x200xf32> {
+  %z = arith.constant 0.000000e+00 : f32
+  %e = tensor.empty() : tensor<100x200xf32>
+  %c = linalg.fill ins(%z : f32) outs(%e : tensor<100x200xf32>) -> tensor<100x200xf32>
+  %m = linalg.matmul ins(%A, %B : tensor<100x300xf32>, tensor<300x200xf32>) outs(%c : tensor<100x200xf32>) -> tensor<100x200xf32>
+  %r = nova.add %m, %bias : tensor<100x200xf32>, tensor<100x200xf32>
+  return %r : tensor<100x200xf32>
+}
+func.func @p13(%x: tensor<128x256xf32>, %w: tensor<256x512xf32>, %b: tensor<512xf32>) -> tensor<128x512xf32> {
+  %r = nova.linear %x, %w, %b : tensor<128x256xf32>, tensor<256x512xf32>, tensor<512xf32>
+  return %r : tensor<128x512xf32>
+}
+"""
+
+
+def test_reference_pipeline_test_shapes(cuda):
+    p = nova_run.Program(REF_SHAPES)
+    A = S.uniform((100, 300), 95)
+    B = S.uniform((300, 200), 95, offset=A.size)
+    (r,) = p.run("p01", A, B)
+    assert np.array_equal(r, ref.gemm(A, B)[0])
+    A3 = S.uniform((4, 64, 256), 96)
+    B3 = S.uniform((4, 256, 64), 96, offset=A3.size)
+    (r,) = p.run("p03", A3, B3)
+    assert np.array_equal(r, ref.gemm(A3, B3))
+    A1 = S.uniform((1, 128, 256), 97)
+    B1 = S.uniform((1, 256, 128), 97, offset=A1.size)
+    (r,) = p.run("p03b", A1, B1)
+    assert np.array_equal(r, ref.gemm(A1, B1))
+    bias2 = S.uniform((100, 200), 98)
+    (r,) = p.run("p04", A, B, bias2)
+    assert np.array_equal(r, ref.binary(ref.gemm(A, B)[0], bias2, ref.ADD))
+    x = S.uniform((128, 256), 99)
+    w = S.uniform((256, 512), 99, offset=x.size)
+    b = S.uniform((512,), 99, offset=x.size + w.size)
+    (r,) = p.run("p13", x, w, b)
+    assert np.array_equal(r, ref.gemm(x, w, bias=b, epilogue=ref.EPI_BIAS)[0])
+
+
+def test_reference_batch_shape_bf16_into_f32_outs(cuda):
+    """03_batch_matmul.mlir's shape with bf16 ins and zero-filled f32 outs
+    (the F1 form): f32 accumulate on the matrix cores, at the bf16 bar."""
+    text = """func.func @b(%A: tensor<4x64x256xbf16>, %B: tensor<4x256x64xbf16>) -> tensor<4x64x64xf32> {
+      %z = arith.constant 0.000000e+00 : f32
+      %e = tensor.empty() : tensor<4x64x64xf32>
+      %c = linalg.fill ins(%z : f32) outs(%e : tensor<4x64x64xf32>) -> tensor<4x64x64xf32>
+      %r = linalg.batch_matmul ins(%A, %B : tensor<4x64x256xbf16>, tensor<4x256x64xbf16>) outs(%c : tensor<4x64x64xf32>) -> tensor<4x64x64xf32>
+      return %r : tensor<4x64x64xf32>
+    }"""
+    A = S.uniform((4, 64, 256), 100, dtype=S.BF16)
+    B = S.uniform((4, 256, 64), 100, dtype=S.BF16, offset=A.size)
+    (r,) = nova_run.Program(text).run("b", A, B)
+    assert_close_lp(r, ref.gemm(A, B, adt=S.BF16, bdt=S.BF16), "03 shape bf16")
