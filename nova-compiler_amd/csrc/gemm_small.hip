@@ -323,6 +323,11 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
   const int tn = __builtin_amdgcn_readfirstlane(t - tm * a.tiles_n);
   const int m0 = tm * s.bm, n0 = tn * s.nt;
   const int m_valid = min(s.bm, a.M - m0), n_valid = min(s.nt, a.N - n0);
+  // The epilogue writes rows [m0, m0 + m_valid) only: its own copy of the
+  // arguments ends the output at the window's last row, so every store of a
+  // row past it is dropped by the range check (or the row test).
+  GemmArgs ge = a;
+  ge.M = m0 + m_valid;
 
   const uint16_t *A = a.A + (int64_t)bidx * a.sab;
   const uint16_t *B = a.B + (int64_t)bidx * a.sbb;
@@ -379,10 +384,10 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
   if constexpr (AD) {
     if (s.buf_store) {
       if (s.b_kc)
-        mfma_direct_store<DT, TNW, true, NT>(acc, fad, lds_b, s.pb, nw, ksteps, a, bidx,
+        mfma_direct_store<DT, TNW, true, NT>(acc, fad, lds_b, s.pb, nw, ksteps, ge, bidx,
                                              m0 + wm * 32, n0, lane);
       else
-        mfma_direct_store<DT, TNW, false, NT>(acc, fad, lds_b, s.pb, nw, ksteps, a, bidx,
+        mfma_direct_store<DT, TNW, false, NT>(acc, fad, lds_b, s.pb, nw, ksteps, ge, bidx,
                                               m0 + wm * 32, n0, lane);
       return;
     }
@@ -403,9 +408,9 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
                                          lane);
   }
   if (s.buf_store)
-    store_f32_buf<TNW, NT>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
+    store_f32_buf<TNW, NT>(acc, ge, bidx, m0 + wm * 32, n0 + nw, lane);
   else
-    store_outputs<1, TNW, NT>(acc, a, bidx, m0 + wm * 32, n0 + nw, lane);
+    store_outputs<1, TNW, NT>(acc, ge, bidx, m0 + wm * 32, n0 + nw, lane);
 }
 
 template <int DT>
@@ -503,8 +508,12 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
   // 788-byte rows) would take longer with it (9.7 -> 12.8 us).
   s.nt_store = a_in.out_dt == NOVA_HIP_DT_F32 && (reinterpret_cast<uintptr_t>(a_in.C) & 127u) == 0 &&
                a_in.scm % 32 == 0 && a_in.scb % 32 == 0 && a_in.N % 32 == 0;
+  // Buffer stores: 32-bit byte offsets.  A store instruction addresses rows
+  // up to 31 past the last valid one (dropped by the range), so the offsets
+  // of rows up to M + 31 must not wrap around 2^32 into the range either.
   s.buf_store = a_in.out_dt == NOVA_HIP_DT_F32 &&
-                ((int64_t)(a_in.M - 1) * a_in.scm + a_in.N) * 4 <= 0x7fffffff;
+                ((int64_t)(a_in.M - 1) * a_in.scm + a_in.N) * 4 <= 0x7fffffff &&
+                ((int64_t)(a_in.M + 31) * a_in.scm + a_in.N) * 4 < ((int64_t)1 << 32);
   s.a_kc = akc;
   s.b_kc = bkc;
   s.pa = p.pa;

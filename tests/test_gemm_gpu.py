@@ -804,3 +804,20 @@ def test_gemm_random_sweep(cuda, case):
         assert_close_f32(gs, want, what)
     else:
         assert np.array_equal(gs, want), (what, float(np.abs(gs - want).max()))
+
+
+def test_small_k_output_rows_far_apart(cuda):
+    """Small-K kernel, f32 output rows 2^26 elements apart (a strided view
+    of a 512 MB buffer) and M = 2: a store instruction of the last row window
+    addresses rows up to 31, whose 32-bit byte offsets (row * 2^28) would
+    wrap around 2^32 onto row 0 if the buffer-store path took them.  Every
+    written row matches the oracle and the rows between stay untouched."""
+    import torch
+    M, N, K, stride = 2, 64, 9, 1 << 26
+    a, b = lp_inputs((1, M, K), (1, K, N), S.F16, seed=17)
+    want = ref.gemm(a, b, adt=S.F16, bdt=S.F16)[0]
+    big = torch.full((M, stride), 7.0, device=cuda)
+    C = big[:, :N]
+    nh.gemm(to_dev(a[0], S.F16, cuda), to_dev(b[0], S.F16, cuda), out=C)
+    assert_close_lp(C.cpu().numpy(), want, "rows 2^26 apart")
+    assert bool((big[:, N:N + 4096] == 7.0).all())
