@@ -55,6 +55,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (cpu_baseline becomes null)")
+    ap.add_argument("--telemetry", action="store_true",
+                    help="also run config 2 (this library and hipBLASLt) and an MFMA-only probe "
+                         "back to back for --telemetry-seconds each while sampling board power "
+                         "and clocks with amd-smi (reported under 'telemetry')")
+    ap.add_argument("--telemetry-seconds", type=float, default=6.0)
     ap.add_argument("--only", default="",
                     help="comma list of configs to run (c2,c3,c4,ln,sce,sce_bwd,sce_fwd_bwd,ln_bwd,"
                          "c3_bwd,c2_vendor,gpt_step; copy = HBM copy calibration)")
@@ -535,6 +540,117 @@ def cpu_baselines(S, only):
     return out
 
 
+class PowerSampler:
+    """Samples `amd-smi metric -g 0 --power --clock --json` in a thread
+    (each call takes ~0.1 s) while a workload runs: socket power and the
+    mean of the graphics clocks of the eight XCDs."""
+
+    def __init__(self):
+        import threading
+        self.samples, self._stop = [], threading.Event()
+        self._th = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self):
+        import subprocess
+        while not self._stop.is_set():
+            try:
+                r = subprocess.run(["amd-smi", "metric", "-g", "0", "--power", "--clock",
+                                    "--json"], capture_output=True, text=True, timeout=20)
+                d = json.loads(r.stdout)
+                g = d["gpu_data"][0] if isinstance(d, dict) else d[0]
+                p = g["power"]["socket_power"]
+                clks = [v["clk"]["value"] for k, v in g["clock"].items()
+                        if k.startswith("gfx_") and isinstance(v, dict)
+                        and isinstance(v.get("clk"), dict)]
+                if isinstance(p, dict) and clks:
+                    self.samples.append((float(p["value"]), sum(clks) / len(clks)))
+            except Exception:  # a missing or failing amd-smi leaves no sample
+                time.sleep(0.2)
+
+    def __enter__(self):
+        self._th.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._th.join()
+
+    def summary(self):
+        if not self.samples:
+            return {"samples": 0}
+        pw = sorted(x[0] for x in self.samples)
+        ck = sorted(x[1] for x in self.samples)
+        return {"samples": len(pw), "power_w_median": pw[len(pw) // 2], "power_w_max": pw[-1],
+                "gfx_clock_mhz_median": ck[len(ck) // 2]}
+
+
+def telemetry(args, torch, nh, S):
+    """Board power and graphics clock (amd-smi) while each workload runs
+    back to back for args.telemetry_seconds: config 2 on this library's
+    kernel, on hipBLASLt (torch.bmm), and a loop of nothing but bf16 MFMAs
+    (nova-compiler_amd/libnova_probe.so, no memory traffic).  The MFMA busy
+    fraction follows as TFLOP/s / (peak x clock / 2.4 GHz)."""
+    import ctypes
+    out = {}
+
+    def drive(fn, flop):
+        t0 = time.time()
+        while time.time() - t0 < 1.0:          # settle the clock
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 0
+        with PowerSampler() as ps:
+            e0.record()
+            t0 = time.time()
+            while time.time() - t0 < args.telemetry_seconds:
+                for _ in range(20):
+                    fn()
+                n += 20
+                torch.cuda.synchronize()
+            e1.record()
+            torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        r = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "calls": n}
+        r.update(ps.summary())
+        if r.get("gfx_clock_mhz_median"):
+            r["mfma_busy_at_clock"] = r["tflops"] / (PEAK_BF16_TFLOPS * r["gfx_clock_mhz_median"]
+                                                     / 2400.0)
+        return r
+
+    inp = S.config_inputs("c2")
+    A = to_dev(inp["A"], S.BF16, torch)
+    B = to_dev(inp["B"], S.BF16, torch)
+    del inp
+    C = torch.empty(8, 4096, 4096, device="cuda", dtype=torch.float32)
+    d = [nh.ref(nh.memref_of(t)) for t in (A, B, C)]
+    f_ = nh.lib()._mlir_ciface_nova_hip_batch_matmul_bf16_f32
+    nh._bind_stream()
+    out["c2_gemm_pers_kernel"] = drive(lambda: f_(*d), C2_FLOP)
+    out["c2_hipblaslt"] = drive(lambda: torch.bmm(A, B, out_dtype=torch.float32, out=C), C2_FLOP)
+    del A, B, C
+    torch.cuda.empty_cache()
+    probe = ctypes.CDLL(os.path.join(REPO, "nova-compiler_amd", "libnova_probe.so"))
+    probe.nova_probe_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_void_p, ctypes.POINTER(ctypes.c_double)]
+    buf = torch.empty(256 * 256, device="cuda")
+    flop = ctypes.c_double(0.0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def mfma():
+        rc = probe.nova_probe_mfma_loop(ctypes.c_void_p(buf.data_ptr()), 256, 20000, stream,
+                                        ctypes.byref(flop))
+        if rc:
+            raise RuntimeError(f"probe launch failed: {rc}")
+
+    mfma()
+    torch.cuda.synchronize()
+    out["mfma_only_probe"] = drive(mfma, flop.value)
+    out["note"] = ("amd-smi socket power and mean XCD graphics clock, medians over the samples; "
+                   "mfma_busy_at_clock = TFLOP/s / (2516.6 x clock / 2400 MHz)")
+    return out
+
+
 def cpu_model():
     """The host CPU's model name, from /proc/cpuinfo."""
     try:
@@ -608,6 +724,8 @@ def main():
     if "copy" in only:  # calibration only; not part of the default run
         cfg["hbm_copy_256MiB"] = stage("copy", lambda: bench_copy(args, torch))
 
+    tele = stage("telemetry", lambda: telemetry(args, torch, nh, S)) if args.telemetry else None
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = stage("cpu_baseline", lambda: cpu_baseline(S))
@@ -662,6 +780,8 @@ def main():
         "cpu_baseline": cpu,
         "configs": cfg,
     }
+    if tele is not None:
+        line["telemetry"] = tele
     print(json.dumps(line), flush=True)
 
 
