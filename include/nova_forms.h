@@ -96,6 +96,8 @@ struct Attrs {
   bool splat_f32 = true;   // nova.constant: a splat dense<value> of f32
   bool ignore_nan = false; // nova.reduce
   bool adjacent = true;    // nova.reduce: the reduced dims are adjacent
+  bool outs_zero = true;   // linalg.(batch_)matmul: outs is a zero fill (else it holds
+                           // the accumulators' initial values)
 };
 
 inline bool is_float(int dt) {
@@ -186,6 +188,16 @@ inline const char *check(const char *op, int nops, const Operand *in, int nres,
     if (!strcmp(op, "linalg.batch_matmul") && (in[0].shape[0] != in[2].shape[0] ||
                                                in[1].shape[0] != in[2].shape[0]))
       return "linalg.batch_matmul batch sizes differ";
+    // Outs holding data (not a zero fill): the body C += A * B runs from
+    // that data, on the exact kernel (NOVA_HIP_GEMM_ACC_C): f32 operands, or
+    // 16-bit ones accumulating in their own type.
+    if (nops == 3 && !at.outs_zero) {
+      if (in[2].stored != out || in[2].logical != in[2].stored)
+        return "outs must be stored as the result type";
+      if (out == NOVA_HIP_DT_F32 && (in[0].stored != NOVA_HIP_DT_F32 || in[1].stored != NOVA_HIP_DT_F32))
+        return "16-bit operands accumulating into data-holding f32 outs are not on this path "
+               "(into a zero fill they are)";
+    }
     return gemm_dtypes(in[0], in[1], out, nullptr);
   }
   if (!strcmp(op, "nova.linear")) {

@@ -133,6 +133,17 @@ enum {
  * entry points. */
 #define NOVA_HIP_GEMM_F32_MFMA 0x20000
 
+/* flags bit 18: C holds the accumulator's initial values.  C = C + A . B in
+ * place, each element summed k ascending from its own value in C: a
+ * linalg.matmul / linalg.batch_matmul whose outs holds data, such as a
+ * function argument (test/pipeline-tests/02_matmul_aligned.mlir:15-19,
+ * 06_matmul_exact_tile.mlir:17-21, 11_lowering_config.mlir:21-27), runs its body
+ * C += A * B from that data where NovaMatmulOpLowering's zero fill
+ * (NovaToLinalg.cpp:1031-1049) would start from 0.  The exact kernel only:
+ * f32 in and out, or bf16 / f16 in and out with NOVA_HIP_GEMM_ACC_OUT; no
+ * epilogue; not with NOVA_HIP_GEMM_F32_MFMA.  C must not overlap A or B. */
+#define NOVA_HIP_GEMM_ACC_C 0x40000
+
 /* ------------------------------------------------------------------------
  * GEMM family.
  *

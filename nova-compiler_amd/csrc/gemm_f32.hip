@@ -53,6 +53,7 @@ struct F32Args {
   int M, N, K;
   int tiles_m, tiles_n;
   int bias_dt, epi;
+  int acc_c;  // the accumulators start from C's own values (C += A . B)
 };
 
 __device__ __forceinline__ float bias_value(const void *bias, int dt, int n) {
@@ -162,6 +163,19 @@ __global__ __launch_bounds__(256) void gemm_exact_kernel(F32Args a) {
     const float init = (has_bias && n < a.N) ? bias_value(a.bias, a.bias_dt, n) : 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i][j] = init;
+  }
+  if (a.acc_c) {
+    // linalg.matmul on data-holding outs: each sum starts from C's value.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + ty * 4 + i;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + tx * 4 + j;
+        if (m < a.M && n < a.N)
+          acc[i][j] = elem<DT>(a.C, (int64_t)b * a.scb + (int64_t)m * a.scm + n);
+      }
+    }
   }
 
   load(0);
@@ -325,6 +339,19 @@ __global__ __launch_bounds__(256) void gemm_exact_vec_kernel(F32Args a, uint32_t
 #pragma unroll
     for (int i = 0; i < RM; ++i) acc[i][j] = init;
   }
+  if (a.acc_c) {
+    // linalg.matmul on data-holding outs: each sum starts from C's value.
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      const int m = m0 + (i >> 2) * 4 * kVt + ty * 4 + (i & 3);
+      const float *crow = static_cast<const float *>(a.C) + (int64_t)b * a.scb + (int64_t)m * a.scm;
+#pragma unroll
+      for (int j = 0; j < CN; ++j) {
+        const int n = n0 + col(j);
+        if (m < a.M && n < a.N) acc[i][j] = crow[n];
+      }
+    }
+  }
   auto step = [&](int buf, int kk) __attribute__((always_inline)) {
     f32x4 av[RM / 4];
 #pragma unroll
@@ -451,6 +478,7 @@ int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s) {
   a.tiles_n = (int)((p.N + kT - 1) / kT);
   a.bias_dt = p.bias_dt;
   a.epi = p.epi;
+  a.acc_c = p.acc_c ? 1 : 0;
   // The vector forms: f32 with 16-byte aligned operand rows (aligned bases,
   // outer and batch strides multiples of 4, 32-bit buffer offsets).  The
   // form is the one of least estimated time: the tiles run in waves of two

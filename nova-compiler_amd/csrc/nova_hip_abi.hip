@@ -114,7 +114,7 @@ bool nonneg_sizes(const D *d, int rank) {
 }
 
 int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt) {
-  if (flags & ~(0xffff | NOVA_HIP_GEMM_ACC_OUT | NOVA_HIP_GEMM_F32_MFMA))
+  if (flags & ~(0xffff | NOVA_HIP_GEMM_ACC_OUT | NOVA_HIP_GEMM_F32_MFMA | NOVA_HIP_GEMM_ACC_C))
     return fail(NOVA_HIP_EINVAL, "gemm: unknown flag bits 0x%x", flags);
   in_dt = flags & 0xf;
   out_dt = (flags >> 4) & 0xf;
@@ -135,6 +135,18 @@ int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt)
         (epi == NOVA_HIP_EPI_BIAS && bias_dt != out_dt))
       return fail(NOVA_HIP_EDTYPE,
                   "gemm: a bf16 / f16 accumulator takes no GELU, and a bias of its own dtype only");
+  }
+  if (flags & NOVA_HIP_GEMM_ACC_C) {
+    // Accumulating into C's data runs on the exact kernel: f32, or a 16-bit
+    // accumulator of the operands' own type.
+    if (flags & NOVA_HIP_GEMM_F32_MFMA)
+      return fail(NOVA_HIP_EINVAL, "gemm: accumulating into C is not an f32 MFMA form");
+    if (in_dt != NOVA_HIP_DT_F32 && !(flags & NOVA_HIP_GEMM_ACC_OUT))
+      return fail(NOVA_HIP_EDTYPE,
+                  "gemm: accumulating into C needs f32 operands, or 16-bit ones with "
+                  "NOVA_HIP_GEMM_ACC_OUT");
+    if (epi != NOVA_HIP_EPI_NONE)
+      return fail(NOVA_HIP_EINVAL, "gemm: accumulating into C takes no epilogue");
   }
   return NOVA_HIP_SUCCESS;
 }
@@ -185,6 +197,7 @@ int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
   p.bias_dt = bias_dt;
   p.acc_out = (flags & NOVA_HIP_GEMM_ACC_OUT) != 0;
   p.f32_mfma = (flags & NOVA_HIP_GEMM_F32_MFMA) != 0;
+  p.acc_c = (flags & NOVA_HIP_GEMM_ACC_C) != 0;
   const int esz = dtype_size(in_dt);
   const int osz = dtype_size(out_dt);
   p.A = data_of(A) + A->offset * esz;
@@ -287,8 +300,9 @@ int32_t gemm2d_to(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C,
 
 // Flags of the backward GEMM entry points: dtypes only, no epilogue.
 int32_t backward_flags(int32_t flags, int &in_dt, int &out_dt, const char *what) {
-  if (flags & NOVA_HIP_GEMM_ACC_OUT)
-    return fail(NOVA_HIP_EINVAL, "%s: no narrow-accumulator form (flags 0x%x)", what, flags);
+  if (flags & (NOVA_HIP_GEMM_ACC_OUT | NOVA_HIP_GEMM_ACC_C))
+    return fail(NOVA_HIP_EINVAL, "%s: no narrow-accumulator or accumulate-into form (flags 0x%x)",
+                what, flags);
   int epi, bias_dt;
   int32_t rc = decode_flags(flags, in_dt, out_dt, epi, bias_dt);
   if (rc) return rc;

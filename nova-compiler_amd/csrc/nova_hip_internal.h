@@ -43,6 +43,7 @@ struct GemmProblem {
   int in_dt, out_dt, bias_dt, epi;
   bool acc_out;  // accumulate in the output dtype (NOVA_HIP_GEMM_ACC_OUT)
   bool f32_mfma;  // f32 on the matrix cores (NOVA_HIP_GEMM_F32_MFMA)
+  bool acc_c;     // C holds the accumulator's initial values (NOVA_HIP_GEMM_ACC_C)
 };
 
 // Launch the MFMA kernels (bf16/f16 in).  Returns a NOVA_HIP_* status.

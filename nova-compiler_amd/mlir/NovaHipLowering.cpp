@@ -51,7 +51,9 @@
 //     [B*M, .];
 //   * nova.sce whose softmax feeds only a nova.sce_backward over the same
 //     targets is one fused call, and the softmax is never materialised;
-//   * non-i32 targets / indices are widened by nova_hip_index_to_i32_* first.
+//   * non-i32 targets / indices are widened by nova_hip_index_to_i32_* first;
+//   * a linalg.(batch_)matmul whose outs holds data (not a zero fill) sums
+//     from a copy of that data (NOVA_HIP_GEMM_ACC_C, the exact kernel).
 // f32 GEMMs run the exact kernel (bit-identical to the CPU pipeline) unless
 // the pass option f32-gemm=mfma selects the f32 matrix cores.
 //
@@ -69,6 +71,7 @@
 #include "mlir/Dialect/LLVMIR/LLVMDialect.h"
 #include "mlir/Dialect/Linalg/IR/Linalg.h"
 #include "mlir/Dialect/MemRef/IR/MemRef.h"
+#include "mlir/Dialect/Tensor/IR/Tensor.h"
 #include "mlir/IR/AffineMap.h"
 #include "mlir/IR/BuiltinOps.h"
 #include "mlir/IR/PatternMatch.h"
@@ -372,15 +375,26 @@ class Lowerer {
     f.add(rhs, b.stored);
     if (bias) f.add(bias, bo.stored);
     if (outs) f.add(outs);
-    if (!rt || declined(op, form_name, f)) return failure();
-    if (bias && bo.transposed) return failure();  // a 1-D bias has no transpose
-    // linalg outs must be a zero fill (the product overwrites them).
+    // linalg outs: a zero fill (the product overwrites it) or data the sums
+    // start from (NOVA_HIP_GEMM_ACC_C); an uninitialised tensor.empty is
+    // neither.
+    bool accInto = false;
     if (outs) {
-      auto fill = outs.getDefiningOp<linalg::FillOp>();
-      if (!fill) return failure();
-      auto c = fill.getInputs()[0].getDefiningOp<arith::ConstantOp>();
-      auto fa = c ? dyn_cast<FloatAttr>(c.getValue()) : FloatAttr();
-      if (!fa || !fa.getValue().isZero()) return failure();
+      bool zeroFill = false;
+      if (auto fill = outs.getDefiningOp<linalg::FillOp>()) {
+        auto c = fill.getInputs()[0].getDefiningOp<arith::ConstantOp>();
+        auto fa = c ? dyn_cast<FloatAttr>(c.getValue()) : FloatAttr();
+        zeroFill = fa && fa.getValue().isZero();
+        if (!zeroFill) return failure();  // a non-zero fill: not on this path
+      }
+      if (!zeroFill && outs.getDefiningOp<tensor::EmptyOp>()) return failure();
+      accInto = !zeroFill;
+    }
+    nova_forms::Attrs at;
+    at.outs_zero = !accInto;
+    if (!rt || declined(op, form_name, f, at)) return failure();
+    if (bias && bo.transposed) return failure();  // a 1-D bias has no transpose
+    if (outs) {
       if (auto mm = dyn_cast<linalg::MatmulOp>(op))
         if (mm.getIndexingMapsArray() != linalg::MatmulOp::getDefaultIndexingMaps(op->getContext()))
           return failure();
@@ -395,7 +409,7 @@ class Lowerer {
     int epi = bias ? NOVA_HIP_EPI_BIAS : NOVA_HIP_EPI_NONE;
     Operation *last = op;
     SmallVector<Operation *> folded;
-    if (!narrow) {
+    if (!narrow && !accInto) {
       if (Value u = singleUse(result)) {
         Operation *user = *u.getUsers().begin();
         if (auto g = dyn_cast<GeluOp>(user)) {
@@ -427,6 +441,8 @@ class Lowerer {
     rewriter.setInsertionPoint(last);
     Value A = gemmOperand(loc, a), B = gemmOperand(loc, b);
     Value cBuf = alloc(loc, outTy);
+    // Summing into a copy of outs' data keeps the outs tensor's own value.
+    if (accInto) rewriter.create<memref::CopyOp>(loc, dense(loc, outs), cBuf);
     auto cs = outTy.getShape();
     const int64_t r = outTy.getRank();
     int64_t batch = 1;
@@ -438,7 +454,8 @@ class Lowerer {
                          : toAbi(loc, alloc(loc, RankedTensorType::get({0}, f32())));
     int32_t flags = NOVA_HIP_GEMM_FLAGS(in, out, epi, bias ? biasDt : 0);
     if (narrow) flags |= NOVA_HIP_GEMM_ACC_OUT;
-    if (in == NOVA_HIP_DT_F32 && f32Mfma) flags |= NOVA_HIP_GEMM_F32_MFMA;
+    if (accInto) flags |= NOVA_HIP_GEMM_ACC_C;  // the exact kernel, from cBuf's data
+    else if (in == NOVA_HIP_DT_F32 && f32Mfma) flags |= NOVA_HIP_GEMM_F32_MFMA;
     call(loc, name, {A, B, C, biasAbi, i32Const(loc, flags)});
     rewriter.replaceAllUsesWith(last->getResult(0), asTensor(loc, cBuf, outTy));
     for (auto it = folded.rbegin(); it != folded.rend(); ++it) {

@@ -75,6 +75,7 @@ EXPORTS = (
 
 GEMM_ACC_OUT = 0x10000  # NOVA_HIP_GEMM_ACC_OUT
 GEMM_F32_MFMA = 0x20000  # NOVA_HIP_GEMM_F32_MFMA
+GEMM_ACC_C = 0x40000  # NOVA_HIP_GEMM_ACC_C
 
 
 def gemm_flags(in_dt: int, out_dt: int, epi: int = EPI_NONE, bias_dt: int = 0) -> int:
@@ -224,7 +225,7 @@ def _as3(t):
 
 
 def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None,
-         acc_out: bool = False, f32_mfma: bool = False):
+         acc_out: bool = False, f32_mfma: bool = False, acc_c: bool = False):
     """Batched GEMM through _mlir_ciface_nova_hip_gemm.
 
     A [Bt,M,K] or [M,K]; B [Bt,K,N] or [K,N] (any unit-stride layout,
@@ -233,9 +234,14 @@ def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None,
     the output dtype (NOVA_HIP_GEMM_ACC_OUT; bf16 / f16 in and out).
     ``f32_mfma``: f32 operands on the f32 matrix cores (NOVA_HIP_GEMM_F32_MFMA;
     within 1e-4, not bit-identical to the sequential-k reference).
+    ``acc_c``: ``out`` holds the accumulators' initial values and receives
+    out + A . B in place (NOVA_HIP_GEMM_ACC_C, linalg.matmul on data-holding
+    outs; f32, or 16-bit with ``acc_out``).
     """
     torch = _torch()
     in_dt = _dt(A)
+    if acc_c and out is None:
+        raise NovaHipError(1, "acc_c accumulates into a given out tensor")
     if _dt(B) != in_dt:
         raise NovaHipError(4, "A and B must share a dtype")
     rank2 = A.dim() == 2 and B.dim() == 2
@@ -251,7 +257,7 @@ def gemm(A, B, out=None, *, bias=None, epilogue: int = EPI_NONE, out_dtype=None,
         C3 = _as3(out)
     bias_dt = _dt(bias) if bias is not None else 0
     flags = (gemm_flags(in_dt, od, epilogue, bias_dt) | (GEMM_ACC_OUT if acc_out else 0)
-             | (GEMM_F32_MFMA if f32_mfma else 0))
+             | (GEMM_F32_MFMA if f32_mfma else 0) | (GEMM_ACC_C if acc_c else 0))
     dA, dB, dC = memref_of(A3), memref_of(B3), memref_of(C3)
     dbias = memref_of(bias) if bias is not None else None
     _bind_stream()

@@ -673,6 +673,7 @@ struct Step {
   int64_t dims[3] = {0, 0, 0};  // reduce_sum: outer, reduced, inner
   bool acc_out = false;         // GEMM accumulating in its bf16 / f16 output dtype
   bool f32_mfma = false;        // f32 GEMM on the matrix cores (NOVA_HIP_GEMM_F32_MFMA)
+  bool acc_c = false;           // GEMM summing from its output's data (NOVA_HIP_GEMM_ACC_C)
 };
 
 int64_t numel_of(const std::vector<int64_t> &shape) {
@@ -727,6 +728,7 @@ struct Planner {
   std::map<std::string, int> uses;
   std::map<std::string, std::string> consts;
   std::set<int> empty_bufs;  // buffers of tensor.empty results
+  std::set<std::string> empty_vals;  // tensor.empty results (uninitialised data)
   std::set<std::string> ones;  // splat 1.0 constants whose every use is an identity multiply
   bool f32_mfma = false;       // plan f32 GEMMs onto the matrix cores
 
@@ -924,6 +926,49 @@ struct Planner {
     return NOVA_HIP_SUCCESS;
   }
 
+  // linalg.matmul / batch_matmul whose outs holds data: the result is
+  // outs + A . B, each sum starting from outs' element (NOVA_HIP_GEMM_ACC_C,
+  // the exact kernel).  The sums go into outs' own buffer when this op is
+  // the only reader of a dense intermediate; otherwise into a copy of it,
+  // so that a function argument or a value read again keeps its data.
+  int32_t emit_gemm_acc(const Op &op, const View &a, const View &b, View c) {
+    if (empty_vals.count(op.operands[2]))
+      return fail(NOVA_HIP_EINVAL, "line %d: %s reads an uninitialised tensor.empty as its outs",
+                  op.line, op.name.c_str());
+    if (!is_dense(c))
+      return fail(NOVA_HIP_ESTRIDE, "line %d: %s outs is a strided view (not on this path)",
+                  op.line, op.name.c_str());
+    const bool narrow = c.dt != DT_F32;
+    // Another value naming the same buffer (a reshape view, a value the
+    // buffer was handed on from) may still be read: then copy too.
+    bool shared = plan.bufs[c.buf].arg >= 0 || uses[op.operands[2]] != 1;
+    for (const auto &kv : env) shared = shared || (kv.first != op.operands[2] && kv.second.buf == c.buf);
+    View out = c;
+    if (shared) {
+      out = fresh(Type{c.shape, c.dt, false});
+      Step cp;
+      cp.kind = "copy";
+      cp.in = {c};
+      cp.out = {out};
+      cp.text = op.name + " outs -> hipMemcpyAsync(" + view_str(out) + " <- " + view_str(c) + ")";
+      plan.steps.push_back(cp);
+    }
+    out.zero = false;
+    out.producer = (int)plan.steps.size();
+    Step s;
+    s.kind = "gemm";
+    s.in = {a, b};
+    s.out = {out};
+    s.out_dt = out.dt;
+    s.acc_out = narrow;
+    s.acc_c = true;
+    s.text = op.name + " -> _mlir_ciface_nova_hip_gemm(" + view_str(a) + ", " + view_str(b) +
+             ") -> " + view_str(out) + " accumulate-into=" + dt_name(out.dt);
+    plan.steps.push_back(s);
+    env[op.results[0]] = out;
+    return NOVA_HIP_SUCCESS;
+  }
+
   int32_t run() {
     for (size_t i = 0; i < f.arg_names.size(); ++i) {
       View v;
@@ -947,6 +992,7 @@ struct Planner {
       } else if (n == "tensor.empty") {
         env[op.results[0]] = fresh(op.result_types[0]);
         empty_bufs.insert(env[op.results[0]].buf);
+        empty_vals.insert(op.results[0]);
       } else if (n == "bufferization.to_tensor") {
         View v;
         if ((rc = get(op, 0, v))) return rc;
@@ -989,11 +1035,13 @@ struct Planner {
       } else if (n == "linalg.matmul" || n == "linalg.batch_matmul") {
         View a, b, c;
         if ((rc = get(op, 0, a)) || (rc = get(op, 1, b)) || (rc = get(op, 2, c))) return rc;
-        if ((rc = form(op, {&a, &b, &c}))) return rc;
-        if (!c.zero)
-          return fail(NOVA_HIP_EINVAL,
-                      "line %d: %s accumulating into a non-zero tensor is not on this path", op.line,
-                      n.c_str());
+        nova_forms::Attrs at;
+        at.outs_zero = c.zero;
+        if ((rc = form(op, {&a, &b, &c}, at))) return rc;
+        if (!c.zero) {
+          if ((rc = emit_gemm_acc(op, a, b, c))) return rc;
+          continue;
+        }
         if (op.result_types[0].dt != DT_F32 && a.dt != op.result_types[0].dt)
           return fail(NOVA_HIP_EDTYPE, "line %d: %s with %s outs is not on this path", op.line,
                       n.c_str(), dt_name(op.result_types[0].dt));
@@ -1485,6 +1533,7 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
                                       reinterpret_cast<const NovaMemRef1D *>(pb),
                                       NOVA_HIP_GEMM_FLAGS(a.dt, s.out_dt, s.epi, bias_dt) |
                                           (s.acc_out ? NOVA_HIP_GEMM_ACC_OUT : 0) |
+                                          (s.acc_c ? NOVA_HIP_GEMM_ACC_C : 0) |
                                           (s.f32_mfma ? NOVA_HIP_GEMM_F32_MFMA : 0));
   }
   if (s.kind == "layer_norm") {

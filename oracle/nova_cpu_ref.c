@@ -217,6 +217,45 @@ int nova_ref_gemm_acc_out(const void *A, const void *B, int64_t sab, int64_t sam
 }
 
 /*
+ * linalg.matmul / linalg.batch_matmul whose outs holds data (a function
+ * argument, as in test/pipeline-tests/02_matmul_aligned.mlir:15-19): the
+ * named op's body C += A * B runs from each element's value in C, k
+ * ascending (the loop nest of nova_ref_gemm; NovaMatmulOpLowering's own
+ * linalg ops start from a zero fill instead, NovaToLinalg.cpp:1031-1049).
+ * C is dense [batch, M, N], read as the initial value and overwritten.
+ * cdt 0 (f32): operands extended to f32 (adt, bdt any float type), f32
+ * products and sums.  cdt 1 / 2 (bf16 / f16, == adt == bdt): every product
+ * and partial sum rounded to cdt, as in nova_ref_gemm_acc_out.
+ */
+int nova_ref_gemm_accumulate(const void *A, int adt, int64_t sab, int64_t sam, int64_t sak,
+                             const void *B, int bdt, int64_t sbb, int64_t sbk, int64_t sbn,
+                             void *C, int cdt, int64_t batch, int64_t M, int64_t N, int64_t K) {
+  if (!A || !B || !C || batch < 0 || M < 0 || N < 0 || K < 0) return -1;
+  if (cdt != 0 && (cdt != adt || cdt != bdt || (cdt != 1 && cdt != 2))) return -1;
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t i = 0; i < M; ++i)
+      for (int64_t j = 0; j < N; ++j) {
+        const int64_t c = (b * M + i) * N + j;
+        float v;
+        if (cdt == 0) {
+          v = dot_elem(A, adt, b * sab + i * sam, sak, B, bdt, b * sbb + j * sbn, sbk, K,
+                       load_as_f32(C, 0, c));
+        } else {
+          float acc = load_as_f32(C, cdt, c);
+          for (int64_t k = 0; k < K; ++k) {
+            float a = load_as_f32(A, cdt, b * sab + i * sam + k * sak);
+            float w = load_as_f32(B, cdt, b * sbb + k * sbk + j * sbn);
+            float p = round_to(cdt, a * w);
+            acc = round_to(cdt, acc + p);
+          }
+          v = acc;
+        }
+        store_from_f32(C, cdt, c, v);
+      }
+  return 0;
+}
+
+/*
  * Same arithmetic as nova_ref_gemm for a list of output coordinates
  * idx[3*t + {0,1,2}] = (b, i, j).  out[t] receives the value the reference
  * would store, widened back to f32 (so bf16/f16 outputs are already rounded).

@@ -33,6 +33,9 @@ def lib() -> ctypes.CDLL:
         L.nova_ref_gemm_sampled.argtypes = [P, I, I64, I64, I64, P, I, I64, I64, I64, P, I, I,
                                             I, I64, P, I64, P]
         L.nova_ref_gemm_sampled.restype = I
+        L.nova_ref_gemm_accumulate.argtypes = [P, I, I64, I64, I64, P, I, I64, I64, I64, P, I,
+                                               I64, I64, I64, I64]
+        L.nova_ref_gemm_accumulate.restype = I
         L.nova_ref_gelu_f32.argtypes = [ctypes.c_float]
         L.nova_ref_gelu_f32.restype = ctypes.c_float
         L.nova_ref_gelu_array.argtypes = [P, P, I64]
@@ -128,6 +131,20 @@ def gemm_acc_out(A, B, *, dt, bias=None) -> np.ndarray:
     rc = lib().nova_ref_gemm_acc_out(pa, pb, sab, sam, sak, sbb, sbk, sbn, pbias,
                                      EPI_BIAS if bias is not None else EPI_NONE,
                                      C.ctypes.data, dt, batch, M, N, K)
+    assert rc == 0, rc
+    return C
+
+
+def gemm_accumulate(A, B, C0, *, adt=None, bdt=None, cdt=F32) -> np.ndarray:
+    """linalg.matmul / batch_matmul on data-holding outs: C0 + A . B with
+    each sum starting from C0's element, k ascending; C0 [Bt,M,N] (f32, or
+    uint16 bits when cdt is bf16 / f16, then equal to adt and bdt).
+    Returns a new array; C0 is not modified."""
+    (pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn, batch, M, N, K) = _gemm_args(A, B, adt, bdt)
+    C = np.array(C0, dtype=np.float32 if cdt == F32 else np.uint16, copy=True).reshape(batch, M, N)
+    C = np.ascontiguousarray(C)
+    rc = lib().nova_ref_gemm_accumulate(pa, da, sab, sam, sak, pb, db, sbb, sbk, sbn,
+                                        C.ctypes.data, cdt, batch, M, N, K)
     assert rc == 0, rc
     return C
 

@@ -100,6 +100,26 @@ def test_gemm_bad_flags():
     assert "bias of its own dtype" in last_error()
 
 
+def test_gemm_accumulate_into_c_flags():
+    """NOVA_HIP_GEMM_ACC_C runs on the exact kernel only: not with the f32
+    MFMA form, not for 16-bit operands into an f32 accumulator, and with no
+    epilogue (the sum starts from C, not from a bias)."""
+    A, B, C = d3((1, 8, 16)), d3((1, 16, 8)), d3((1, 8, 8))
+    f32 = nh.gemm_flags(nh.DT_F32, nh.DT_F32)
+    accc = nh.GEMM_ACC_C
+    assert gemm_rc(A, B, C, flags=f32 | accc | nh.GEMM_F32_MFMA) == 1
+    assert "f32 MFMA" in last_error()
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_BF16, nh.DT_F32) | accc) == 4
+    assert gemm_rc(A, B, C, d1(8),
+                   nh.gemm_flags(nh.DT_F32, nh.DT_F32, nh.EPI_BIAS, nh.DT_F32) | accc) == 1
+    assert "no epilogue" in last_error()
+    assert gemm_rc(A, B, C, flags=nh.gemm_flags(nh.DT_F32, nh.DT_F32, nh.EPI_GELU) | accc) == 1
+    # an empty problem stays a no-op
+    assert gemm_rc(d3((1, 0, 16)), B, d3((1, 0, 8)), flags=f32 | accc) == 0
+    assert gemm_rc(d3((1, 0, 16)), B, d3((1, 0, 8)),
+                   flags=nh.gemm_flags(nh.DT_F16, nh.DT_F16) | nh.GEMM_ACC_OUT | accc) == 0
+
+
 def test_gemm_bias_required_and_checked():
     A, B, C = d3((1, 8, 16)), d3((1, 16, 8)), d3((1, 8, 8))
     f = nh.gemm_flags(nh.DT_BF16, nh.DT_BF16, nh.EPI_BIAS_GELU, nh.DT_BF16)
@@ -259,6 +279,7 @@ def test_linear_backward_validation():
     assert f(None, x, w) == 1
     assert f(go, x, w, flags=nh.gemm_flags(nh.DT_BF16, nh.DT_F32, nh.EPI_BIAS)) == 1
     assert f(go, x, w, flags=0x10000) == 1
+    assert f(go, x, w, flags=fl | 0x40000) == 1          # no accumulate-into form
     assert f(go, x, d2((31, 16))) == 2
     assert f(d2((8, 15)), x, w) == 2
     assert f(go, x, w, gi=d2((8, 31))) == 2          # grad_input must be [M, K]

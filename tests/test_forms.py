@@ -279,6 +279,26 @@ def test_linalg_matmul_dtype_forms(ins, outs, ok):
             p.plan("f")
 
 
+@pytest.mark.parametrize("ins,outs,ok", [
+    ("f32", "f32", True), ("bf16", "bf16", True), ("f16", "f16", True),
+    ("bf16", "f32", False), ("f16", "f32", False), ("bf16", "f16", False), ("f32", "bf16", False),
+])
+def test_linalg_matmul_into_data_holding_outs_dtype_forms(ins, outs, ok):
+    """outs holding data (a function argument): the exact kernel sums from it,
+    f32 or a 16-bit accumulator of the operands' own type; 16-bit operands
+    into f32 data are declined (their zero-filled form is not)."""
+    text = f"""func.func @f(%a: {T([4, 8], ins)}, %b: {T([8, 3], ins)}, %c: {T([4, 3], outs)}) {{
+      %r = linalg.matmul ins(%a, %b : {T([4, 8], ins)}, {T([8, 3], ins)}) outs(%c : {T([4, 3], outs)}) -> {T([4, 3], outs)}
+      return
+    }}"""
+    p = nova_run.Program(text)
+    if ok:
+        assert "accumulate-into=" in p.plan("f")
+    else:
+        with pytest.raises(nova_run.NovaRunError, match="not on this path"):
+            p.plan("f")
+
+
 @pytest.mark.parametrize("dt,cast,ok", [
     ("f32", False, True), ("bf16", True, True), ("bf16", False, False), ("f16", False, False),
 ])

@@ -821,3 +821,47 @@ def test_small_k_output_rows_far_apart(cuda):
     nh.gemm(to_dev(a[0], S.F16, cuda), to_dev(b[0], S.F16, cuda), out=C)
     assert_close_lp(C.cpu().numpy(), want, "rows 2^26 apart")
     assert bool((big[:, N:N + 4096] == 7.0).all())
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("shape", [(1, 100, 200, 300), (1, 256, 512, 128), (1, 128, 128, 128),
+                                   (2, 37, 45, 23), (3, 65, 70, 129), (4, 64, 64, 256)])
+def test_gemm_accumulate_into_c_bit_exact(cuda, layout, shape):
+    """NOVA_HIP_GEMM_ACC_C (linalg.matmul on data-holding outs): C + A . B with
+    each sum starting from C's value, k ascending; the exact kernel's scalar
+    form (unaligned rows) and vector forms (aligned), bit for bit."""
+    import torch
+    batch, M, N, K = shape
+    g = np.random.default_rng(131 + K)
+    a = g.uniform(-1, 1, (batch, M, K)).astype(np.float32)
+    b = g.uniform(-1, 1, (batch, K, N)).astype(np.float32)
+    c0 = g.uniform(-4, 4, (batch, M, N)).astype(np.float32)
+    A = view_as(a, layout[0], cuda, S.F32)
+    B = view_as(b, layout[1], cuda, S.F32)
+    C = torch.from_numpy(c0).to(cuda)
+    nh.gemm(A, B, C, acc_c=True)
+    assert np.array_equal(C.cpu().numpy(), ref.gemm_accumulate(a, b, c0)), (shape, layout)
+
+
+@pytest.mark.parametrize("dt", [S.BF16, S.F16])
+def test_gemm_accumulate_into_narrow_c_bit_exact(cuda, dt):
+    """The same into bf16 / f16 outs: every product and partial sum rounded
+    to that type, starting from C's value."""
+    import torch
+    batch, M, N, K = 2, 37, 45, 23
+    A, B = lp_inputs((batch, M, K), (batch, K, N), dt, 133)
+    c0 = S.uniform((batch, M, N), 134, dtype=dt)
+    C = to_dev(c0, dt, cuda).clone()
+    nh.gemm(to_dev(A, dt, cuda), to_dev(B, dt, cuda), C, acc_out=True, acc_c=True)
+    got = C.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, ref.gemm_accumulate(A, B, c0, adt=dt, bdt=dt, cdt=dt))
+
+
+def test_gemm_accumulate_with_k0_leaves_c(cuda):
+    import torch
+    A = torch.zeros((1, 5, 0), device=cuda)
+    B = torch.zeros((1, 0, 7), device=cuda)
+    C = torch.arange(35, dtype=torch.float32, device=cuda).reshape(1, 5, 7)
+    before = C.clone()
+    nh.gemm(A, B, C, acc_c=True)
+    assert torch.equal(C, before)

@@ -361,3 +361,59 @@ def test_narrow_accumulator_matches_torch_bfloat16():
     bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)
     got = ref.gemm_acc_out(bits(A), bits(B), dt=BF16, bias=bits(bias))[0]
     assert np.array_equal(got, bits(want))
+
+
+# ---- linalg.matmul on data-holding outs (C0 + A . B, from C0) ------------
+
+def test_gemm_accumulate_from_zero_and_from_bias_rows():
+    """Starting from zeros it is the plain GEMM; from C0 rows equal to a bias
+    it is the bias-first GEMM (FuseMatmulBias's accumulator init), bit for
+    bit.  C0 is left unmodified."""
+    g = rng(21)
+    A = g.uniform(-1, 1, (3, 17, 29)).astype(np.float32)
+    B = g.uniform(-1, 1, (3, 29, 11)).astype(np.float32)
+    zero = np.zeros((3, 17, 11), np.float32)
+    assert np.array_equal(ref.gemm_accumulate(A, B, zero), ref.gemm(A, B))
+    assert not zero.any()
+    bias = g.uniform(-2, 2, 11).astype(np.float32)
+    rows = np.broadcast_to(bias, (3, 17, 11)).copy()
+    assert np.array_equal(ref.gemm_accumulate(A, B, rows),
+                          ref.gemm(A, B, bias=bias, epilogue=ref.EPI_BIAS))
+
+
+def test_gemm_accumulate_starts_from_c():
+    """(1 + 1e8) - 1e8 = 0 in f32 when the sum starts from C0 = 1; adding C0
+    after the products ((1e8 - 1e8) + 1) would give 1."""
+    A = np.array([[1.0, 1.0]], np.float32)
+    B = np.array([[1e8], [-1e8]], np.float32)
+    assert ref.gemm_accumulate(A, B, np.ones((1, 1), np.float32))[0, 0, 0] == 0.0
+
+
+def test_gemm_accumulate_integer_grid_exact():
+    g = rng(22)
+    A = g.integers(-8, 9, (2, 33, 40)).astype(np.float32)
+    B = g.integers(-8, 9, (2, 40, 19)).astype(np.float32)
+    C0 = g.integers(-1000, 1001, (2, 33, 19)).astype(np.float32)
+    want = C0.astype(np.int64) + np.einsum("bmk,bkn->bmn", A.astype(np.int64), B.astype(np.int64))
+    assert np.array_equal(ref.gemm_accumulate(A, B, C0), want.astype(np.float32))
+    # a transposed A view, a rank-2 B broadcast over the batch
+    At = np.ascontiguousarray(A.transpose(0, 2, 1)).transpose(0, 2, 1)
+    want2 = C0.astype(np.int64) + np.einsum("bmk,kn->bmn", A.astype(np.int64),
+                                            B[0].astype(np.int64))
+    assert np.array_equal(ref.gemm_accumulate(At, B[0], C0), want2.astype(np.float32))
+
+
+def test_gemm_accumulate_narrow_outs():
+    """f16 outs: from zeros it is the narrow-accumulator GEMM; from 2048 a
+    sum of ones stays 2048 (each partial sum rounded to f16, C0 first)."""
+    g = rng(23)
+    A = g.uniform(-2, 2, (9, 31)).astype(np.float16).view(np.uint16)
+    B = g.uniform(-2, 2, (31, 5)).astype(np.float16).view(np.uint16)
+    zero = np.zeros((1, 9, 5), np.uint16)
+    assert np.array_equal(ref.gemm_accumulate(A, B, zero, adt=F16, bdt=F16, cdt=F16),
+                          ref.gemm_acc_out(A, B, dt=F16))
+    ones_a = _bits(np.ones((2, 3)), F16)
+    ones_b = _bits(np.ones((3, 4)), F16)
+    c0 = _bits(np.full((1, 2, 4), 2048.0), F16)
+    got = _widen(ref.gemm_accumulate(ones_a, ones_b, c0, adt=F16, bdt=F16, cdt=F16), F16)
+    assert np.all(got == 2048.0)

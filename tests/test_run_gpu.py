@@ -392,6 +392,18 @@ func.func @p13(%x: tensor<128x256xf32>, %w: tensor<256x512xf32>, %b: tensor<512x
   %r = nova.linear %x, %w, %b : tensor<128x256xf32>, tensor<256x512xf32>, tensor<512xf32>
   return %r : tensor<128x512xf32>
 }
+func.func @p02(%A: tensor<256x128xf32>, %B: tensor<128x512xf32>, %C: tensor<256x512xf32>) -> tensor<256x512xf32> {
+  %r = linalg.matmul ins(%A, %B : tensor<256x128xf32>, tensor<128x512xf32>) outs(%C : tensor<256x512xf32>) -> tensor<256x512xf32>
+  return %r : tensor<256x512xf32>
+}
+func.func @p06(%A: tensor<128x128xf32>, %B: tensor<128x128xf32>, %C: tensor<128x128xf32>) -> tensor<128x128xf32> {
+  %r = linalg.matmul ins(%A, %B : tensor<128x128xf32>, tensor<128x128xf32>) outs(%C : tensor<128x128xf32>) -> tensor<128x128xf32>
+  return %r : tensor<128x128xf32>
+}
+func.func @p11(%A: tensor<128x256xf32>, %B: tensor<256x512xf32>, %C: tensor<128x512xf32>) -> tensor<128x512xf32> {
+  %r = linalg.matmul ins(%A, %B : tensor<128x256xf32>, tensor<256x512xf32>) outs(%C : tensor<128x512xf32>) -> tensor<128x512xf32>
+  return %r : tensor<128x512xf32>
+}
 """
 
 
@@ -417,6 +429,28 @@ def test_reference_pipeline_test_shapes(cuda):
     b = S.uniform((512,), 99, offset=x.size + w.size)
     (r,) = p.run("p13", x, w, b)
     assert np.array_equal(r, ref.gemm(x, w, bias=b, epilogue=ref.EPI_BIAS)[0])
+
+
+@pytest.mark.parametrize("name,m,n,k", [("p02", 256, 512, 128), ("p06", 128, 128, 128),
+                                        ("p11", 128, 512, 256)])
+def test_reference_pipeline_tests_accumulating_into_outs(cuda, name, m, n, k):
+    """02_matmul_aligned.mlir, 06_matmul_exact_tile.mlir and
+    11_lowering_config.mlir run linalg.matmul into a function argument C:
+    the result is C + A . B with each sum starting from C (bit-exact against
+    the oracle), and C itself keeps its data, on host arrays and on device."""
+    import torch
+    p = nova_run.Program(REF_SHAPES)
+    A = S.uniform((m, k), 101)
+    B = S.uniform((k, n), 101, offset=A.size)
+    C = S.uniform((m, n), 102)
+    want = ref.gemm_accumulate(A, B, C)[0]
+    (r,) = p.run(name, A, B, C)
+    assert np.array_equal(r, want)
+    dA, dB, dC = (torch.from_numpy(np.ascontiguousarray(x)).to(cuda) for x in (A, B, C))
+    (dr,) = p.run_device(name, dA, dB, dC)
+    torch.cuda.synchronize()
+    assert np.array_equal(dr.cpu().numpy(), want)
+    assert np.array_equal(dC.cpu().numpy(), C)
 
 
 def test_reference_batch_shape_bf16_into_f32_outs(cuda):

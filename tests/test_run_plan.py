@@ -294,3 +294,74 @@ def test_rank4_matmul_plans_and_batch_transpose_is_refused():
         p.plan("mm4_batch_transposed")
     with pytest.raises(nova_run.NovaRunError, match="operand 1 is a view whose leading dims"):
         p.plan("sce_labels_transposed")
+
+
+ACC_PROGRAMS = """func.func @arg(%A: tensor<256x128xf32>, %B: tensor<128x512xf32>, %C: tensor<256x512xf32>) -> tensor<256x512xf32> {
+  %r = linalg.matmul ins(%A, %B : tensor<256x128xf32>, tensor<128x512xf32>) outs(%C : tensor<256x512xf32>) -> tensor<256x512xf32>
+  return %r : tensor<256x512xf32>
+}
+func.func @chain(%A: tensor<8x16xf32>, %B: tensor<16x4xf32>, %D: tensor<8x4xf32>, %E: tensor<4x4xf32>) -> tensor<8x4xf32> {
+  %p = nova.matmul %A, %B : tensor<8x16xf32>, tensor<16x4xf32>
+  %r = linalg.matmul ins(%D, %E : tensor<8x4xf32>, tensor<4x4xf32>) outs(%p : tensor<8x4xf32>) -> tensor<8x4xf32>
+  return %r : tensor<8x4xf32>
+}
+func.func @reread(%A: tensor<8x16xf32>, %B: tensor<16x4xf32>, %D: tensor<8x4xf32>, %E: tensor<4x4xf32>) -> (tensor<8x4xf32>, tensor<8x4xf32>) {
+  %p = nova.matmul %A, %B : tensor<8x16xf32>, tensor<16x4xf32>
+  %r = linalg.matmul ins(%D, %E : tensor<8x4xf32>, tensor<4x4xf32>) outs(%p : tensor<8x4xf32>) -> tensor<8x4xf32>
+  return %r, %p : tensor<8x4xf32>, tensor<8x4xf32>
+}
+func.func @batch(%A: tensor<4x64x256xf32>, %B: tensor<4x256x64xf32>, %C: tensor<4x64x64xf32>) -> tensor<4x64x64xf32> {
+  %r = linalg.batch_matmul ins(%A, %B : tensor<4x64x256xf32>, tensor<4x256x64xf32>) outs(%C : tensor<4x64x64xf32>) -> tensor<4x64x64xf32>
+  return %r : tensor<4x64x64xf32>
+}
+func.func @narrow(%A: tensor<8x16xf16>, %B: tensor<16x4xf16>, %C: tensor<8x4xf16>) -> tensor<8x4xf16> {
+  %r = linalg.matmul ins(%A, %B : tensor<8x16xf16>, tensor<16x4xf16>) outs(%C : tensor<8x4xf16>) -> tensor<8x4xf16>
+  return %r : tensor<8x4xf16>
+}
+func.func @wide16(%A: tensor<8x16xbf16>, %B: tensor<16x4xbf16>, %C: tensor<8x4xf32>) -> tensor<8x4xf32> {
+  %r = linalg.matmul ins(%A, %B : tensor<8x16xbf16>, tensor<16x4xbf16>) outs(%C : tensor<8x4xf32>) -> tensor<8x4xf32>
+  return %r : tensor<8x4xf32>
+}
+func.func @uninit(%A: tensor<8x16xf32>, %B: tensor<16x4xf32>) -> tensor<8x4xf32> {
+  %e = tensor.empty() : tensor<8x4xf32>
+  %r = linalg.matmul ins(%A, %B : tensor<8x16xf32>, tensor<16x4xf32>) outs(%e : tensor<8x4xf32>) -> tensor<8x4xf32>
+  return %r : tensor<8x4xf32>
+}
+"""
+
+
+def test_linalg_matmul_accumulates_into_data_holding_outs():
+    """linalg.matmul outs(%C) with %C holding data (the reference's
+    pipeline-test form, 02_matmul_aligned.mlir:15-19): one exact GEMM that
+    sums from C's values.  A function argument keeps its data (the sums go
+    into a copy); a sole-use intermediate is summed into in place; an
+    intermediate that is read again is copied first."""
+    p = nova_run.Program(ACC_PROGRAMS)
+    plan = p.plan("arg")
+    assert plan.count("hipMemcpyAsync") == 1 and "accumulate-into=f32" in plan
+    assert 2 not in _gemm_outputs(plan)                       # b2 is %C
+    assert p.results("arg") == [(0, (256, 512))]
+    chain = p.plan("chain")
+    assert "hipMemcpyAsync" not in chain
+    outs = _gemm_outputs(chain)
+    assert len(outs) == 2 and outs[0] == outs[1]              # in place
+    reread = p.plan("reread")
+    assert reread.count("hipMemcpyAsync") == 1
+    outs = _gemm_outputs(reread)
+    assert len(outs) == 2 and outs[0] != outs[1]
+    assert "accumulate-into=f32" in p.plan("batch")
+    narrow = p.plan("narrow")
+    assert "accumulate-into=f16" in narrow
+    # f32 matrix-core mode leaves the accumulate form on the exact kernel
+    p.set_f32_gemm(nova_run.F32_GEMM_MFMA)
+    assert "f32=mfma" not in p.plan("arg")
+    assert "f32=mfma" in p.plan("chain")   # the plain nova.matmul in front of it
+    p.set_f32_gemm(nova_run.F32_GEMM_EXACT)
+
+
+def test_linalg_matmul_accumulate_forms_off_the_path():
+    p = nova_run.Program(ACC_PROGRAMS)
+    with pytest.raises(nova_run.NovaRunError, match="16-bit operands accumulating into data-holding"):
+        p.plan("wide16")
+    with pytest.raises(nova_run.NovaRunError, match="uninitialised tensor.empty"):
+        p.plan("uninit")
