@@ -1029,7 +1029,9 @@ struct Planner {
           Step s;
           s.kind = "zero";
           s.out = {dst};
-          s.text = "linalg.fill 0 -> hipMemsetAsync(" + view_str(dst) + ")";
+          s.text = numel_of(dst.shape) * dt_size(dst.dt) % 4 == 0
+                       ? "linalg.fill 0 -> _mlir_ciface_nova_hip_fill_f32(" + view_str(dst) + ", 0)"
+                       : "linalg.fill 0 -> hipMemsetAsync(" + view_str(dst) + ")";
           plan.steps.push_back(s);
         }
       } else if (n == "linalg.matmul" || n == "linalg.batch_matmul") {
@@ -1498,7 +1500,16 @@ int32_t run_step(const Step &s, const std::vector<void *> &ptr, hipStream_t st) 
   if (s.kind == "zero") {
     int64_t n = 1;
     for (int64_t d : s.out[0].shape) n *= d;
-    return hipMemsetAsync(ptr[s.out[0].buf], 0, n * dt_size(s.out[0].dt), st) == hipSuccess
+    // A fill kernel, not hipMemsetAsync: a caller may capture the
+    // execution in a HIP graph, where memset nodes are to be avoided.  Zero
+    // bits are zero in every dtype, so an even byte count of four is filled
+    // as f32 words.
+    const int64_t bytes = n * dt_size(s.out[0].dt);
+    if (bytes % 4 == 0) {
+      NovaMemRef1D d{ptr[s.out[0].buf], ptr[s.out[0].buf], 0, {bytes / 4}, {1}};
+      return _mlir_ciface_nova_hip_fill_f32(&d, 0.0f);
+    }
+    return hipMemsetAsync(ptr[s.out[0].buf], 0, bytes, st) == hipSuccess
                ? NOVA_HIP_SUCCESS
                : fail(NOVA_HIP_EDEVICE, "memset failed");
   }

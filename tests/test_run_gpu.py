@@ -467,3 +467,31 @@ def test_reference_batch_shape_bf16_into_f32_outs(cuda):
     B = S.uniform((4, 256, 64), 100, dtype=S.BF16, offset=A.size)
     (r,) = nova_run.Program(text).run("b", A, B)
     assert_close_lp(r, ref.gemm(A, B, adt=S.BF16, bdt=S.BF16), "03 shape bf16")
+
+
+def test_materialised_zero_fills(cuda):
+    """A zero fill that is read (here: returned) is written on the device: by
+    the fill kernel when its byte count is a multiple of four, else by a
+    memset (the odd bf16 count), over buffers that held other data before."""
+    import torch
+    text = """func.func @z(%x: tensor<3x5xf32>, %y: tensor<3x5xbf16>) -> (tensor<3x5xf32>, tensor<3x5xbf16>, tensor<4x6xbf16>) {
+      %z = arith.constant 0.000000e+00 : f32
+      %zb = arith.constant 0.000000e+00 : bf16
+      %f = linalg.fill ins(%z : f32) outs(%x : tensor<3x5xf32>) -> tensor<3x5xf32>
+      %g = linalg.fill ins(%zb : bf16) outs(%y : tensor<3x5xbf16>) -> tensor<3x5xbf16>
+      %e = tensor.empty() : tensor<4x6xbf16>
+      %h = linalg.fill ins(%zb : bf16) outs(%e : tensor<4x6xbf16>) -> tensor<4x6xbf16>
+      return %f, %g, %h : tensor<3x5xf32>, tensor<3x5xbf16>, tensor<4x6xbf16>
+    }"""
+    p = nova_run.Program(text)
+    plan = p.plan("z")
+    assert plan.count("nova_hip_fill_f32") == 2 and plan.count("hipMemsetAsync") == 1
+    x = torch.full((3, 5), 7.0, device=cuda)
+    y = torch.full((3, 5), 7.0, device=cuda, dtype=torch.bfloat16)
+    res = [torch.full(s, 9.0, device=cuda, dtype=d) for s, d in
+           (((3, 5), torch.float32), ((3, 5), torch.bfloat16), ((4, 6), torch.bfloat16))]
+    out = p.run_device("z", x, y, results=res)
+    torch.cuda.synchronize()
+    for t in out:
+        assert (t.float() == 0).all()
+    assert (x == 7).all() and (y.float() == 7).all()
