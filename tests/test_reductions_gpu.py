@@ -92,8 +92,8 @@ def test_sce_closed_forms_on_gpu(cuda):
 
 
 def test_sce_repeat_calls_identical(cuda):
-    """The last-workgroup mean restores its arrival counter: back-to-back
-    calls (and a smaller second call) give identical, correct results."""
+    """Back-to-back calls (and a smaller second call) give identical,
+    correct results."""
     x = S.normal((300, 777), 42, 0, 2)
     t = S.labels(300, 777, 42, offset=2 * 300 * 777)
     X, T = dev(x, cuda), dev(t, cuda)
@@ -144,6 +144,40 @@ def test_sce_mean_is_the_chunked_order_of_its_row_losses(cuda, rows, C):
     assert torch.equal(lf, loss)
     _, loss_ref, _ = ref.sce(x, t)
     assert_close_f32(loss.cpu().numpy(), loss_ref, f"sce {rows}x{C}")
+
+
+@pytest.mark.parametrize("C,pitch", [(32003, 32004), (50303, 50304), (4099, 4100)])
+def test_sce_row_kernel_labels_in_every_part(cuda, C, pitch):
+    """The on-chip row kernel takes x[label] from where the row sits: a
+    thread's registers, the LDS part past 32768 classes, or thread 0's C % 4
+    tail (rows padded to a 16-byte pitch, so the row kernel runs with
+    C % 4 != 0).  Labels in each part, at their edges, and out of range:
+    loss and fused gradient against the oracle, NaN for the bad label."""
+    import torch
+    labels = [0, 1, 4097, 8191 * 4 + 3, C - 1, C - 3, 4 * (C // 4) - 1, 32768, 40001]
+    labels = [l for l in labels if l < C]
+    rows = len(labels)
+    x = S.normal((rows, C), 49, 0, 2)
+    t = np.array(labels, np.int32)
+    wide = np.zeros((rows, pitch), np.float32)
+    wide[:, :C] = x
+    X = dev(wide, cuda)[:, :C]
+    T = dev(t, cuda)
+    _, loss = nh.sce(X, T)
+    sm_ref, loss_ref, _ = ref.sce(x, t, softmax=True)
+    assert_close_f32(loss.cpu().numpy(), loss_ref, f"sce labels {C}")
+    single = np.array([nh.sce(X[r:r + 1], T[r:r + 1])[1].cpu().numpy()[0] for r in range(rows)])
+    for r in range(rows):
+        _, lr, _ = ref.sce(x[r:r + 1], t[r:r + 1])
+        assert_close_f32(single[r:r + 1], lr, f"row {r} label {labels[r]}")
+    gpad = torch.zeros(rows, pitch, device=cuda)
+    lf, _ = nh.sce_fwd_bwd(X, T, grad=gpad[:, :C])
+    assert torch.equal(lf, loss)
+    assert_close_f32(gpad[:, :C].cpu().numpy(), ref.sce_backward(sm_ref, t), "fused grad")
+    bad = T.clone()
+    bad[1] = C
+    _, lb = nh.sce(X, bad)
+    assert math.isnan(float(lb.cpu()[0]))
 
 
 def test_sce_strided_rows(cuda):
