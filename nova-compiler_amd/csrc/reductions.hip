@@ -330,8 +330,11 @@ __global__ __launch_bounds__(kRowThreads, 4) void sce_row_kernel(SceArgs a) {
   // LDS part: chunk f = 512 NV + tid + 512 j goes to part[tid + 512 j] (a
   // wave's DMA writes 64 consecutive chunks, lane l at l * 16 bytes), issued
   // first; chunks past the row read as zero and are skipped below.
+  // The chunk index's j-dependent part is wave-uniform: the bound and the
+  // DMA's scalar offset carry it, so no per-j vector value stays live (the
+  // compiler had kept nine of them and spilled five to scratch).
   auto in_part = [&](int j) __attribute__((always_inline)) {
-    return kRowThreads * NV + tid + kRowThreads * j < n4;
+    return tid < n4 - kRowThreads * (NV + j);
   };
   if constexpr (NL > 0) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -340,8 +343,8 @@ __global__ __launch_bounds__(kRowThreads, 4) void sce_row_kernel(SceArgs a) {
 #pragma unroll
     for (int j = 0; j < NL; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (lds_void *)(part + wave * 64 + kRowThreads * j), 16,
-          (uint32_t)(kRowThreads * NV + tid + kRowThreads * j) * 16u, 0, 0, 0);
+          rs, (lds_void *)(part + wave * 64 + kRowThreads * j), 16, (uint32_t)tid * 16u,
+          (uint32_t)(kRowThreads * (NV + j)) * 16u, 0, 0);
   }
   f32x4 v[NV];
 #pragma unroll
