@@ -10,7 +10,7 @@
 //
 // 128x128 output tile per 256-thread workgroup (2x2 waves of 64x64, each
 // 2x2 tiles of 32x32), K staged through LDS 32 at a time, register-staged
-// global loads of stage s+1 while stage s is multiplied.  Each MFMA takes
+// global loads two stages ahead of the stage being multiplied.  Each MFMA takes
 // k = 2 values per lane half: lane half h of MFMA j (j = 0..3) of an
 // 8-deep k group holds k = 8g + 4h + j, so a K-contiguous operand's four
 // values for the four MFMAs are one 16-byte LDS read.  An operand whose
@@ -192,19 +192,23 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(F32MArgs a) 
       for (int v = 0; v < 16; ++v) acc[i][jb][v] = init;
   }
 
+  // Global loads run two stages ahead: register set P holds the stage that
+  // goes into LDS buffer P.  Stage s + 2 is loaded into set P (whose stage s
+  // is already in LDS) while stage s is multiplied, and stage s + 1 (set
+  // P ^ 1, loaded a stage earlier) is written to LDS after it, so each load
+  // has two stages' MFMA time to arrive.
+  Stager<AKC, VEC> ga1 = ga;
+  Stager<BKC, VEC> gb1 = gb;
   ga.load(kbeg, kend);
   gb.load(kbeg, kend);
   ga.store(sa[0]);
   gb.store(sb[0]);
+  if (kbeg + kBK < kend) {
+    ga1.load(kbeg + kBK, kend);
+    gb1.load(kbeg + kBK, kend);
+  }
   __syncthreads();
-  int buf = 0;
-  for (int k0 = kbeg; k0 < kend; k0 += kBK) {
-    const bool more = k0 + kBK < kend;
-    if (more) {
-      ga.load(k0 + kBK, kend);
-      gb.load(k0 + kBK, kend);
-    }
-    const float *A = sa[buf], *B = sb[buf];
+  auto multiply = [&](const float *A, const float *B) __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < kBK / 8; ++g) {
       f32x4 fa[2], fb[2];
@@ -221,12 +225,31 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(F32MArgs a) 
             acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][j], fb[jb][j], acc[i][jb],
                                                               0, 0, 0);
     }
-    if (more) {
-      ga.store(sa[buf ^ 1]);
-      gb.store(sb[buf ^ 1]);
+  };
+  for (int k0 = kbeg; k0 < kend; k0 += 2 * kBK) {
+    // stage k0: LDS buffer 0, register set 0 / 1 for stages k0 + 2 / k0 + 1
+    if (k0 + 2 * kBK < kend) {
+      ga.load(k0 + 2 * kBK, kend);
+      gb.load(k0 + 2 * kBK, kend);
+    }
+    multiply(sa[0], sb[0]);
+    if (k0 + kBK < kend) {
+      ga1.store(sa[1]);
+      gb1.store(sb[1]);
     }
     __syncthreads();
-    buf ^= 1;
+    if (k0 + kBK >= kend) break;
+    // stage k0 + 1: LDS buffer 1, register sets swapped
+    if (k0 + 3 * kBK < kend) {
+      ga1.load(k0 + 3 * kBK, kend);
+      gb1.load(k0 + 3 * kBK, kend);
+    }
+    multiply(sa[1], sb[1]);
+    if (k0 + 2 * kBK < kend) {
+      ga.store(sa[0]);
+      gb.store(sb[0]);
+    }
+    __syncthreads();
   }
 
   // Accumulator element v of lane l: row 8 (v / 4) + 4 h + v % 4, column l % 32
