@@ -56,7 +56,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (cpu_baseline becomes null)")
     ap.add_argument("--telemetry", action="store_true",
-                    help="also run config 2 (this library and hipBLASLt) and an MFMA-only probe "
+                    help="also run config 2 (this library and hipBLASLt), config 3 and an MFMA-only probe "
                          "back to back for --telemetry-seconds each while sampling board power "
                          "and clocks with amd-smi (reported under 'telemetry')")
     ap.add_argument("--telemetry-seconds", type=float, default=6.0)
@@ -587,7 +587,8 @@ class PowerSampler:
 def telemetry(args, torch, nh, S):
     """Board power and graphics clock (amd-smi) while each workload runs
     back to back for args.telemetry_seconds: config 2 on this library's
-    kernel, on hipBLASLt (torch.bmm), and a loop of nothing but bf16 MFMAs
+    kernel, on hipBLASLt (torch.bmm), config 3 on this library's kernel, and
+    a loop of nothing but bf16 MFMAs
     (nova-compiler_amd/libnova_probe.so, no memory traffic).  The MFMA busy
     fraction follows as TFLOP/s / (peak x clock / 2.4 GHz)."""
     import ctypes
@@ -630,6 +631,18 @@ def telemetry(args, torch, nh, S):
     out["c2_hipblaslt"] = drive(lambda: torch.bmm(A, B, out_dtype=torch.float32, out=C), C2_FLOP)
     del A, B, C
     torch.cuda.empty_cache()
+    inp = S.config_inputs("c3")
+    x = to_dev(inp["x"], S.BF16, torch)
+    W = to_dev(inp["W"], S.BF16, torch)
+    b = to_dev(inp["bias"], S.BF16, torch)
+    del inp
+    y = torch.empty(4096, 11008, device="cuda", dtype=torch.bfloat16)
+    d3 = [nh.memref_of(t) for t in (x, W.t(), b, y)]
+    r3 = [nh.ref(v) for v in d3]
+    f3 = nh.lib()._mlir_ciface_nova_hip_linear_bf16_bias_gelu
+    out["c3_gemm_pers_kernel"] = drive(lambda: f3(*r3), C3_FLOP)
+    del x, W, b, y, d3, r3
+    torch.cuda.empty_cache()
     probe = ctypes.CDLL(os.path.join(REPO, "nova-compiler_amd", "libnova_probe.so"))
     probe.nova_probe_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_void_p, ctypes.POINTER(ctypes.c_double)]
@@ -646,6 +659,18 @@ def telemetry(args, torch, nh, S):
     mfma()
     torch.cuda.synchronize()
     out["mfma_only_probe"] = drive(mfma, flop.value)
+    probe.nova_probe_mfma_loop16.argtypes = probe.nova_probe_mfma_loop.argtypes
+    flop16 = ctypes.c_double(0.0)
+
+    def mfma16():
+        rc = probe.nova_probe_mfma_loop16(ctypes.c_void_p(buf.data_ptr()), 256, 20000, stream,
+                                          ctypes.byref(flop16))
+        if rc:
+            raise RuntimeError(f"probe launch failed: {rc}")
+
+    mfma16()
+    torch.cuda.synchronize()
+    out["mfma_only_probe_16x16x32"] = drive(mfma16, flop16.value)
     out["note"] = ("amd-smi socket power and mean XCD graphics clock, medians over the samples; "
                    "mfma_busy_at_clock = TFLOP/s / (2516.6 x clock / 2400 MHz)")
     return out
