@@ -20,7 +20,9 @@
 // A K-contiguous A with 16-byte aligned rows and K a multiple of 16 (up to
 // 64) is not staged: each computing wave loads its A fragments straight from
 // memory before the B staging starts (config 4a: 10.4 -> 9.7 us, same bits).
-// Eight waves stage.  In a 64-row window four of them, in a 2x2 grid, then
+// Eight waves stage (sixteen in a workgroup alone on its CU, so that the
+// chunks go out in half the rounds: configs 4a / 4b 8.90 -> 8.62 /
+// 7.75 -> 7.36 us, the same bits).  In a 64-row window four of them, in a 2x2 grid, then
 // each own 32 rows x NT/2 columns as NT/64 tiles of v_mfma_f32_32x32x16; in
 // a 128-row window all eight do, in a 4x2 grid.  The MFMA loops are
 // specialised per operand layout and read the next fragments from LDS while
@@ -42,8 +44,10 @@ constexpr int kMaxNT = 256;
 constexpr int kLdsBytes = 80 * 1024;    // staging budget per workgroup (two fit a CU)
 constexpr int kCuLdsBytes = 160 * 1024;  // a CU's LDS, for a workgroup alone on its CU
 // Staging runs on eight waves, the MFMAs and the epilogue on the first four
-// (2x2 grid): staging is the long, latency-bound part.
+// (2x2 grid): staging is the long, latency-bound part.  A workgroup alone on
+// its CU stages on sixteen (kWideThreads); waves 8-15 only stage.
 constexpr int kStageThreads = 512;
+constexpr int kWideThreads = 1024;
 // Chunks staged per thread per round, for A and for B (two loads each).
 constexpr int kBatchA = 4, kBatchB = 4;
 
@@ -58,6 +62,7 @@ struct SmallArgs {
   int nt;          // output columns per workgroup
   int a_direct;    // A fragments loaded from memory, A not staged
   int nt_store;    // f32 output in whole 128-byte lines: nontemporal stores
+  int threads;     // staging threads: kStageThreads, or kWideThreads when alone on a CU
   int buf_store;   // f32 output whose batch slice fits 31-bit byte offsets: buffer stores
 };
 
@@ -155,9 +160,9 @@ __device__ __forceinline__ void chunk_store(const Lines &l, char *lds, int q, in
 // kBatchB of B per thread (two loads each) before their LDS writes, so the
 // latencies overlap.  (A and B get loops of their own: a resource chosen per
 // lane would leave the wave-uniform registers.)
+template <int T>
 __device__ __forceinline__ void stage(const Lines &la, const Lines &lb, char *lds_a, char *lds_b,
                                       int tid) {
-  constexpr int T = kStageThreads;
   const int na = la.nalloc * la.ncpl, nb = lb.nalloc * lb.ncpl;
   for (int r = 0; r * T * kBatchA < na || r * T * kBatchB < nb; ++r) {
     Raw va[kBatchA], vb[kBatchB];
@@ -305,8 +310,8 @@ __device__ __forceinline__ void mfma_direct_store(f32x16 (&acc)[1][TNW], const u
   }
 }
 
-template <int DT, int TNW, bool AD, bool NT>
-__global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) {
+template <int DT, int TNW, bool AD, bool NT, int ST>
+__global__ __launch_bounds__(ST) void gemm_small_kernel(SmallArgs s) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const GemmArgs &a = s.g;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -366,10 +371,11 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
       if (computes && kk * 16 < s.kp)
         fad[kk] = __builtin_amdgcn_raw_buffer_load_b128(ra, rowoff + 32u * kk, 0, 0);
   }
-  stage(la, lb, lds_a, lds_b, tid);
+  stage<ST>(la, lb, lds_a, lds_b, tid);
   __syncthreads();
-  // 64-row windows: waves 0-3 compute (2x2); 128-row windows: all eight
-  // (4x2), a wave past the window's valid rows stops here.
+  // 64-row windows: waves 0-3 compute (2x2); 128-row windows: waves 0-7
+  // (4x2), a wave past the window's valid rows stops here (waves 8-15 of a
+  // wide workgroup, whose wm >= 4, always do).
   if (s.bm == 64 && wave >= 4) return;
   if (wm * 32 >= m_valid) return;
 
@@ -413,13 +419,13 @@ __global__ __launch_bounds__(kStageThreads) void gemm_small_kernel(SmallArgs s) 
     store_outputs<1, TNW, NT>(acc, ge, bidx, m0 + wm * 32, n0 + nw, lane);
 }
 
-template <int DT>
-int32_t launch_dt(const SmallArgs &s, size_t lds, hipStream_t st) {
-  const dim3 grid((unsigned)(s.g.batch * s.g.tiles_m * s.g.tiles_n)), block(kStageThreads);
+template <int DT, int ST>
+int32_t launch_st(const SmallArgs &s, size_t lds, hipStream_t st) {
+  const dim3 grid((unsigned)(s.g.batch * s.g.tiles_m * s.g.tiles_n)), block(ST);
   switch ((s.a_direct ? 8 : 0) + (s.nt_store ? 4 : 0) + s.nt / 64 - 1) {
-#define NOVA_SMALL(AD, NT, T)                                                        \
-  case (AD ? 8 : 0) + (NT ? 4 : 0) + T - 1:                                         \
-    hipLaunchKernelGGL((gemm_small_kernel<DT, T, AD, NT>), grid, block, lds, st, s); \
+#define NOVA_SMALL(AD, NT, T)                                                            \
+  case (AD ? 8 : 0) + (NT ? 4 : 0) + T - 1:                                             \
+    hipLaunchKernelGGL((gemm_small_kernel<DT, T, AD, NT, ST>), grid, block, lds, st, s); \
     break;
     NOVA_SMALL(false, false, 1) NOVA_SMALL(false, false, 2)
     NOVA_SMALL(false, false, 3) NOVA_SMALL(false, false, 4)
@@ -433,6 +439,12 @@ int32_t launch_dt(const SmallArgs &s, size_t lds, hipStream_t st) {
     default: break;
   }
   return check_hip(hipGetLastError(), "gemm_small launch");
+}
+
+template <int DT>
+int32_t launch_dt(const SmallArgs &s, size_t lds, hipStream_t st) {
+  return s.threads == kWideThreads ? launch_st<DT, kWideThreads>(s, lds, st)
+                                   : launch_st<DT, kStageThreads>(s, lds, st);
 }
 
 // Staging geometry chosen on the host: output columns per workgroup, K
@@ -476,6 +488,7 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
   s.g = a_in;
   SmallPlan p = plan_small(a_in.N, a_in.K, akc, bkc);
   s.bm = kBM;
+  s.threads = kStageThreads;
   // 128-row windows (eight computing waves) when they still fit the staging
   // budget and cut the workgroups a CU must run: each wave's share of the
   // work is the same, so the time follows the most loaded CU.  Config 4a:
@@ -494,6 +507,9 @@ int32_t launch_gemm_small(const gemm::GemmArgs &a_in, int in_dt, bool akc, bool 
     if (p2.lds <= budget && (t128 + cus - 1) / cus < (t64 + cus - 1) / cus) {
       p = p2;
       s.bm = 2 * kBM;
+      // No more workgroups than CUs: each runs alone and stages on sixteen
+      // waves (the CU's 64 wave slots hold them at up to 128 VGPRs).
+      if (t128 <= cus) s.threads = kWideThreads;
     }
   }
   // A read straight into MFMA fragments: K-contiguous, every row 16-byte

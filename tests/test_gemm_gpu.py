@@ -516,12 +516,16 @@ def test_gemm_small_epilogues(cuda, epi, odt, shape):
 
 @pytest.mark.parametrize("dt", [S.F16, S.BF16])
 @pytest.mark.parametrize("shape", [(2, 197, 197, 64), (5, 100, 131, 32), (1, 37, 301, 16),
-                                   (3, 260, 77, 48), (2, 129, 255, 64)])
+                                   (3, 260, 77, 48), (2, 129, 255, 64), (96, 197, 197, 64),
+                                   (100, 150, 50, 32)])
 def test_gemm_small_direct_a_exact(cuda, dt, shape):
     """The small-K kernel with A read straight into MFMA fragments (K-
     contiguous A with 16-byte aligned rows, K a multiple of 16 up to 64; B
     with unaligned N-contiguous rows is staged): 64- and 128-row windows,
-    M off the 32-row blocks, N past one 256-column tile.  Integer-valued
+    M off the 32-row blocks, N past one 256-column tile.  The last two
+    shapes make more 64-row tiles than CUs but no more 128-row ones, so each
+    workgroup is alone on its CU and stages on sixteen waves (config 4a's
+    form), eight of which only stage.  Integer-valued
     inputs make every product and sum exact, so the output must equal the
     oracle's exactly."""
     import torch
@@ -543,7 +547,8 @@ def test_gemm_small_128_row_windows_exact(cuda, dt, layout, shape):
     """The small-K kernel in 128-row windows with A staged: more 64-row tiles
     than CUs, so the 128-row form (eight computing waves) is chosen, and at
     K = 197 its staging (up to ~106 KB with A transposed) only fits because
-    each workgroup has a CU to itself.  Integer-valued inputs make every
+    each workgroup has a CU to itself; such a workgroup stages on sixteen
+    waves.  Integer-valued inputs make every
     product and sum exact, so every layout must equal the oracle exactly."""
     batch, M, N, K = shape
     g = np.random.default_rng(73)
