@@ -48,8 +48,11 @@ constexpr int kCuLdsBytes = 160 * 1024;  // a CU's LDS, for a workgroup alone on
 // its CU stages on sixteen (kWideThreads); waves 8-15 only stage.
 constexpr int kStageThreads = 512;
 constexpr int kWideThreads = 1024;
-// Chunks staged per thread per round, for A and for B (two loads each).
-constexpr int kBatchA = 4, kBatchB = 4;
+// Chunks staged per thread per round, for A and for B (two loads each).  A
+// wide workgroup whose A is read directly stages B alone, whose at most
+// ~2,100 chunks (K <= 64) two per thread cover: four would issue loads past
+// the end (config 4a: 8.63 -> 8.38 us, the same bits).
+constexpr int kBatchA = 4, kBatchB = 4, kBatchBWide = 2;
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
@@ -160,21 +163,24 @@ __device__ __forceinline__ void chunk_store(const Lines &l, char *lds, int q, in
 // kBatchB of B per thread (two loads each) before their LDS writes, so the
 // latencies overlap.  (A and B get loops of their own: a resource chosen per
 // lane would leave the wave-uniform registers.)
-template <int T>
+// SA: A is staged (otherwise B alone is).
+template <int T, bool SA>
 __device__ __forceinline__ void stage(const Lines &la, const Lines &lb, char *lds_a, char *lds_b,
                                       int tid) {
-  const int na = la.nalloc * la.ncpl, nb = lb.nalloc * lb.ncpl;
-  for (int r = 0; r * T * kBatchA < na || r * T * kBatchB < nb; ++r) {
-    Raw va[kBatchA], vb[kBatchB];
-    const int qa = tid + r * T * kBatchA, qb = tid + r * T * kBatchB;
+  constexpr int BA = SA ? kBatchA : 0;
+  constexpr int BB = !SA && T == kWideThreads ? kBatchBWide : kBatchB;
+  const int na = SA ? la.nalloc * la.ncpl : 0, nb = lb.nalloc * lb.ncpl;
+  for (int r = 0; r * T * BA < na || r * T * BB < nb; ++r) {
+    Raw va[SA ? BA : 1], vb[BB];
+    const int qa = tid + r * T * BA, qb = tid + r * T * BB;
 #pragma unroll
-    for (int u = 0; u < kBatchA; ++u) va[u] = chunk_load(la, qa + u * T, na);
+    for (int u = 0; u < BA; ++u) va[u] = chunk_load(la, qa + u * T, na);
 #pragma unroll
-    for (int u = 0; u < kBatchB; ++u) vb[u] = chunk_load(lb, qb + u * T, nb);
+    for (int u = 0; u < BB; ++u) vb[u] = chunk_load(lb, qb + u * T, nb);
 #pragma unroll
-    for (int u = 0; u < kBatchA; ++u) chunk_store(la, lds_a, qa + u * T, na, va[u]);
+    for (int u = 0; u < BA; ++u) chunk_store(la, lds_a, qa + u * T, na, va[u]);
 #pragma unroll
-    for (int u = 0; u < kBatchB; ++u) chunk_store(lb, lds_b, qb + u * T, nb, vb[u]);
+    for (int u = 0; u < BB; ++u) chunk_store(lb, lds_b, qb + u * T, nb, vb[u]);
   }
 }
 
@@ -371,7 +377,7 @@ __global__ __launch_bounds__(ST) void gemm_small_kernel(SmallArgs s) {
       if (computes && kk * 16 < s.kp)
         fad[kk] = __builtin_amdgcn_raw_buffer_load_b128(ra, rowoff + 32u * kk, 0, 0);
   }
-  stage<ST>(la, lb, lds_a, lds_b, tid);
+  stage<ST, !AD>(la, lb, lds_a, lds_b, tid);
   __syncthreads();
   // 64-row windows: waves 0-3 compute (2x2); 128-row windows: waves 0-7
   // (4x2), a wave past the window's valid rows stops here (waves 8-15 of a
