@@ -256,7 +256,6 @@ __device__ __forceinline__ void mfma_staged(f32x16 (&acc)[1][TNW], const char *l
   u32x4 fb[TNW];
 #pragma unroll
   for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, pb, BKC, nw + 32 * j, 0, lane);
-#pragma unroll 2
   for (int kk = 0; kk < ksteps; ++kk) {
     // The last step reads its own fragments again: in bounds, unused.
     const int kn = kk + 1 < ksteps ? kk + 1 : kk;
