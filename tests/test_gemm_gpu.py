@@ -486,15 +486,16 @@ def test_persistent_nn_epilogue(cuda, epi, odt):
 @pytest.mark.parametrize("epi,odt", [(nh.EPI_BIAS_GELU, "bf16"), (nh.EPI_BIAS, "f16"),
                                      (nh.EPI_GELU, "f32"), (nh.EPI_BIAS_GELU, "f32")])
 @pytest.mark.parametrize("shape", [(3, 197, 197, 64), (2, 70, 61, 197), (1, 33, 257, 40),
-                                   (2, 70, 64, 197), (96, 197, 64, 197)])
+                                   (2, 70, 64, 197), (96, 197, 64, 197), (96, 197, 197, 64)])
 def test_gemm_small_epilogues(cuda, epi, odt, shape):
     """The small-K staged kernel (rows not 16-byte aligned) with bias / GELU
     epilogues and every output dtype: odd N puts a partial quad of four
     columns at the row end (element stores), and 16-bit rows of odd length
     leave some quads without 4-byte alignment.  N = 64 with f32 output
     writes whole 128-byte lines (the nontemporal-store form).  96 batches of
-    197 rows make more 64-row tiles than CUs, so the last shape runs in
-    128-row windows with A staged (config 4b's form)."""
+    197 rows make more 64-row tiles than CUs, so the last two shapes run in
+    128-row windows, one workgroup per CU staging on sixteen waves: A staged
+    (config 4b's form) and A read directly (config 4a's form)."""
     import torch
     cdt, tdt = {"bf16": (S.BF16, torch.bfloat16), "f16": (S.F16, torch.float16),
                 "f32": (S.F32, torch.float32)}[odt]
