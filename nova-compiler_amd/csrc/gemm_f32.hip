@@ -417,6 +417,123 @@ __global__ __launch_bounds__(256) void gemm_exact_vec_kernel(F32Args a, uint32_t
   }
 }
 
+// The tiny form, for problems whose vector-form tiles leave CUs idle (config
+// 1, 256^3: the 64x32 form's 32 tiles occupy 32 of 256 CUs, each thread
+// running eight 256-long chains): a 16x16 tile per 256-thread workgroup,
+// one output per thread.  Per stage of KS k each thread loads KS / 64 float4
+// of A and of B along their unit-stride dims; LDS holds A as [m][k] and B
+// as [n][k] (KS + 4 floats apart: the 16 columns a wave reads fall on 64
+// distinct banks), so a thread reads four k of its row and of its column
+// with two 16-byte reads.  The arithmetic per output is the other forms'.
+// Stages of 128 k (in-process A/B, us, stages of 64 / 128 / 256): 256^3
+// 4.88 / 4.75 / 4.50, 512^3 12.84 / 12.42 / 13.95 (256-deep stages leave
+// two workgroups per CU), 64x64x1024 13.4 / 12.1 / 11.2; the 64x32 form
+// took 14.1, 25.7 and 47.9.
+constexpr int kTinyKs = 128;
+
+template <bool AKC, bool BKC>
+__global__ __launch_bounds__(256) void gemm_exact_tiny_kernel(F32Args a, uint32_t a_bytes,
+                                                               uint32_t b_bytes) {
+#pragma clang fp contract(off)
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int KS = kTinyKs, P = KS + 4;
+  constexpr int E = KS / 64;  // float4 of each operand per thread per stage
+  static_assert(KS % 64 == 0, "a stage is a whole number of float4 per thread");
+  __shared__ __attribute__((aligned(16))) float sa[2][kVt * P];
+  __shared__ __attribute__((aligned(16))) float sb[2][kVt * P];
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x / tiles;
+  const int t = blockIdx.x - b * tiles;
+  const int m0 = (t / a.tiles_n) * kVt, n0 = (t % a.tiles_n) * kVt;
+  const int tid = threadIdx.x, tx = tid % kVt, ty = tid / kVt;
+  const int64_t sa_outer = AKC ? a.sam : a.sak;
+  const int64_t sb_outer = BKC ? a.sbn : a.sbk;
+  const __amdgpu_buffer_rsrc_t ra = f32_rsrc(static_cast<const float *>(a.A) + b * a.sab, a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = f32_rsrc(static_cast<const float *>(a.B) + b * a.sbb, b_bytes);
+  // float4 q = tid + 256 e of a stage: K-contiguous, row q / (KS / 4) and
+  // k 4 (q % (KS / 4)); otherwise k q / 4 and rows 4 (q % 4) .. + 3.  Rows
+  // past M / N read neighbouring data or zero (their outputs are not
+  // stored); k past K is never multiplied.
+  auto row_of = [&](int q) __attribute__((always_inline)) { return q / (KS / 4); };
+  auto k4_of = [&](int q) __attribute__((always_inline)) { return (q % (KS / 4)) * 4; };
+  auto ld4 = [&](const __amdgpu_buffer_rsrc_t &r, int64_t e) __attribute__((always_inline)) {
+    return __builtin_bit_cast(f32x4,
+                              __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(e * 4), 0, 0));
+  };
+  f32x4 ga[E], gb[E];
+  auto gload = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int q = tid + 256 * e;
+      ga[e] = ld4(ra, AKC ? (int64_t)(m0 + row_of(q)) * sa_outer + k0 + k4_of(q)
+                          : (int64_t)(k0 + q / 4) * sa_outer + m0 + (q % 4) * 4);
+      gb[e] = ld4(rb, BKC ? (int64_t)(n0 + row_of(q)) * sb_outer + k0 + k4_of(q)
+                          : (int64_t)(k0 + q / 4) * sb_outer + n0 + (q % 4) * 4);
+    }
+  };
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int q = tid + 256 * e;
+      if (AKC) {
+        *reinterpret_cast<f32x4 *>(&sa[buf][row_of(q) * P + k4_of(q)]) = ga[e];
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sa[buf][((q % 4) * 4 + u) * P + q / 4] = ga[e][u];
+      }
+      if (BKC) {
+        *reinterpret_cast<f32x4 *>(&sb[buf][row_of(q) * P + k4_of(q)]) = gb[e];
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sb[buf][((q % 4) * 4 + u) * P + q / 4] = gb[e][u];
+      }
+    }
+  };
+  const int m = m0 + ty, n = n0 + tx;
+  const bool has_bias = (a.epi == NOVA_HIP_EPI_BIAS || a.epi == NOVA_HIP_EPI_BIAS_GELU);
+  const bool has_gelu = (a.epi == NOVA_HIP_EPI_BIAS_GELU || a.epi == NOVA_HIP_EPI_GELU);
+  float acc = (has_bias && n < a.N) ? bias_value(a.bias, a.bias_dt, n) : 0.0f;
+  // linalg.matmul on data-holding outs: the sum starts from C's value.
+  if (a.acc_c && m < a.M && n < a.N)
+    acc = static_cast<const float *>(a.C)[(int64_t)b * a.scb + (int64_t)m * a.scm + n];
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = 0; k0 < a.K; k0 += KS) {
+    const bool more = k0 + KS < a.K;
+    if (more) gload(k0 + KS);
+    const float *ar = &sa[buf][ty * P], *br = &sb[buf][tx * P];
+    if (a.K - k0 >= KS) {
+#pragma unroll 4
+      for (int kq = 0; kq < KS / 4; ++kq) {
+        const f32x4 av = *reinterpret_cast<const f32x4 *>(ar + 4 * kq);
+        const f32x4 bv = *reinterpret_cast<const f32x4 *>(br + 4 * kq);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float p = av[u] * bv[u];
+          acc = acc + p;
+        }
+      }
+    } else {
+      // The last, partial stage: only its real k (a padded k would add
+      // 0 * b, which turns a -0 sum into +0 and an infinite b into NaN).
+      for (int kk = 0; kk < a.K - k0; ++kk) {
+        const float p = ar[kk] * br[kk];
+        acc = acc + p;
+      }
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  if (m < a.M && n < a.N) {
+    float v = acc;
+    if (has_gelu) v = gelu_ref(v);
+    static_cast<float *>(a.C)[(int64_t)b * a.scb + (int64_t)m * a.scm + n] = v;
+  }
+}
+
 // The vector forms: rows and columns per thread, k per stage, and the
 // relative rate of one CU running two or more of its workgroups (measured on
 // the GPT step's shapes: 55, 52, 51 and ~44 TFLOP/s when every CU holds
@@ -429,6 +546,20 @@ struct VecForm {
 constexpr VecForm kVecForms[] = {{8, 8, 16, 1.0}, {4, 8, 16, 0.95}, {4, 6, 32, 0.93},
                                  {4, 4, 64, 0.8}, {4, 2, 64, 0.6}};
 constexpr int kNumVecForms = sizeof(kVecForms) / sizeof(kVecForms[0]);
+constexpr double kTinyRate = 0.5;
+
+template <bool AKC, bool BKC>
+void launch_tiny_t(const F32Args &a, uint32_t ab, uint32_t bb, unsigned grid, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_exact_tiny_kernel<AKC, BKC>), dim3(grid), dim3(256), 0, s, a, ab, bb);
+}
+
+void launch_tiny(const F32Args &a, bool akc, bool bkc, uint32_t ab, uint32_t bb, unsigned grid,
+                 hipStream_t s) {
+  if (akc && bkc) launch_tiny_t<true, true>(a, ab, bb, grid, s);
+  else if (akc) launch_tiny_t<true, false>(a, ab, bb, grid, s);
+  else if (bkc) launch_tiny_t<false, true>(a, ab, bb, grid, s);
+  else launch_tiny_t<false, false>(a, ab, bb, grid, s);
+}
 
 template <int RM, int CN, int KS>
 void launch_vec(const F32Args &a, bool akc, bool bkc, uint32_t ab, uint32_t bb, unsigned grid,
@@ -510,6 +641,20 @@ int32_t launch_gemm_exact(const GemmProblem &p, hipStream_t s) {
           best = f;
           best_cost = cost;
           best_tiles = tiles;
+        }
+      }
+      // The tiny form, only where the smallest vector form's tiles leave
+      // CUs idle; its tiles are costed like the others' at rate 0.5.
+      const int64_t small_tiles = p.batch * ((p.M + 63) / 64) * ((p.N + 31) / 32);
+      const int64_t tiny_tiles = p.batch * ((p.M + kVt - 1) / kVt) * ((p.N + kVt - 1) / kVt);
+      if (small_tiles < cus && tiny_tiles <= 0x7fffffff) {
+        const int64_t waves = (tiny_tiles + 2 * (int64_t)cus - 1) / (2 * (int64_t)cus);
+        if ((double)waves * (kVt * kVt) / kTinyRate < best_cost) {
+          a.tiles_m = (int)((p.M + kVt - 1) / kVt);
+          a.tiles_n = (int)((p.N + kVt - 1) / kVt);
+          launch_tiny(a, p.a_kcontig, p.b_kcontig, (uint32_t)(a_ext * 4), (uint32_t)(b_ext * 4),
+                      (unsigned)tiny_tiles, s);
+          return check_hip(hipGetLastError(), "gemm_exact launch");
         }
       }
       if (best >= 0) {

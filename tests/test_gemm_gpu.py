@@ -226,7 +226,8 @@ VEC_FORMS = [(8, 8, 1.0), (4, 8, 0.95), (4, 6, 0.93), (4, 4, 0.8), (4, 2, 0.6)]
 
 def vec_form(batch, M, N, cus):
     """The form the library picks: least (waves of two tiles per CU) x tile
-    area / rate."""
+    area / rate; the 16x16 tiny form (index 5, rate 0.5) only when the 64x32
+    form's tiles are fewer than the CUs."""
     best, best_cost = None, None
     for f, (rm, cn, rate) in enumerate(VEC_FORMS):
         tm, tn = 16 * rm, 16 * cn
@@ -234,14 +235,18 @@ def vec_form(batch, M, N, cus):
         cost = -(-tiles // (2 * cus)) * tm * tn / rate
         if best is None or cost < best_cost:
             best, best_cost = f, cost
+    if batch * -(-M // 64) * -(-N // 32) < cus:
+        tiny = batch * -(-M // 16) * -(-N // 16)
+        if -(-tiny // (2 * cus)) * 256 / 0.5 < best_cost:
+            return 5
     return best
 
 
 # One problem per form (on a 256-CU part), M and N off the tile edges, K
-# ending in a partial stage (stages of 16, 16, 32, 64 and 64 k).
+# ending in a partial stage (stages of 16, 16, 32, 64, 64 and 128 k).
 VEC_CASES = [(0, (1, 2044, 4092, 37)), (1, (1, 2044, 2044, 70)), (2, (1, 1020, 3070, 101)),
-             (3, (1, 1000, 1100, 130)), (4, (2, 500, 777, 130))]
-VEC_IDS = ["128x128", "64x128", "64x96", "64x64", "64x32"]
+             (3, (1, 1000, 1100, 130)), (4, (2, 500, 777, 130)), (5, (3, 100, 200, 200))]
+VEC_IDS = ["128x128", "64x128", "64x96", "64x64", "64x32", "16x16"]
 
 
 def _vec_case(cuda, form, shape):
@@ -257,7 +262,7 @@ def _vec_case(cuda, form, shape):
 @pytest.mark.parametrize("form,shape", VEC_CASES, ids=VEC_IDS)
 def test_f32_gemm_vector_forms_bit_exact(cuda, layout, bias_dt, form, shape):
     """The exact f32 GEMM's vector forms (aligned rows; 128x128, 64x128, 64x96,
-    64x64 and 64x32 tiles) against the oracle's sequential arithmetic, bit for bit,
+    64x64, 64x32 and 16x16 tiles) against the oracle's sequential arithmetic, bit for bit,
     on 65,536 sampled outputs and the corners, in all four layouts, with no
     bias, an f32 bias and a bf16 bias."""
     import torch
