@@ -62,7 +62,8 @@ def parse():
     ap.add_argument("--telemetry-seconds", type=float, default=6.0)
     ap.add_argument("--only", default="",
                     help="comma list of configs to run (c2,c3,c4,ln,sce,sce_bwd,sce_fwd_bwd,ln_bwd,"
-                         "c3_bwd,c2_vendor,gpt_step; copy = HBM copy calibration)")
+                         "c3_bwd,c2_vendor,gpt_step; copy = HBM copy calibration); the HBM "
+                         "copy ceiling runs whenever a reduction config does")
     return ap.parse_args()
 
 
@@ -401,6 +402,34 @@ def bench_copy(args, torch):
         ys[i % 3].copy_(xs[i % 3])
 
     ms = time_launches(fn, args.steps * 2, args.warmup, torch)
+    gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+    return {"ms": ms, "bytes": 2 * n * 4, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
+
+
+def bench_copy_ceiling(args, torch):
+    """The practical HBM read+write ceiling on this box: the fastest copy
+    form (nova-compiler_amd/libnova_probe.so nova_probe_copy: one 16-byte
+    element per thread, nontemporal) over 256 MiB, three rotated buffer
+    sets.  The reductions' GB/s are also given as a fraction of it
+    (frac_copy_ceiling), beside their fraction of the 8 TB/s peak."""
+    import ctypes
+    probe = ctypes.CDLL(os.path.join(REPO, "nova-compiler_amd", "libnova_probe.so"))
+    probe.nova_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                      ctypes.c_void_p]
+    n = 64 * 1024 * 1024
+    xs = [torch.empty(n, device="cuda").fill_(1.0) for _ in range(3)]
+    ys = [torch.empty(n, device="cuda") for _ in range(3)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fn(i):
+        rc = probe.nova_probe_copy(ctypes.c_void_p(xs[i % 3].data_ptr()),
+                                   ctypes.c_void_p(ys[i % 3].data_ptr()), n * 4, stream)
+        if rc:
+            raise RuntimeError(f"nova_probe_copy failed: {rc}")
+
+    ms = time_launches(fn, args.steps * 2, args.warmup, torch)
+    if not torch.equal(ys[0], xs[0]):
+        raise RuntimeError("nova_probe_copy: the copy differs from its source")
     gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
     return {"ms": ms, "bytes": 2 * n * 4, "gbs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
 
@@ -748,6 +777,12 @@ def main():
         cfg["c2_vendor_hipblaslt_reference"] = stage("c2_vendor", lambda: bench_c2_vendor(args, torch, S))
     if "copy" in only:  # calibration only; not part of the default run
         cfg["hbm_copy_256MiB"] = stage("copy", lambda: bench_copy(args, torch))
+    if only & {"ln", "sce", "sce_bwd", "sce_fwd_bwd", "ln_bwd", "copy"}:
+        ceil = stage("copy_ceiling", lambda: bench_copy_ceiling(args, torch))
+        cfg["hbm_copy_ceiling_256MiB"] = ceil
+        for key, r in cfg.items():
+            if key.startswith("c5_") and isinstance(r, dict) and "gbs" in r:
+                r["frac_copy_ceiling"] = r["gbs"] / ceil["gbs"]
 
     tele = stage("telemetry", lambda: telemetry(args, torch, nh, S)) if args.telemetry else None
 
