@@ -19,7 +19,7 @@
 // (NovaGPUNestedLayoutDistributionPatterns.cpp:2460); this kernel does not,
 // because tf32 breaks 1e-4 parity.
 //
-// Two families, with the same per-output arithmetic (so the same bits):
+// Three families, with the same per-output arithmetic (so the same bits):
 //   * 64x64 output tile per 256-thread workgroup, 4x4 outputs per thread,
 //     K staged through LDS 16 at a time, element loads: any strides, every
 //     dtype;
@@ -27,7 +27,9 @@
 //     and 64x32 tiles (8x8, 4x8, 4x6, 4x4 and 4x2 outputs per thread), 16-byte global
 //     loads along each operand's unit-stride dim, LDS stages [k][m] / [k][n]
 //     read with 16-byte reads; the tile is chosen per problem so that the
-//     CUs stay busy.
+//     CUs stay busy;
+//   * the same operands, problems too small for those tiles to fill the
+//     CUs: 16x16 tiles, one output per thread.
 // Without contraction every multiply-add is two VALU operations, so the
 // ceiling is half the f32 FMA rate.
 #include <hip/hip_runtime.h>
