@@ -700,6 +700,27 @@ def telemetry(args, torch, nh, S):
     mfma16()
     torch.cuda.synchronize()
     out["mfma_only_probe_16x16x32"] = drive(mfma16, flop16.value)
+    # The GEMM's per-K-step work from an L2-resident source, its operands
+    # staged into LDS by LDS-DMA or by loads into registers plus ds_write.
+    probe.nova_probe_stage.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.POINTER(ctypes.c_double)]
+    probe.nova_probe_stage_src_bytes.restype = ctypes.c_int64
+    nsrc = probe.nova_probe_stage_src_bytes() // 2
+    src = torch.randn(nsrc, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).cuda()
+    for name, dma in (("lds_dma", 1), ("registers_ds_write", 0)):
+        fl = ctypes.c_double(0.0)
+
+        def staged(dma=dma, fl=fl):
+            rc = probe.nova_probe_stage(ctypes.c_void_p(src.data_ptr()),
+                                        ctypes.c_void_p(buf.data_ptr()), 256, 2000, dma,
+                                        stream, ctypes.byref(fl))
+            if rc:
+                raise RuntimeError(f"probe launch failed: {rc}")
+
+        staged()
+        torch.cuda.synchronize()
+        out[f"staging_probe_{name}"] = drive(staged, fl.value)
     out["note"] = ("amd-smi socket power and mean XCD graphics clock, medians over the samples; "
                    "mfma_busy_at_clock = TFLOP/s / (2516.6 x clock / 2400 MHz)")
     return out
