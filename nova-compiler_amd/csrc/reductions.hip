@@ -501,18 +501,55 @@ __global__ __launch_bounds__(64) void sce_mean_kernel(const float *row_loss, int
   const int per = (rows + 63) / 64;
   const int start = threadIdx.x * per;
   const int end = min(start + per, rows);
-  // The chunk's loads go out 64 at a time (a whole chunk of up to 4096
-  // rows) and are summed in order (a load-add loop waited out one memory
-  // latency per row: ~9 us at 4096 rows).
+  // A chunk's rows go out 64 at a time (a whole chunk of up to 64 rows
+  // at once) and are summed in order (a load-add loop waited out one
+  // memory latency per row: ~9 us at 4096 rows).  With the losses 16-byte
+  // aligned the chunk is read as up to three single rows up to a 16-byte
+  // boundary, float4 loads, and up to three single rows at the end: four
+  // times fewer load instructions (forward / fused, the same bits:
+  // 4096 x 32000 80.6 -> 78.8 / 185.3 -> 184.0 us, 8192 x 50304 243.2 ->
+  // 239.8 / 600.5 -> 598.0 us, 100000 x 64 87.1 -> 52.6 us).
   constexpr int kBatch = 64;
   float p = 0.0f;
-  for (int b0 = start; b0 < end; b0 += kBatch) {
-    float v[kBatch];
+  if ((reinterpret_cast<uintptr_t>(row_loss) & 15u) == 0) {
+    const int a0 = min(end, (start + 3) & ~3);  // first 16-byte boundary
+    const int a1 = max(a0, end & ~3);           // last one
+    const f32x4 *r4 = reinterpret_cast<const f32x4 *>(row_loss);
+    float hd[3], tl[3];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) v[u] = b0 + u < end ? row_loss[b0 + u] : 0.0f;
+    for (int e = 0; e < 3; ++e) {
+      hd[e] = start + e < a0 ? row_loss[start + e] : 0.0f;
+      tl[e] = a1 + e < end ? row_loss[a1 + e] : 0.0f;
+    }
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (b0 + u < end) p = p + v[u];
+    for (int e = 0; e < 3; ++e)
+      if (start + e < a0) p = p + hd[e];
+    for (int b0 = a0; b0 < a1; b0 += kBatch) {
+      f32x4 v[kBatch / 4];
+#pragma unroll
+      for (int u = 0; u < kBatch / 4; ++u)
+        if (b0 + 4 * u < a1) v[u] = r4[(b0 >> 2) + u];
+#pragma unroll
+      for (int u = 0; u < kBatch / 4; ++u)
+        if (b0 + 4 * u < a1) {
+          p = p + v[u].x;
+          p = p + v[u].y;
+          p = p + v[u].z;
+          p = p + v[u].w;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 3; ++e)
+      if (a1 + e < end) p = p + tl[e];
+  } else {
+    for (int b0 = start; b0 < end; b0 += kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = b0 + u < end ? row_loss[b0 + u] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (b0 + u < end) p = p + v[u];
+    }
   }
   part[threadIdx.x] = p;
   __syncthreads();
