@@ -834,6 +834,47 @@ def test_small_k_output_rows_far_apart(cuda):
     assert bool((big[:, N:N + 4096] == 7.0).all())
 
 
+def _wide_small_cases(n=12, seed=2026):
+    """Seeded shapes for the small-K kernel's sixteen-wave form: 197 rows,
+    odd K or N (16-bit rows not 16-byte aligned), and a batch that makes
+    more 64-row tiles than a 256-CU part has CUs but no more 128-row ones."""
+    g = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        i = len(cases)
+        dt = [S.F16, S.BF16][(i // 3) % 2]
+        if i % 3 == 0:
+            # K-contiguous A with 16-byte aligned rows, K a multiple of 16
+            # up to 64: A read directly; B's N-contiguous rows of odd N keep
+            # the small-K kernel.
+            K = 16 * int(g.integers(1, 5))
+            N = int(g.integers(1, 129)) | 1
+            layout = "NN"
+        else:
+            K = int(g.integers(1, 161)) | 1
+            N = int(g.integers(1, 257))
+            layout = ["NN", "NT", "TN", "TT"][i % 4]
+        batch = int(g.integers(65, 129))
+        cases.append((batch, 197, N, K, layout, dt))
+    return cases
+
+
+@pytest.mark.parametrize("case", _wide_small_cases())
+def test_gemm_small_sixteen_wave_random_exact(cuda, case):
+    """The small-K kernel when each workgroup has a CU to itself (128-row
+    windows, sixteen staging waves; A staged or, for K-contiguous aligned A,
+    read directly): random shapes and layouts from a fixed seed.  Integer-
+    valued inputs make every product and sum exact, so the output must equal
+    the oracle's exactly."""
+    batch, M, N, K, layout, dt = case
+    g = np.random.default_rng(batch * 100003 + N * 311 + K)
+    a = S.round_to(g.integers(-4, 5, (batch, M, K)).astype(np.float32), dt)
+    b = S.round_to(g.integers(-4, 5, (batch, K, N)).astype(np.float32), dt)
+    got = nh.gemm(view_as(a, layout[0], cuda, dt), view_as(b, layout[1], cuda, dt)).cpu().numpy()
+    want = ref.gemm(a, b, adt=dt, bdt=dt)
+    assert np.array_equal(got, want), case
+
+
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
 @pytest.mark.parametrize("shape", [(1, 100, 200, 300), (1, 256, 512, 128), (1, 128, 128, 128),
                                    (2, 37, 45, 23), (3, 65, 70, 129), (4, 64, 64, 256)])
