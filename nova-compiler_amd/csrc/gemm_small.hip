@@ -244,30 +244,44 @@ __device__ __forceinline__ void store_f32_buf(const f32x16 (&acc)[1][TNW], const
   for (int j = 0; j < TNW; ++j) store_f32_blk<NT>(acc[0][j], a, bidx, mw, nw + 32 * j, lane);
 }
 
-// MFMA phase of a window whose A is staged: the fragments of k16 step kk+1
-// are read from LDS while step kk multiplies.  The layouts are template
-// parameters, so the loop has no branches around its LDS reads (with the
-// layouts as runtime values every step waited for its own reads).
+// MFMA phase of a window whose A is staged: the fragments of the next k16
+// steps are read from LDS while step kk multiplies, D - 1 steps ahead in a
+// ring of D fragment sets (the loop unrolled by D keeps the ring's indices
+// constant).  D = 3 for up to two 32-column blocks per wave (config 4b:
+// 7.37 -> 7.28 us, the same bits; four sets ran 7.88), 2 for more, whose
+// third set would not fit the 128 VGPRs of a sixteen-wave workgroup.  The
+// layouts are template parameters, so the loop has no branches around its
+// LDS reads (with the layouts as runtime values every step waited for its
+// own reads).
 template <int DT, int TNW, bool AKC, bool BKC>
 __device__ __forceinline__ void mfma_staged(f32x16 (&acc)[1][TNW], const char *lds_a, int pa,
                                             const char *lds_b, int pb, int row0, int nw,
                                             int ksteps, int lane) {
-  u32x4 fa = read_frag(lds_a, pa, AKC, row0, 0, lane);
-  u32x4 fb[TNW];
+  constexpr int D = TNW <= 2 ? 3 : 2;
+  u32x4 fa[D], fb[D][TNW];
 #pragma unroll
-  for (int j = 0; j < TNW; ++j) fb[j] = read_frag(lds_b, pb, BKC, nw + 32 * j, 0, lane);
-  for (int kk = 0; kk < ksteps; ++kk) {
-    // The last step reads its own fragments again: in bounds, unused.
-    const int kn = kk + 1 < ksteps ? kk + 1 : kk;
-    const u32x4 na = read_frag(lds_a, pa, AKC, row0, kn, lane);
-    u32x4 nb[TNW];
+  for (int d = 0; d < D - 1; ++d) {
+    const int ks = d < ksteps ? d : ksteps - 1;
+    fa[d] = read_frag(lds_a, pa, AKC, row0, ks, lane);
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) nb[j] = read_frag(lds_b, pb, BKC, nw + 32 * j, kn, lane);
+    for (int j = 0; j < TNW; ++j) fb[d][j] = read_frag(lds_b, pb, BKC, nw + 32 * j, ks, lane);
+  }
+  for (int k0 = 0; k0 < ksteps; k0 += D) {
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa, fb[j], acc[0][j]);
-    fa = na;
+    for (int d = 0; d < D; ++d) {
+      const int kk = k0 + d;
+      if (kk < ksteps) {
+        // D - 1 steps ahead; past the end the last step is read again (in
+        // bounds, unused).
+        const int kr = kk + D - 1 < ksteps ? kk + D - 1 : ksteps - 1;
+        const int w = (d + D - 1) % D;
+        fa[w] = read_frag(lds_a, pa, AKC, row0, kr, lane);
 #pragma unroll
-    for (int j = 0; j < TNW; ++j) fb[j] = nb[j];
+        for (int j = 0; j < TNW; ++j) fb[w][j] = read_frag(lds_b, pb, BKC, nw + 32 * j, kr, lane);
+#pragma unroll
+        for (int j = 0; j < TNW; ++j) acc[0][j] = mfma_32x32x16<DT>(fa[d], fb[d][j], acc[0][j]);
+      }
+    }
   }
 }
 
