@@ -413,7 +413,10 @@ def bench_copy_ceiling(args, torch):
     sets.  The reductions' GB/s are also given as a fraction of it
     (frac_copy_ceiling), beside their fraction of the 8 TB/s peak."""
     import ctypes
-    probe = ctypes.CDLL(os.path.join(REPO, "nova-compiler_amd", "libnova_probe.so"))
+    try:
+        probe = ctypes.CDLL(os.path.join(REPO, "nova-compiler_amd", "libnova_probe.so"))
+    except OSError as e:  # the probe library is a measurement aid, not the op path
+        return {"error": f"libnova_probe.so not loaded: {e}"[:200]}
     probe.nova_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
                                       ctypes.c_void_p]
     n = 64 * 1024 * 1024
@@ -802,7 +805,7 @@ def main():
         ceil = stage("copy_ceiling", lambda: bench_copy_ceiling(args, torch))
         cfg["hbm_copy_ceiling_256MiB"] = ceil
         for key, r in cfg.items():
-            if key.startswith("c5_") and isinstance(r, dict) and "gbs" in r:
+            if key.startswith("c5_") and isinstance(r, dict) and "gbs" in r and "gbs" in ceil:
                 r["frac_copy_ceiling"] = r["gbs"] / ceil["gbs"]
 
     tele = stage("telemetry", lambda: telemetry(args, torch, nh, S)) if args.telemetry else None
