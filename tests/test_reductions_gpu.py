@@ -120,14 +120,16 @@ def _chunk_mean_f32(v):
     return np.float32(total / np.float32(R))
 
 
-@pytest.mark.parametrize("rows,C", [(5, 2052), (1000, 2052), (4173, 2052), (64, 32000)])
+@pytest.mark.parametrize("rows,C", [(5, 2052), (1000, 2052), (4173, 2052), (4288, 2052),
+                                    (64, 32000)])
 def test_sce_mean_is_the_chunked_order_of_its_row_losses(cuda, rows, C):
     """Each row's loss, taken from a one-row call (whose mean is the row loss
     itself), summed on the host in the reference's 64-chunk order, gives the
     batched call's loss bit for bit: the device mean keeps that order
-    exactly, for chunks of one row, 16 and 66 rows (more than one wave's
-    worth) and 64 chunks of one row each.  The fused forward+backward gives
-    the same loss bits."""
+    exactly, for chunks of one row, 16, 66 and 67 rows (more than one
+    float4 batch; chunk starts 0-3 rows off a 16-byte boundary, so every
+    length of the single-row head and tail) and 64 chunks of one row each.
+    The fused forward+backward gives the same loss bits."""
     import torch
     x = S.normal((rows, C), 47, 0, 2)
     t = S.labels(rows, C, 47, offset=rows * C)
