@@ -646,6 +646,9 @@ def telemetry(args, torch, nh, S):
         ms = e0.elapsed_time(e1) / n
         r = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "calls": n}
         r.update(ps.summary())
+        # One line per workload: the stage runs for minutes in all.
+        print(f"[bench] telemetry: {r['tflops']:.1f} TFLOP/s, {r.get('samples', 0)} samples",
+              file=sys.stderr, flush=True)
         if r.get("gfx_clock_mhz_median"):
             r["mfma_busy_at_clock"] = r["tflops"] / (PEAK_BF16_TFLOPS * r["gfx_clock_mhz_median"]
                                                      / 2400.0)
@@ -711,7 +714,7 @@ def telemetry(args, torch, nh, S):
     probe.nova_probe_stage_src_bytes.restype = ctypes.c_int64
     nsrc = probe.nova_probe_stage_src_bytes() // 2
     src = torch.randn(nsrc, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).cuda()
-    for name, dma in (("lds_dma", 1), ("registers_ds_write", 0)):
+    for name, dma in (("lds_dma", 1), ("registers_ds_write", 0), ("lds_dma_transposing_b", 2)):
         fl = ctypes.c_double(0.0)
 
         def staged(dma=dma, fl=fl):
