@@ -664,7 +664,13 @@ def telemetry(args, torch, nh, S):
     nh._bind_stream()
     out["c2_gemm_pers_kernel"] = drive(lambda: f_(*d), C2_FLOP)
     out["c2_hipblaslt"] = drive(lambda: torch.bmm(A, B, out_dtype=torch.float32, out=C), C2_FLOP)
-    del A, B, C
+    # The same product with B stored K-contiguous (a transposed copy, passed
+    # as a view): the kernel reads B's fragments with plain 16-byte LDS reads
+    # instead of transposing ones; everything else is unchanged.
+    Bt = B.transpose(1, 2).contiguous()
+    dt = [nh.ref(nh.memref_of(t)) for t in (A, Bt.transpose(1, 2), C)]
+    out["c2_gemm_pers_kernel_b_k_contiguous"] = drive(lambda: f_(*dt), C2_FLOP)
+    del A, B, Bt, C
     torch.cuda.empty_cache()
     inp = S.config_inputs("c3")
     x = to_dev(inp["x"], S.BF16, torch)
