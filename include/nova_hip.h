@@ -70,7 +70,11 @@ typedef struct NovaMemRef4D {
   int64_t strides[4];
 } NovaMemRef4D;
 
-/* Status codes. */
+/* Status codes.  Every entry point checks all of its descriptors before it
+ * launches anything, so a call that returns 1-4 has written nothing.  A
+ * call with two or three outputs (linear_backward, matmul_backward) may
+ * return 5-7 from a later output's launch after an earlier output has
+ * been written. */
 enum {
   NOVA_HIP_SUCCESS = 0,
   NOVA_HIP_EINVAL = 1,    /* null descriptor / data pointer, bad flag bits  */

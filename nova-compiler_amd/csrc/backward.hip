@@ -726,10 +726,17 @@ int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_
                          ws + part_floats, s);
 }
 
+bool col_sum_in_range(int64_t rows, int64_t cols) {
+  // A row chunk's end (chunk start + chunk, chunks up to 2^16 rows) and a
+  // thread's first column (up to 8 per thread past the last) stay in int.
+  return rows <= 0x7fffffff - (1 << 20) && cols <= 0x7fffffff - (1 << 20);
+}
+
 int32_t launch_col_sum(const ColSumProblem &p, hipStream_t s) {
   if (p.cols == 0) return NOVA_HIP_SUCCESS;
-  if (p.rows > 0x7fffffff || p.cols > 0x7fffffff - 256)
-    return fail(NOVA_HIP_ERANGE, "column sum: size exceeds 2^31-1");
+  if (!col_sum_in_range(p.rows, p.cols))
+    return fail(NOVA_HIP_ERANGE, "column sum: [%lld, %lld] exceeds 2^31 - 2^20",
+                (long long)p.rows, (long long)p.cols);
   // Row chunks of 64 (at most 65535 of them).
   int64_t chunk = 64;
   while ((p.rows + chunk - 1) / chunk > 65535) chunk *= 2;

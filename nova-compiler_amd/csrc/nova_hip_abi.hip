@@ -151,9 +151,11 @@ int decode_flags(int32_t flags, int &in_dt, int &out_dt, int &epi, int &bias_dt)
   return NOVA_HIP_SUCCESS;
 }
 
-// Validate and normalise a batched GEMM given 3-D views.
+// Validate and normalise a batched GEMM given 3-D views, then launch it
+// (with launch false: validate only, so that an entry point with several
+// outputs can check them all before it writes any).
 int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
-                  const NovaMemRef1D *bias, int32_t flags) {
+                  const NovaMemRef1D *bias, int32_t flags, bool launch = true) {
   clear_error();
   if (!A || !B || !C) return fail(NOVA_HIP_EINVAL, "gemm: null descriptor");
   int in_dt, out_dt, epi, bias_dt;
@@ -242,7 +244,7 @@ int32_t gemm_core(const NovaMemRef3D *A, const NovaMemRef3D *B, NovaMemRef3D *C,
   p.scm = C->strides[1];
   if (p.sab < 0 || p.sbb < 0 || p.scb < 0)
     return fail(NOVA_HIP_ESTRIDE, "gemm: negative batch stride");
-  if (empty) return NOVA_HIP_SUCCESS;
+  if (empty || !launch) return NOVA_HIP_SUCCESS;
 
   hipStream_t s = current_stream();
   if (p.f32_mfma) {
@@ -269,13 +271,13 @@ NovaMemRef3D lift(const NovaMemRef2D *d) {
 }
 
 int32_t gemm2d(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C,
-               const NovaMemRef1D *bias, int32_t flags) {
+               const NovaMemRef1D *bias, int32_t flags, bool launch = true) {
   if (!A || !B || !C) {
     clear_error();
     return fail(NOVA_HIP_EINVAL, "gemm: null descriptor");
   }
   NovaMemRef3D a = lift(A), b = lift(B), c = lift(C);
-  return gemm_core(&a, &b, &c, bias, flags);
+  return gemm_core(&a, &b, &c, bias, flags, launch);
 }
 
 NovaMemRef2D transposed(const NovaMemRef2D *d) {
@@ -290,12 +292,13 @@ NovaMemRef2D transposed(const NovaMemRef2D *d) {
 // C = A . B into C as laid out: row-major C directly; a transposed view of
 // a row-major buffer (unit stride on dim 0) as C^T = B^T . A^T into that
 // buffer, since the kernels store rows with unit stride.
-int32_t gemm2d_to(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C, int32_t flags) {
+int32_t gemm2d_to(const NovaMemRef2D *A, const NovaMemRef2D *B, NovaMemRef2D *C, int32_t flags,
+                  bool launch = true) {
   if (C && C->strides[1] != 1 && C->sizes[1] > 1 && (C->strides[0] == 1 || C->sizes[0] <= 1)) {
     NovaMemRef2D at = transposed(A), bt = transposed(B), ct = transposed(C);
-    return gemm2d(&bt, &at, &ct, nullptr, flags);
+    return gemm2d(&bt, &at, &ct, nullptr, flags, launch);
   }
-  return gemm2d(A, B, C, nullptr, flags);
+  return gemm2d(A, B, C, nullptr, flags, launch);
 }
 
 // Flags of the backward GEMM entry points: dtypes only, no epilogue.
@@ -578,16 +581,13 @@ int32_t _mlir_ciface_nova_hip_linear_backward(const NovaMemRef2D *grad_out, cons
                 w, (long long)M, (long long)K, (long long)weight->sizes[0], (long long)N,
                 (long long)grad_out->sizes[0], (long long)grad_out->sizes[1]);
   // grad_input [M,K] = grad_out . weight^T  (NovaToLinalgGeneric.cpp:1867-1911)
-  if (grad_input) {
-    NovaMemRef2D wt = transposed(weight);
-    if ((rc = gemm2d_to(grad_out, &wt, grad_input, flags))) return rc;
-  }
   // grad_weight [K,N] = x^T . grad_out  (:1913-1968)
-  if (grad_weight) {
-    NovaMemRef2D xt = transposed(x);
-    if ((rc = gemm2d_to(&xt, grad_out, grad_weight, flags))) return rc;
-  }
   // grad_bias [N] = column sums of grad_out  (:1970-1989)
+  // Every requested output is validated before the first launch, so a call
+  // that fails writes nothing.
+  NovaMemRef2D wt = transposed(weight), xt = transposed(x);
+  if (grad_input && (rc = gemm2d_to(grad_out, &wt, grad_input, flags, false))) return rc;
+  if (grad_weight && (rc = gemm2d_to(&xt, grad_out, grad_weight, flags, false))) return rc;
   if (grad_bias) {
     clear_error();
     if (grad_bias->sizes[0] != N) return fail(NOVA_HIP_ESHAPE, "%s: grad_bias size != N", w);
@@ -598,6 +598,13 @@ int32_t _mlir_ciface_nova_hip_linear_backward(const NovaMemRef2D *grad_out, cons
     if (M > 1 && grad_out->strides[0] < N) return fail(NOVA_HIP_ESTRIDE, "%s: grad_out rows overlap", w);
     if (N > 0 && (!grad_bias->aligned || (M > 0 && !grad_out->aligned)))
       return fail(NOVA_HIP_EINVAL, "%s: null data pointer", w);
+    if (!col_sum_in_range(M, N))
+      return fail(NOVA_HIP_ERANGE, "%s: grad_bias of [%lld, %lld] exceeds the column sum's range",
+                  w, (long long)M, (long long)N);
+  }
+  if (grad_input && (rc = gemm2d_to(grad_out, &wt, grad_input, flags))) return rc;
+  if (grad_weight && (rc = gemm2d_to(&xt, grad_out, grad_weight, flags))) return rc;
+  if (grad_bias) {
     ColSumProblem p;
     p.in = data_of(grad_out) + grad_out->offset * dtype_size(in_dt);
     p.out = const_cast<char *>(data_of(grad_bias)) + grad_bias->offset * dtype_size(out_dt);
@@ -626,15 +633,13 @@ int32_t _mlir_ciface_nova_hip_matmul_backward(const NovaMemRef2D *grad, const No
                 (long long)M, (long long)K, (long long)B->sizes[0], (long long)N,
                 (long long)grad->sizes[0], (long long)grad->sizes[1]);
   // grad_a [M,K] = grad . B^T; grad_b [K,N] = A^T . grad
-  // (NovaMatmulBackwardPattern, NovaToLinalgGeneric.cpp:160-239)
-  if (grad_a) {
-    NovaMemRef2D bt = transposed(B);
-    if ((rc = gemm2d_to(grad, &bt, grad_a, flags))) return rc;
-  }
-  if (grad_b) {
-    NovaMemRef2D at = transposed(A);
-    if ((rc = gemm2d_to(&at, grad, grad_b, flags))) return rc;
-  }
+  // (NovaMatmulBackwardPattern, NovaToLinalgGeneric.cpp:160-239), both
+  // validated before either is launched.
+  NovaMemRef2D bt = transposed(B), at = transposed(A);
+  if (grad_a && (rc = gemm2d_to(grad, &bt, grad_a, flags, false))) return rc;
+  if (grad_b && (rc = gemm2d_to(&at, grad, grad_b, flags, false))) return rc;
+  if (grad_a && (rc = gemm2d_to(grad, &bt, grad_a, flags))) return rc;
+  if (grad_b && (rc = gemm2d_to(&at, grad, grad_b, flags))) return rc;
   return NOVA_HIP_SUCCESS;
 }
 

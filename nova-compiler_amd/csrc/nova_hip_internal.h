@@ -116,6 +116,9 @@ struct ColSumProblem {
   int in_dt, out_dt;
 };
 int32_t launch_col_sum(const ColSumProblem &p, hipStream_t s);
+// Whether launch_col_sum takes [rows, cols] (its row chunks and column
+// groups index with 32-bit ints and run up to 2^20 past the extents).
+bool col_sum_in_range(int64_t rows, int64_t cols);
 
 // ---- program glue (glue.hip) -------------------------------------------------
 // c = a (op) b over a [4]-shaped index space; strides in elements, 0 on a

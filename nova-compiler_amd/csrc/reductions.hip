@@ -566,8 +566,11 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int32_t launch_layer_norm(const LayerNormProblem &p, hipStream_t s) {
   if (p.rows == 0) return NOVA_HIP_SUCCESS;
-  if (p.rows > 0x7fffffff - kWaves || p.D > 0x7fffffff)
-    return fail(NOVA_HIP_ERANGE, "layer_norm: size exceeds 2^31-1");
+  // The persistent kernels' row blocks end up to a grid's worth (2048) of
+  // rows past the last: rows stay below 2^31 - 2^20 so that this stays in int.
+  if (p.rows > 0x7fffffff - (1 << 20) || p.D > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "layer_norm: %lld rows exceed 2^31 - 2^20 or D exceeds 2^31-1",
+                (long long)p.rows);
   LnArgs a;
   a.x = p.x;
   a.gamma = p.gamma;
@@ -698,8 +701,11 @@ int32_t scratch_of_device(float **out) {
 }  // namespace
 
 int32_t launch_sce(const SceProblem &p, hipStream_t s) {
-  if (p.rows > 0x7fffffff - kWaves || p.C > 0x7fffffff)
-    return fail(NOVA_HIP_ERANGE, "sce: size exceeds 2^31-1");
+  // The mean's 64 chunks of ceil(rows / 64) end up to 63 rows past the
+  // last, its batches of 64 up to 63 more: rows stay below 2^31 - 2^20.
+  if (p.rows > 0x7fffffff - (1 << 20) || p.C > 0x7fffffff)
+    return fail(NOVA_HIP_ERANGE, "sce: %lld rows exceed 2^31 - 2^20 or C exceeds 2^31-1",
+                (long long)p.rows);
   // Workspace: the per-row losses.
   float *ws = static_cast<float *>(workspace(s, (size_t)p.rows * 4 + 4));
   if (!ws) return NOVA_HIP_ENOMEM;

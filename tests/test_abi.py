@@ -208,6 +208,23 @@ def test_sce_noalloc_validation_and_row_limit():
     assert "scratch maximum of 262144" in last_error()
 
 
+# One past the row limit of the row kernels and the column sum: their
+# in-kernel row arithmetic is 32-bit and runs up to a grid's worth of rows
+# past the last row.
+ROWS_OVER = 0x7fffffff - (1 << 20) + 1
+
+
+def test_row_limits_are_checked_before_any_launch():
+    assert sce_rc(d2((ROWS_OVER, 1)), d1(ROWS_OVER), d1(1)) == 5
+    assert "rows exceed 2^31 - 2^20" in last_error()
+    L = nh.lib()
+    assert L._mlir_ciface_nova_hip_sce_fwd_bwd_f32(
+        nh.ref(d2((ROWS_OVER, 1))), nh.ref(d1(ROWS_OVER)), nh.ref(d1(1)),
+        nh.ref(d2((ROWS_OVER, 1)))) == 5
+    assert ln_rc(d2((ROWS_OVER, 4)), d1(4), d1(4), d2((ROWS_OVER, 4))) == 5
+    assert "rows exceed 2^31 - 2^20" in last_error()
+
+
 def test_error_text_is_per_call():
     assert gemm_rc(d3((2, 8, 16)), d3((2, 15, 8)), d3((2, 8, 8))) == 2
     assert last_error()
@@ -289,6 +306,16 @@ def test_linear_backward_validation():
     assert f(d2((8, 16), (1, 8)), x, w, gb=d1(16)) == 3  # column sums need unit stride on N
     # empty batch: both GEMMs are no-ops, and no bias gradient asked for
     assert f(d2((0, 16)), d2((0, 32)), w, gi=d2((0, 32))) == 0
+    # Every output is validated before the first launch: with both GEMM
+    # outputs given, a malformed grad_weight or grad_bias still fails
+    # validation (a launch, with no GPU here, would give a HIP error).
+    gi, gw = d2((8, 32)), d2((32, 16))
+    assert f(go, x, w, gi=gi, gw=gw, gb=d1(15)) == 2
+    assert f(go, x, w, gi=gi, gw=d2((32, 15))) == 2
+    assert f(go, x, w, gi=gi, gw=gw, gb=d1(16, ptr=0)) == 1
+    assert f(d2((ROWS_OVER, 16)), d2((ROWS_OVER, 32)), w, gi=d2((ROWS_OVER, 32)),
+             gb=d1(16)) == 5
+    assert "column sum" in last_error()
 
 
 def test_matmul_backward_validation():
@@ -306,6 +333,8 @@ def test_matmul_backward_validation():
     assert f(g, A, B, flags=nh.gemm_flags(nh.DT_F32, nh.DT_BF16)) == 4
     assert f(g, A, B, flags=nh.gemm_flags(nh.DT_F32, nh.DT_F32, nh.EPI_GELU)) == 1
     assert f(g, A, B, ga=d2((8, 31))) == 2
+    # both outputs validated before either GEMM is launched
+    assert f(g, A, B, ga=d2((8, 32)), gb=d2((32, 15))) == 2
 
 
 def d4(sizes, strides=None, ptr=FAKE):
