@@ -691,7 +691,8 @@ int32_t launch_layer_norm_backward(const LayerNormBackwardProblem &p, hipStream_
   const int ng = (grid + kGroup - 1) / kGroup;
   const size_t part_floats = (size_t)grid * 2 * p.D;
   const size_t ws_floats = part_floats + (size_t)(ng + 1) * 2 * p.D;
-  float *ws = static_cast<float *>(workspace(s, ws_floats * 4));
+  WorkspaceLease lease(s, ws_floats * 4);  // held until the column sums are enqueued
+  float *ws = static_cast<float *>(lease.get());
   if (!ws) return NOVA_HIP_ENOMEM;
   LnBwdArgs a;
   a.gy = p.gy;
@@ -743,7 +744,8 @@ int32_t launch_col_sum(const ColSumProblem &p, hipStream_t s) {
   const int nch = (int)((p.rows + chunk - 1) / chunk > 0 ? (p.rows + chunk - 1) / chunk : 1);
   const int ng = (nch + kGroup - 1) / kGroup;
   const size_t part_floats = (size_t)nch * p.cols;
-  float *ws = static_cast<float *>(workspace(s, (part_floats + (size_t)(ng + 1) * p.cols) * 4));
+  WorkspaceLease lease(s, (part_floats + (size_t)(ng + 1) * p.cols) * 4);
+  float *ws = static_cast<float *>(lease.get());
   if (!ws) return NOVA_HIP_ENOMEM;
   const int esz = p.in_dt == NOVA_HIP_DT_F32 ? 4 : 2;
   const int V = 16 / esz;

@@ -376,8 +376,9 @@ int32_t launch_gemm_f32_mfma(const GemmProblem &p, hipStream_t s) {
   if (splits < 1) splits = 1;
   a.splits = splits;
   const int64_t per_split = p.batch * p.M * p.N;
+  WorkspaceLease lease;  // the partials, held until their reduction is enqueued
   if (splits > 1) {
-    a.part = static_cast<float *>(workspace(s, (size_t)(splits * per_split) * 4));
+    a.part = static_cast<float *>(lease.acquire(s, (size_t)(splits * per_split) * 4));
     if (!a.part) return NOVA_HIP_ENOMEM;
   }
   const int64_t grid = tiles * splits;

@@ -9,7 +9,9 @@
 
 #include <atomic>
 #include <mutex>
+#include <memory>
 #include <unordered_map>
+#include <vector>
 
 #include "nova_hip_internal.h"
 
@@ -25,6 +27,19 @@ struct Workspace {
 };
 std::mutex g_ws_mu;
 std::unordered_map<hipStream_t, Workspace> g_ws;
+
+// One enqueue mutex per stream, never erased (a later stream with a
+// recycled handle shares it, which only serialises more).  Lock order: a
+// stream's mutex, then g_ws_mu.
+std::mutex g_stream_mu_mu;
+std::unordered_map<hipStream_t, std::unique_ptr<std::mutex>> g_stream_mu;
+
+std::mutex &stream_mutex(hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_stream_mu_mu);
+  std::unique_ptr<std::mutex> &m = g_stream_mu[s];
+  if (!m) m.reset(new std::mutex);
+  return *m;
+}
 }  // namespace
 
 int32_t fail(int32_t code, const char *fmt, ...) {
@@ -71,7 +86,10 @@ int32_t check_hip(hipError_t e, const char *what) {
   return fail(NOVA_HIP_EDEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
-void *workspace(hipStream_t s, size_t bytes) {
+namespace {
+// The stream's buffer, grown to at least `bytes`; the caller holds the
+// stream's mutex.
+void *workspace_locked(hipStream_t s, size_t bytes) {
   std::lock_guard<std::mutex> lock(g_ws_mu);
   Workspace &w = g_ws[s];
   if (w.bytes >= bytes && w.ptr) return w.ptr;
@@ -96,6 +114,13 @@ void *workspace(hipStream_t s, size_t bytes) {
   w.ptr = p;
   w.bytes = want;
   return p;
+}
+}  // namespace
+
+void *WorkspaceLease::acquire(hipStream_t s, size_t bytes) {
+  lock_ = std::unique_lock<std::mutex>(stream_mutex(s));
+  ptr_ = workspace_locked(s, bytes);
+  return ptr_;
 }
 
 namespace {
@@ -918,16 +943,26 @@ const char *nova_hip_version(void) { return "libnova_hip 0.1.0 (gfx950)"; }
 
 int32_t nova_hip_release_workspace(void) {
   clear_error();
-  std::lock_guard<std::mutex> lock(g_ws_mu);
+  std::vector<hipStream_t> streams;
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    for (auto &kv : g_ws) streams.push_back(kv.first);
+  }
   int32_t rc = NOVA_HIP_SUCCESS;
-  for (auto &kv : g_ws) {
-    if (kv.second.ptr) {
-      hipError_t e = hipStreamSynchronize(kv.first);
-      if (e == hipSuccess) e = hipFree(kv.second.ptr);
+  // Each stream's buffer is freed under that stream's mutex: a call that
+  // holds the buffer finishes its launches first.
+  for (hipStream_t st : streams) {
+    std::lock_guard<std::mutex> stream_lock(stream_mutex(st));
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_ws.find(st);
+    if (it == g_ws.end()) continue;
+    if (it->second.ptr) {
+      hipError_t e = hipStreamSynchronize(st);
+      if (e == hipSuccess) e = hipFree(it->second.ptr);
       if (e != hipSuccess) rc = check_hip(e, "release_workspace");
     }
+    g_ws.erase(it);
   }
-  g_ws.clear();
   return rc;
 }
 

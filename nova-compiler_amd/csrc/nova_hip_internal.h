@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/nova_hip.h"
 
 namespace nova_hip {
@@ -171,9 +173,27 @@ struct ReduceSumProblem {
 };
 int32_t launch_reduce_sum(const ReduceSumProblem &p, hipStream_t s);
 
-// Per-stream device workspace owned by the library.  Returns null and sets
-// the error text on failure.  The pointer stays valid until the next call
-// with a larger size on the same stream, or nova_hip_release_workspace().
-void *workspace(hipStream_t s, size_t bytes);
+// The per-stream device workspace owned by the library, held for one
+// call's launches.  acquire() locks the stream's enqueue mutex until the
+// lease ends, then returns the stream's buffer grown to at least `bytes`
+// (null, with the error text set, when the allocation fails).  Calls made
+// on one stream from several threads (every thread that has set no stream
+// shares the null stream) therefore enqueue their kernels one call at a
+// time: no call's kernels read another call's partials, and the buffer is
+// not regrown or released while a call still has launches to make with it.
+// A lease must not be acquired on a stream whose lease the thread holds.
+class WorkspaceLease {
+ public:
+  WorkspaceLease() = default;
+  WorkspaceLease(hipStream_t s, size_t bytes) { acquire(s, bytes); }
+  WorkspaceLease(const WorkspaceLease &) = delete;
+  WorkspaceLease &operator=(const WorkspaceLease &) = delete;
+  void *acquire(hipStream_t s, size_t bytes);
+  void *get() const { return ptr_; }
+
+ private:
+  std::unique_lock<std::mutex> lock_;
+  void *ptr_ = nullptr;
+};
 
 }  // namespace nova_hip

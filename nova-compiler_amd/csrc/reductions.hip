@@ -706,8 +706,9 @@ int32_t launch_sce(const SceProblem &p, hipStream_t s) {
   if (p.rows > 0x7fffffff - (1 << 20) || p.C > 0x7fffffff)
     return fail(NOVA_HIP_ERANGE, "sce: %lld rows exceed 2^31 - 2^20 or C exceeds 2^31-1",
                 (long long)p.rows);
-  // Workspace: the per-row losses.
-  float *ws = static_cast<float *>(workspace(s, (size_t)p.rows * 4 + 4));
+  // Workspace: the per-row losses, held until the mean is enqueued.
+  WorkspaceLease lease(s, (size_t)p.rows * 4 + 4);
+  float *ws = static_cast<float *>(lease.get());
   if (!ws) return NOVA_HIP_ENOMEM;
   return launch_sce_into(p, ws, s);
 }

@@ -1,7 +1,8 @@
-"""Concurrent calls from several host threads, each on a stream of its own:
-the calling thread's stream (nova_hip_set_stream is thread-local) and the
-per-stream workspace (SCE row losses, LayerNorm-backward partials, split-K
-partials of the f32 matrix-core GEMM) keep the calls apart, and every
+"""Concurrent calls from several host threads, each on a stream of its own
+or all on one: the calling thread's stream (nova_hip_set_stream is
+thread-local) and the per-stream workspace (SCE row losses,
+LayerNorm-backward partials, split-K partials of the f32 matrix-core GEMM),
+held per call under the stream's lease, keep the calls apart, and every
 result equals the same call made alone on one stream, bit for bit."""
 import threading
 
@@ -68,3 +69,42 @@ def test_threads_on_own_streams_match_single_stream(cuda):
     for i in range(len(inputs)):
         for n, a, b in zip(names, got[i], want[i]):
             assert torch.equal(a, b), (i, n)
+
+
+def test_threads_sharing_one_stream_match_single_stream(cuda):
+    """Threads on one stream (as every thread that sets no stream shares the
+    null stream): each call enqueues its kernels under the stream's
+    workspace lease, so no call's mean, column sums or split-K reduction
+    reads another call's partials.  Equal sizes on every thread: the shared
+    buffer is never regrown, only contended."""
+    import torch
+    inputs = [_work(torch, cuda, s, 640) for s in range(4)]
+    inputs = [(x, lab, gy, gamma, A[:64].contiguous(), B) for x, lab, gy, gamma, A, B in inputs]
+    want = [[t.clone() for t in _run(torch, inp)] for inp in inputs]
+    torch.cuda.synchronize()
+    shared = torch.cuda.Stream()
+    got = [None] * len(inputs)
+    errors = []
+
+    def worker(i):
+        try:
+            with torch.cuda.stream(shared):
+                outs = [_run(torch, inputs[i]) for _ in range(8)]
+                shared.synchronize()
+                got[i] = [[t.clone() for t in out] for out in outs]
+                shared.synchronize()
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(inputs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    names = ["loss", "grad", "y", "dx", "dgamma", "dbeta", "gemm"]
+    for i in range(len(inputs)):
+        for k, out in enumerate(got[i]):
+            for n, a, b in zip(names, out, want[i]):
+                assert torch.equal(a, b), (i, k, n)
