@@ -15,7 +15,7 @@ import nova_seed as S
 pytestmark = pytest.mark.gpu
 
 
-def _work(torch, dev, seed, rows):
+def _inputs(torch, dev, seed, rows):
     """One thread's inputs: sizes differ per thread, so the workspaces do."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     x = torch.randn(rows, 1024, generator=g).to(dev)
@@ -39,7 +39,7 @@ def _run(torch, inp):
 
 def test_threads_on_own_streams_match_single_stream(cuda):
     import torch
-    inputs = [_work(torch, cuda, s, 512 + 96 * s) for s in range(4)]
+    inputs = [_inputs(torch, cuda, s, 512 + 96 * s) for s in range(4)]
     want = [[t.clone() for t in _run(torch, inp)] for inp in inputs]
     torch.cuda.synchronize()
     got = [None] * len(inputs)
@@ -78,7 +78,7 @@ def test_threads_sharing_one_stream_match_single_stream(cuda):
     reads another call's partials.  Equal sizes on every thread: the shared
     buffer is never regrown, only contended."""
     import torch
-    inputs = [_work(torch, cuda, s, 640) for s in range(4)]
+    inputs = [_inputs(torch, cuda, s, 640) for s in range(4)]
     inputs = [(x, lab, gy, gamma, A[:64].contiguous(), B) for x, lab, gy, gamma, A, B in inputs]
     want = [[t.clone() for t in _run(torch, inp)] for inp in inputs]
     torch.cuda.synchronize()
