@@ -21,6 +21,7 @@
 //   execute -- device buffers for every planned buffer, host->device copies
 //              of the arguments, the launches on the calling thread's stream,
 //              one synchronisation, device->host copies of the results.
+#include <errno.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -160,7 +161,19 @@ bool parse_type(const std::string &s_in, Type &t) {
     const size_t x = body.find('x', pos);
     const std::string tok = body.substr(pos, x == std::string::npos ? std::string::npos : x - pos);
     if (!tok.empty() && isdigit((unsigned char)tok[0]) && x != std::string::npos) {
-      t.shape.push_back(strtoll(tok.c_str(), nullptr, 10));
+      // Every size product below is plain int64 arithmetic: a dimension
+      // past 2^40 (or digits that do not parse whole) and an element count
+      // past 2^50 are refused here, so no byte count can overflow.
+      errno = 0;
+      char *end = nullptr;
+      const long long d = strtoll(tok.c_str(), &end, 10);
+      if (errno != 0 || *end != '\0' || d > (1LL << 40)) return false;
+      int64_t n = d;
+      for (int64_t e : t.shape)
+        if (e != 0 && n > (int64_t(1) << 50) / e) return false;
+        else n *= e;
+      if (n > (int64_t(1) << 50)) return false;
+      t.shape.push_back(d);
       pos = x + 1;
       continue;
     }

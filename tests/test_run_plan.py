@@ -100,6 +100,11 @@ def test_bad_syntax_and_types_are_reported_with_lines():
         }""")
     with pytest.raises(nova_run.NovaRunError, match="unsupported"):
         nova_run.Program("func.func @f(%x: tensor<?x8xf32>) { return }")
+    # sizes whose element or byte counts would overflow 64-bit products
+    for t in ("99999999999999999999x8xf32", "1099511627777x8xf32",
+              "1048576x1048576x1048576xf32", "0x8xf32x"):
+        with pytest.raises(nova_run.NovaRunError, match="unsupported"):
+            nova_run.Program("func.func @f(%x: tensor<" + t + ">) { return }")
 
 
 def test_library_exports_every_declared_symbol():
