@@ -139,6 +139,36 @@ __device__ __forceinline__ u32x2v lds_read_tr(uint32_t addr) {
   return v;
 }
 
+__device__ __forceinline__ u32x2v lds_read_tr_hi(uint32_t addr) {
+  u32x2v v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:2048" : "=v"(v) : "v"(addr));
+  return v;
+}
+// Byte offset, from the stage base, of this lane's read of fragment
+// row_base for k16-step kk (the second transposing read is 2048 bytes on).
+template <bool KC>
+__device__ __forceinline__ uint32_t frag_ofs(int row_base, int kk, int lane) {
+  if constexpr (KC) {
+    const int row = row_base + (lane & 31);
+    return (uint32_t)kc_slot(row, kk * 2 + (lane >> 5)) * 16u;
+  } else {
+    const int g = lane >> 4, p = lane & 15;
+    const int n = row_base + 16 * (g & 1) + 4 * (p & 3);
+    const int kb = kk * 16 + 8 * (g >> 1) + (p >> 2);
+    return (uint32_t)(mn_slot(kb, n >> 3) * 8 + (n & 7)) * 2u;
+  }
+}
+template <bool KC>
+__device__ __forceinline__ u32x4 read_frag_at(uint32_t addr) {
+  if constexpr (KC) {
+    return lds_read_b128(addr);
+  } else {
+    const u32x2v lo = lds_read_tr(addr);
+    const u32x2v hi = lds_read_tr_hi(addr);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
+}
+
 // Fragment of a 32-row block for k16-step kk (issued, not yet landed).
 template <bool KC>
 __device__ __forceinline__ u32x4 read_frag(const u32x4 *stage, int row_base, int kk, int lane) {
